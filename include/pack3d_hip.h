@@ -1,0 +1,190 @@
+/*
+ * pack3d_hip.h -- C ABI of the MI355X (gfx950) PACK3D attention backend.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), launches asynchronously on that stream, allocates no
+ * memory and never synchronises, except where stated.  Each returns 0 on
+ * success or a nonzero P3D_E* code; the message of the last failure on the
+ * calling thread is p3d_last_error().  No exception crosses this boundary.
+ *
+ * The boundary replaces, in amilworks/Pack3D:
+ *   - the CPU geometry construction of build_layout / prepare_geometry /
+ *     TokenLayout.repack (src/pack3d/geometry.py:53-101,189-220,223-266);
+ *   - the staged Triton forward of the core contract
+ *     core(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature)
+ *     (src/pack3d/backends/triton/kernels.py:289-311, autograd.py:40-64),
+ *     with the rotary pre-pass rotate_projections (rotary.py:94-106) fused
+ *     into the attention and pooling loads;
+ *   - the explicit backward (kernels.py:314-356, rotary.py:64-70).
+ */
+#ifndef PACK3D_HIP_H
+#define PACK3D_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define P3D_ABI_VERSION 1
+
+enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
+enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
+
+/* A rank-4 tensor [B, H, N, C] whose channel stride is 1: element (b,h,n,c)
+ * lives at data + b*sb + h*sh + n*sn + c (strides in elements).  Rows must
+ * start on 16-byte boundaries. */
+typedef struct p3d_view {
+    void* data;
+    int64_t sb, sh, sn;
+} p3d_view;
+
+/* Axial rotary embedding, applied on load (rope.py:15-48).  For rotary pair
+ * j (channels 2j, 2j+1) with pairs[j] = {base, stride, axis}, the rotation is
+ * table[base + stride * pos_axis] = (cos, sin).  pos is the token's (z,y,x)
+ * coordinate (coords[n] or, in the grid kernels, the brick coordinate) or,
+ * when packed != 0, (packed row, 0, 0).  A one-entry table {1, 0} with all
+ * strides 0 is the exact identity (pre-rotated inputs). */
+typedef struct p3d_rope {
+    const float* table;     /* float2 entries (cos, sin), built on the host */
+    const int32_t* pairs;   /* [head_dim/2][3] */
+    const int64_t* coords;  /* [N, 3] (z, y, x) or NULL when packed != 0 */
+    int32_t packed;
+    int32_t pad_;
+} p3d_rope;
+
+const char* p3d_last_error(void);
+int p3d_abi_version(void);
+
+/* ---- geometry (replaces geometry.py:223-266, 53-101, 189-220) ---------- */
+
+/* build_layout for a complete grid: packed order, coordinates, raster->packed
+ * map, neighbour table [N, W] in itertools.product offset order, and the
+ * fine blocks [N/V, V] = arange.  morton != 0 selects native_block_morton
+ * (Morton-ranked blocks, Morton-ranked slots); 0 selects raster_block.
+ * Replaces geometry.py:241-260. */
+int p3d_build_layout(const int64_t grid[3], const int64_t block[3], const int64_t radius[3],
+                     int32_t morton, int64_t* order, int64_t* coords,
+                     int32_t* raster_to_packed, int32_t* neighbors, int32_t* blocks,
+                     void* stream);
+
+/* prepare_geometry pass 1 (geometry.py:61-95): copies neighbours and blocks
+ * (int32 or int64 input, is64 flags) to int32, and counts into flags[8]:
+ *   [0] out-of-range neighbours  [1] out-of-range block members
+ *   [2] rows with duplicate edges [3] tokens not covered exactly once
+ *   [4] empty coarse groups       [5] maximum in-degree
+ * degree[n] receives the in-degree of each token.  flags and degree are
+ * cleared by the call.  The caller reads flags back (one small copy). */
+int p3d_geometry_check(const void* neighbors, int32_t nb_is64, int64_t n, int32_t width,
+                       const void* blocks, int32_t blocks_is64, int64_t fine, int32_t slots,
+                       int32_t pool_size, int32_t* neighbors32, int32_t* blocks32,
+                       int32_t* degree, int32_t* cover, int32_t* flags, void* stream);
+
+/* Reverse adjacency (geometry.py:88-99): reverse[j] lists ascending the rows i
+ * whose neighbour row contains j, padded with -1 to rwidth columns.  cursor[n]
+ * is scratch (cleared by the call). */
+int p3d_reverse_adjacency(const int32_t* neighbors, int64_t n, int32_t width, int32_t* cursor,
+                          int32_t* reverse, int32_t rwidth, void* stream);
+
+/* TokenLayout.repack (geometry.py:189-220): new row i = old row perm[i].
+ * inverse[n] (int64 scratch) receives perm^-1.  flags[0] counts entries of perm
+ * that are out of range or repeated (cleared by the call).  raster_map may be
+ * NULL (identity); raster_map_out may be NULL (no grid tag). */
+int p3d_repack(const int64_t* perm, int64_t n, const int32_t* neighbors, int32_t width,
+               const int32_t* blocks, int64_t fine, int32_t slots, const int64_t* order,
+               const int64_t* coords, const int32_t* raster_map, int64_t* inverse,
+               int32_t* neighbors_out, int32_t* blocks_out, int64_t* order_out,
+               int64_t* coords_out, int32_t* raster_map_out, int32_t* flags, void* stream);
+
+/* TokenLayout validation (geometry.py:145-160): flags[0] counts tokens whose
+ * order entry is out of range or repeated or whose coordinate disagrees with
+ * order.  scratch[n] is cleared by the call. */
+int p3d_check_layout(const int64_t grid[3], const int64_t* order, const int64_t* coords,
+                     int32_t* scratch, int32_t* flags, void* stream);
+
+/* ---- forward (replaces kernels.py:289-311 and rotary.py:94-106) -------- */
+
+/* Two-stage summary pooling with the key rotation fused (compression.py:28-44,
+ * kernels.py:12-40).  Outputs, for M summaries padded to Mp = ceil(M/32)*32:
+ *   sk  [B, G, Mp, D]           pooled rotated keys (dtype), pad rows zero
+ *   svt [B, G, Mp/32, D, 32]    pooled values, transposed per 32 summaries */
+typedef struct p3d_pool_args {
+    int32_t batch, kv_heads, tokens, head_dim, dtype;
+    int32_t fine_blocks, slots, pool_size, summaries;
+    float temperature;
+    p3d_view kg, vg;
+    const int32_t* blocks;      /* [F, V] */
+    const float* weight;        /* [D] fp32 */
+    const float* bias;          /* [V] fp32 */
+    p3d_rope rope;
+    void* sk;
+    void* svt;
+} p3d_pool_args;
+int p3d_pool_fwd(const p3d_pool_args* args, void* stream);
+
+/* Fused local + global attention with the fusion epilogue
+ * y = sl * o_L + gate * sg * o_G (reference.py:20-31; kernels.py:43-103).
+ * Two online-softmax states (local over the neighbourhood, global over all
+ * summaries) are kept and combined at the end.
+ *
+ * p3d_attn_fwd_grid: complete-grid layouts (build_layout and its repacks).
+ *   Queries are tiled by 3-D bricks in coordinate space; the local pathway
+ *   reads the radius (<= 2 per axis) stencil from an LDS halo, so the
+ *   neighbour table is not read.  raster_to_packed may be NULL (identity).
+ * p3d_attn_fwd_rows: any validated geometry.  Queries are tiled by packed
+ *   rows; o_local (fp32 [B,H,N,D], from p3d_local_fwd_indexed) supplies the
+ *   local branch. */
+typedef struct p3d_attn_args {
+    int32_t batch, heads, kv_heads, tokens, head_dim, dtype;
+    int32_t summaries;          /* M */
+    int32_t gate_dtype;
+    p3d_view q, kl, vl;         /* q [B,H,N,D]; kl, vl [B,G,N,D] */
+    p3d_view gate;              /* [B,H,N]; only sb, sh, sn are used */
+    const float* local_scale;   /* [D] fp32 */
+    const float* global_scale;  /* [D] fp32 */
+    const void* sk;             /* from p3d_pool_fwd */
+    const void* svt;
+    p3d_rope rope;
+    int32_t grid[3];            /* grid kernel: (Z, Y, X) */
+    int32_t radius[3];          /* grid kernel: per-axis radius, each <= 2 */
+    const int32_t* raster_to_packed;
+    const float* o_local_in;    /* rows kernel: fp32 [B,H,N,D] contiguous */
+    p3d_view y;                 /* output [B,H,N,D], dtype */
+    /* optional saved state for backward (NULL to skip), contiguous: */
+    float* lse_local;           /* [B,H,N] */
+    float* lse_global;          /* [B,H,N] */
+    void* o_local;              /* [B,H,N,D] dtype */
+    void* o_global;             /* [B,H,N,D] dtype */
+} p3d_attn_args;
+int p3d_attn_fwd_grid(const p3d_attn_args* args, void* stream);
+int p3d_attn_fwd_rows(const p3d_attn_args* args, void* stream);
+
+/* Indexed local attention for arbitrary validated graphs (reference.py:23-30,
+ * kernels.py:43-66).  q and kl must already be rotated (rope identity) or are
+ * rotated with args->rope.  Writes fp32 o_local [B,H,N,D] and, if non-NULL,
+ * lse_local [B,H,N].  An all-masked row gives 0 and lse = -inf. */
+int p3d_local_fwd_indexed(const p3d_attn_args* args, const int32_t* neighbors, int32_t width,
+                          float* o_local, void* stream);
+
+/* Standalone rotation (rotary.py:10-45): y = R(pos) x, or R(pos)^T x when
+ * inverse != 0, for x and y [B, H, N, D] views of dtype. */
+int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tokens,
+               int32_t head_dim, int32_t dtype, const p3d_rope* rope, int32_t inverse, void* stream);
+
+/* ---- self-tests (no counterpart in the reference) ---------------------- */
+
+/* One MFMA of the kind the attention kernels issue for dtype (32x32x16 bf16 /
+ * f16, 32x32x2 f32), loading A [32 x K] and B [K x 32] (row-major, dtype) with
+ * the fragment layout the kernels assume and storing D = A B (fp32, row-major
+ * 32 x 32) with the assumed accumulator layout.  Tests compare D with a
+ * matmul to pin that layout on the device. */
+int p3d_selftest_mfma(int32_t dtype, const void* a, const void* b, float* d, void* stream);
+
+/* sizeof of p3d_view, p3d_rope, p3d_pool_args, p3d_attn_args into out[4], so
+ * a binding can check its struct mirrors. */
+int p3d_struct_sizes(int64_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PACK3D_HIP_H */

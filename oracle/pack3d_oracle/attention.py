@@ -79,4 +79,6 @@ class PACK3DAttention(nn.Module):
         out = pack3d_reference(q, kl, vl, kg, vg, self.pool_weight, self.slot_bias, gate,
                                self.local_scale, self.global_scale, layout.geometry,
                                temperature=self.temperature, **core_kwargs)
-        return x + self.to_out(out.transpose(1, 2).reshape(b, n, -1))
+        rows = core_kwargs.get("rows")
+        residual = x if rows is None else x[:, torch.as_tensor(rows, dtype=torch.long)]
+        return residual + self.to_out(out.transpose(1, 2).reshape(b, residual.shape[1], -1))

@@ -1,0 +1,128 @@
+"""ctypes binding of ``libpack3d_hip.so`` (declared in ``include/pack3d_hip.h``).
+
+Loading fails loudly: there is no CPU or PyTorch fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpack3d_hip.so")
+
+c_int32, c_int64, c_float, c_void_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+P3D_F32, P3D_F16, P3D_BF16 = 0, 1, 2
+DTYPES = {torch.float32: P3D_F32, torch.float16: P3D_F16, torch.bfloat16: P3D_BF16}
+
+
+class View(ctypes.Structure):
+    _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
+
+
+class Rope(ctypes.Structure):
+    _fields_ = [("table", c_void_p), ("pairs", c_void_p), ("coords", c_void_p),
+                ("packed", c_int32), ("pad_", c_int32)]
+
+
+class PoolArgs(ctypes.Structure):
+    _fields_ = [("batch", c_int32), ("kv_heads", c_int32), ("tokens", c_int32), ("head_dim", c_int32),
+                ("dtype", c_int32), ("fine_blocks", c_int32), ("slots", c_int32), ("pool_size", c_int32),
+                ("summaries", c_int32), ("temperature", c_float), ("kg", View), ("vg", View),
+                ("blocks", c_void_p), ("weight", c_void_p), ("bias", c_void_p), ("rope", Rope),
+                ("sk", c_void_p), ("svt", c_void_p)]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("batch", c_int32), ("heads", c_int32), ("kv_heads", c_int32), ("tokens", c_int32),
+                ("head_dim", c_int32), ("dtype", c_int32), ("summaries", c_int32), ("gate_dtype", c_int32),
+                ("q", View), ("kl", View), ("vl", View), ("gate", View),
+                ("local_scale", c_void_p), ("global_scale", c_void_p), ("sk", c_void_p), ("svt", c_void_p),
+                ("rope", Rope), ("grid", c_int32 * 3), ("radius", c_int32 * 3),
+                ("raster_to_packed", c_void_p), ("o_local_in", c_void_p), ("y", View),
+                ("lse_local", c_void_p), ("lse_global", c_void_p), ("o_local", c_void_p),
+                ("o_global", c_void_p)]
+
+
+_P = c_void_p
+SIGNATURES = {
+    "p3d_last_error": ([], ctypes.c_char_p),
+    "p3d_abi_version": ([], c_int32),
+    "p3d_build_layout": ([_P, _P, _P, c_int32, _P, _P, _P, _P, _P, _P], c_int32),
+    "p3d_geometry_check": ([_P, c_int32, c_int64, c_int32, _P, c_int32, c_int64, c_int32, c_int32,
+                            _P, _P, _P, _P, _P, _P], c_int32),
+    "p3d_reverse_adjacency": ([_P, c_int64, c_int32, _P, _P, c_int32, _P], c_int32),
+    "p3d_repack": ([_P, c_int64, _P, c_int32, _P, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                    _P, _P], c_int32),
+    "p3d_check_layout": ([_P, _P, _P, _P, _P, _P], c_int32),
+    "p3d_pool_fwd": ([ctypes.POINTER(PoolArgs), _P], c_int32),
+    "p3d_attn_fwd_grid": ([ctypes.POINTER(AttnArgs), _P], c_int32),
+    "p3d_attn_fwd_rows": ([ctypes.POINTER(AttnArgs), _P], c_int32),
+    "p3d_local_fwd_indexed": ([ctypes.POINTER(AttnArgs), _P, c_int32, _P, _P], c_int32),
+    "p3d_selftest_mfma": ([c_int32, _P, _P, _P, _P], c_int32),
+    "p3d_struct_sizes": ([_P], c_int32),
+    "p3d_rotate": ([View, View, c_int32, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(Rope), c_int32, _P],
+                   c_int32),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib():
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(f"pack3d_amd HIP library missing at {LIB_PATH}; "
+                                       "build it with `python -m pack3d_amd.build`")
+                handle = ctypes.CDLL(LIB_PATH)
+                for name, (args, res) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.argtypes = args
+                    fn.restype = res
+                if handle.p3d_abi_version() != 1:
+                    raise RuntimeError("pack3d_amd HIP library ABI mismatch; rebuild it")
+                _lib = handle
+    return _lib
+
+
+def call(name, *args):
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().p3d_last_error().decode()
+        raise RuntimeError(f"{name} failed ({rc}): {msg}")
+
+
+def stream_of(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def i64x3(values):
+    return (c_int64 * 3)(*[int(v) for v in values])
+
+
+def view(t: torch.Tensor) -> View:
+    """A [B, H, N, C] tensor with unit channel stride as a p3d_view."""
+    sb, sh, sn, sc = t.stride()
+    assert sc == 1 or t.shape[3] == 1
+    return View(t.data_ptr(), sb, sh, sn)
+
+
+def view3(t: torch.Tensor) -> View:
+    """A [B, H, N] tensor (the gate) as a p3d_view."""
+    sb, sh, sn = t.stride()
+    return View(t.data_ptr(), sb, sh, sn)
+
+
+def require_device(t: torch.Tensor, what="tensor"):
+    if t.device.type != "cuda":
+        raise ValueError(f"the hip backend requires {what} on a HIP device; no CPU fallback exists")

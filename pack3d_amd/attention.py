@@ -1,0 +1,83 @@
+"""The PACK3D attention layer with the MI355X HIP backend.
+
+Same constructor, parameters (names, shapes, initialisation order) and
+forward as ``PACK3DAttention`` of amilworks/Pack3D (``src/pack3d/attention.py``),
+with ``backend="hip"``: LayerNorm, projections, the gate softmax, ``to_out``
+and the residual stay in PyTorch (hipBLASLt GEMMs); the rotation, pooling,
+local and global attention and their fusion run in ``libpack3d_hip.so``.
+The projections are consumed as strided views, without copies.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+
+from .core import SUPPORTED_HEAD_DIMS, pack3d_hip_rope
+from .geometry import TokenLayout
+from .rope import axial_rope, balanced_pairs, packed_rope
+
+
+class PACK3DAttention(nn.Module):
+    """Local residual plus gated compressed attention and an outer residual (attention.py:10-21)."""
+
+    def __init__(self, dim, *, heads=4, kv_heads=2, head_dim=32, block_volume=8,
+                 backend="hip", position_encoding="axial", temperature=1.0):
+        super().__init__()
+        if any(type(v) is not int or v <= 0 for v in (dim, heads, kv_heads, head_dim, block_volume)):
+            raise ValueError("dimensions must be positive integers")
+        if heads % kv_heads or head_dim not in SUPPORTED_HEAD_DIMS or block_volume > 64:
+            raise ValueError("unsupported grouped-head dimensions or block volume")
+        if backend != "hip":
+            raise ValueError("backend must be explicitly hip (this package has no other backend)")
+        if position_encoding not in ("axial", "packed"):
+            raise ValueError("position_encoding must be axial or packed")
+        if not math.isfinite(temperature) or temperature <= 0:
+            raise ValueError("temperature must be finite and positive")
+        self.dim, self.heads, self.kv_heads, self.head_dim = dim, heads, kv_heads, head_dim
+        self.backend, self.position_encoding = backend, position_encoding
+        self.temperature = float(temperature)
+        # Creation order fixes the RNG stream (attention.py:40-51).
+        self.norm = nn.LayerNorm(dim)
+        self.to_q = nn.Linear(dim, heads * head_dim, bias=False)
+        self.to_kv = nn.Linear(dim, 4 * kv_heads * head_dim, bias=False)
+        self.pool_weight = nn.Parameter(torch.empty(head_dim))
+        nn.init.uniform_(self.pool_weight, -1 / math.sqrt(head_dim), 1 / math.sqrt(head_dim))
+        self.slot_bias = nn.Parameter(torch.empty(block_volume))
+        nn.init.normal_(self.slot_bias, std=0.02)
+        self.gate = nn.Linear(dim, heads * 2)
+        nn.init.zeros_(self.gate.bias)
+        self.local_scale = nn.Parameter(torch.ones(head_dim))
+        self.global_scale = nn.Parameter(torch.full((head_dim,), 0.25))
+        self.to_out = nn.Linear(heads * head_dim, dim, bias=False)
+
+    def core_inputs(self, x, layout: TokenLayout):
+        """Unrotated q, kl, vl, kg, vg (views of the projections), gate, and the rotation."""
+        b, n = x.shape[0], x.shape[1]
+        xn = self.norm(x)
+        q = self.to_q(xn).view(b, n, self.heads, self.head_dim).transpose(1, 2)
+        kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
+                          for t in self.to_kv(xn).view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
+        gate = self.gate(xn).view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
+        if self.position_encoding == "packed":
+            rope = packed_rope(self.head_dim, n, x.device)
+        else:
+            rope = axial_rope(self.head_dim, layout.grid_shape, layout.coords, balanced_pairs(self.head_dim))
+        return q, kl, vl, kg, vg, gate, rope
+
+    def forward(self, x, layout: TokenLayout):
+        layout.check_unmodified()
+        if x.ndim != 3 or x.shape[0] == 0 or tuple(x.shape[1:]) != (layout.geometry.num_tokens, self.dim):
+            raise ValueError("x must be [batch,layout_tokens,dim] with a nonempty batch")
+        if x.device != layout.coords.device:
+            raise ValueError("x and layout are on different devices; move both with .to(device)")
+        if layout.geometry.blocks.shape[1] != len(self.slot_bias):
+            raise ValueError("layout canonical slot count must match block_volume")
+        if self.backend != "hip":
+            raise ValueError("unknown backend; implicit fallback is disabled")
+        b, n = x.shape[0], x.shape[1]
+        q, kl, vl, kg, vg, gate, rope = self.core_inputs(x, layout)
+        out = pack3d_hip_rope(q, kl, vl, kg, vg, self.pool_weight, self.slot_bias, gate, self.local_scale,
+                              self.global_scale, layout.geometry, rope, temperature=self.temperature)
+        return x + self.to_out(out.transpose(1, 2).reshape(b, n, -1))

@@ -1,0 +1,233 @@
+"""The PACK3D core on MI355X: validation, dispatch to the HIP kernels, autograd.
+
+``pack3d_hip`` has the core contract of ``pack3d_reference`` /
+``pack3d_streamed`` of amilworks/Pack3D (``src/pack3d/reference.py:8-9``,
+``src/pack3d/backends/triton/autograd.py:40-64``): rotated q, kl, kg.
+``pack3d_hip_rope`` takes the unrotated projections and fuses the axial
+rotation into the kernels' loads; the layer uses it.
+
+There is no fallback: inputs that the HIP kernels cannot take raise.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .rope import RopeSpec, identity_rope
+
+SUPPORTED_HEAD_DIMS = (16, 32, 48, 64, 128)
+
+
+def _validate_inputs(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature):
+    """The core contract (``_validation.py:4-37``); head_dim 48 is also accepted."""
+    geometry.check_unmodified()
+    if q.ndim != 4 or min(q.shape) < 1:
+        raise ValueError("Q must have shape [batch, query_heads, tokens, head_dim]")
+    b, h, n, d = q.shape
+    if kl.ndim != 4 or kl.shape[0] != b or tuple(kl.shape[2:]) != (n, d):
+        raise ValueError("local K has incompatible dimensions")
+    if not 0 < kl.shape[1] <= h or h % kl.shape[1]:
+        raise ValueError("query heads must be divisible by KV heads")
+    if any(t.shape != kl.shape for t in (vl, kg, vg)):
+        raise ValueError("all branch K/V tensors must have matching shapes")
+    if any(t.dtype != q.dtype for t in (kl, vl, kg, vg)):
+        raise ValueError("Q/K/V must have the same dtype")
+    if d not in SUPPORTED_HEAD_DIMS:
+        raise ValueError("supported head dimensions are 16, 32, 48, 64 and 128")
+    if q.numel() >= 2 ** 31 or b * kl.shape[1] * 32 * geometry.num_summaries * d >= 2 ** 31:
+        raise ValueError("shape exceeds the 32-bit kernel indexing limit")
+    if weight.shape != (d,) or bias.shape != (geometry.blocks.shape[1],):
+        raise ValueError("pool scorer/slot bias shape mismatch")
+    if gate.shape != (b, h, n) or sl.shape != (d,) or sg.shape != (d,):
+        raise ValueError("gate or channelwise branch scale shape mismatch")
+    if n != geometry.num_tokens:
+        raise ValueError("geometry token count does not match Q")
+    every = (q, kl, vl, kg, vg, weight, bias, gate, sl, sg, *geometry.tensors)
+    if any(t.device != q.device for t in every):
+        raise ValueError("all tensors and prepared geometry must be on the same device")
+    if any(not t.is_floating_point() for t in every[:10]):
+        raise ValueError("attention inputs must be floating point")
+    if not math.isfinite(temperature) or temperature <= 0:
+        raise ValueError("temperature must be finite and positive")
+
+
+def _check_hip(q):
+    """No implicit fallback (autograd.py:31-37 of the reference)."""
+    if q.device.type != "cuda" or q.dtype not in _lib.DTYPES:
+        raise ValueError("hip backend requires HIP-device fp32/fp16/bf16 Q/K/V")
+
+
+def _rows_ok(t):
+    """Unit channel stride and 16-byte aligned rows, as the kernels require."""
+    step = 16 // t.element_size()
+    s = t.stride()
+    return s[-1] == 1 and t.data_ptr() % 16 == 0 and all(x % step == 0 for x in s[:-1])
+
+
+def _kernel_view(t):
+    return t if _rows_ok(t) else t.contiguous()
+
+
+def grid_kernel_applies(geometry):
+    """Complete-grid stencils with radius <= 2 per axis take the brick kernel."""
+    grid = geometry._grid
+    return grid is not None and all(r <= 2 for r in grid[1])
+
+
+class ForwardPlan:
+    """Buffers and ctypes argument blocks of one forward; ``run()`` launches it.
+
+    Splitting construction from launch lets callers time or replay the
+    pooling and attention kernels individually.
+    """
+
+    def __init__(self, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature,
+                 rope: RopeSpec, pool_rope: RopeSpec, save_state=False):
+        b, h, n, d = q.shape
+        g = kl.shape[1]
+        dev = q.device
+        dt = _lib.DTYPES[q.dtype]
+        self.device = dev
+        q, kl, vl, kg, vg = (_kernel_view(t) for t in (q, kl, vl, kg, vg))
+        f, slots = geometry.blocks.shape
+        m = geometry.num_summaries
+        mp = -(-m // 32) * 32
+        self.sk = torch.empty(b, g, mp, d, dtype=q.dtype, device=dev)
+        self.svt = torch.empty(b, g, mp // 32, d, 32, dtype=q.dtype, device=dev)
+        self._keep = [q, kl, vl, kg, vg, geometry, rope, pool_rope]
+        w32 = weight.detach().float().contiguous()
+        b32 = bias.detach().float().contiguous()
+        self.pool_args = _lib.PoolArgs(b, g, n, d, dt, f, slots, geometry.pool_size, m, float(temperature),
+                                       _lib.view(kg), _lib.view(vg), geometry.blocks.data_ptr(),
+                                       w32.data_ptr(), b32.data_ptr(), pool_rope.struct(),
+                                       self.sk.data_ptr(), self.svt.data_ptr())
+        self.y = torch.empty(b, n, h, d, dtype=q.dtype, device=dev).transpose(1, 2)
+        sl32, sg32 = sl.detach().float().contiguous(), sg.detach().float().contiguous()
+        if gate.dtype not in _lib.DTYPES:
+            gate = gate.float()
+        self._keep += [w32, b32, sl32, sg32, gate]
+        self.saved = {}
+        if save_state:
+            self.saved = {"lse_local": torch.empty(b, h, n, dtype=torch.float32, device=dev),
+                          "lse_global": torch.empty(b, h, n, dtype=torch.float32, device=dev),
+                          "o_local": torch.empty(b, h, n, d, dtype=q.dtype, device=dev),
+                          "o_global": torch.empty(b, h, n, d, dtype=q.dtype, device=dev)}
+        a = _lib.AttnArgs()
+        a.batch, a.heads, a.kv_heads, a.tokens, a.head_dim, a.dtype = b, h, g, n, d, dt
+        a.summaries, a.gate_dtype = m, _lib.DTYPES[gate.dtype]
+        a.gate = _lib.view3(gate)
+        a.local_scale, a.global_scale = sl32.data_ptr(), sg32.data_ptr()
+        a.sk, a.svt = self.sk.data_ptr(), self.svt.data_ptr()
+        a.y = _lib.view(self.y)
+        a.lse_local = _lib.ptr(self.saved.get("lse_local"))
+        a.lse_global = _lib.ptr(self.saved.get("lse_global"))
+        a.o_local = _lib.ptr(self.saved.get("o_local"))
+        a.o_global = _lib.ptr(self.saved.get("o_global"))
+        a.vl = _lib.view(vl)
+        self.attn_args = a
+        self.grid = grid_kernel_applies(geometry)
+        self.pre = []  # (name, args) launched before the attention kernel
+        if self.grid:
+            shape, radius = geometry._grid
+            a.q, a.kl = _lib.view(q), _lib.view(kl)
+            a.rope = rope.struct()
+            a.grid[:] = list(shape)
+            a.radius[:] = list(radius)
+            a.raster_to_packed = _lib.ptr(geometry._raster_to_packed)
+            self.attn_name = "p3d_attn_fwd_grid"
+        else:
+            # Arbitrary graph: rotate Q and local K once, indexed local branch
+            # on VALU, then the summary branch and the epilogue by packed rows.
+            if not rope.identity:
+                qr = torch.empty(q.shape, dtype=q.dtype, device=dev)
+                klr = torch.empty(kl.shape, dtype=kl.dtype, device=dev)
+                for src, dst, heads in ((q, qr, h), (kl, klr, g)):
+                    self.pre.append(("p3d_rotate", (_lib.view(src), _lib.view(dst), b, heads, n, d, dt,
+                                                    rope.struct(), 0)))
+                q, kl = qr, klr
+                self._keep += [qr, klr]
+            ident = identity_rope(d, dev)
+            a.q, a.kl = _lib.view(q), _lib.view(kl)
+            a.rope = ident.struct()
+            self.o_local = torch.empty(b, h, n, d, dtype=torch.float32, device=dev)
+            self._keep += [ident]
+            self.pre.append(("p3d_local_fwd_indexed", (a, geometry.neighbors.data_ptr(),
+                                                       geometry.neighbors.shape[1], self.o_local.data_ptr())))
+            self.rows_args = _lib.AttnArgs()
+            ctypes_copy(self.rows_args, a)
+            self.rows_args.o_local_in = self.o_local.data_ptr()
+            self.rows_args.lse_local = None
+            self.attn_name = "p3d_attn_fwd_rows"
+
+    def pool(self):
+        _lib.call("p3d_pool_fwd", self.pool_args, _lib.stream_of(self.device))
+
+    def attention(self):
+        stream = _lib.stream_of(self.device)
+        for name, args in self.pre:
+            _lib.call(name, *args, stream)
+        if self.grid:
+            _lib.call(self.attn_name, self.attn_args, stream)
+        else:
+            _lib.call(self.attn_name, self.rows_args, stream)
+            if self.saved:
+                self.saved["o_local"].copy_(self.o_local)
+
+    def run(self):
+        self.pool()
+        self.attention()
+        saved = dict(self.saved)
+        saved.update({"sk": self.sk, "svt": self.svt})
+        return self.y, saved
+
+
+def ctypes_copy(dst, src):
+    import ctypes
+    ctypes.memmove(ctypes.addressof(dst), ctypes.addressof(src), ctypes.sizeof(src))
+
+
+def forward(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature,
+            rope: RopeSpec, pool_rope: RopeSpec, save_state=False):
+    """Launch pooling and attention; returns y [B, H, N, d] (a transposed view of
+    a [B, N, H, d] buffer) and, if ``save_state``, the tensors backward needs."""
+    return ForwardPlan(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope,
+                       save_state).run()
+
+
+class _Pack3DHip(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope):
+        y, _ = forward(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope,
+                       save_state=False)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        raise NotImplementedError("the hip backward is not available yet")
+
+
+def _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope):
+    _validate_inputs(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature)
+    _check_hip(q)
+    inputs = (q, kl, vl, kg, vg, weight, bias, gate, sl, sg)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        return _Pack3DHip.apply(*inputs, geometry, float(temperature), rope, pool_rope)
+    y, _ = forward(*inputs, geometry, float(temperature), rope, pool_rope, save_state=False)
+    return y
+
+
+def pack3d_hip(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, *, temperature=1.0):
+    """PACK3D core on the GPU with rotated q, kl, kg (the contract of reference.py:8-9).
+
+    Returns ``sl * o_L + gate * sg * o_G`` with shape [B, H, N, d] in q.dtype.
+    """
+    ident = identity_rope(q.shape[-1], q.device) if q.device.type == "cuda" else None
+    return _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, ident, ident)
+
+
+def pack3d_hip_rope(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, rope: RopeSpec, *,
+                    temperature=1.0):
+    """PACK3D core with unrotated q, kl, kg: the rotation ``rope`` is applied on load."""
+    return _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, rope)

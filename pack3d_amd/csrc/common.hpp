@@ -1,0 +1,165 @@
+// Shared helpers for the gfx950 PACK3D kernels: status reporting, element
+// conversion, MFMA operand traits and wavefront utilities.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/pack3d_hip.h"
+
+namespace p3d {
+
+// ---------------------------------------------------------------- status
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+#define P3D_REQUIRE(cond, msg)                          \
+    do {                                                \
+        if (!(cond)) return ::p3d::fail(P3D_EINVAL, msg); \
+    } while (0)
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------ elements
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+template <>
+__device__ __forceinline__ __bf16 from_f32<__bf16>(float x) { return (__bf16)x; }
+
+// Load a scalar of runtime dtype (used for the gate, whose dtype may differ).
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+    if (dtype == P3D_F32) return reinterpret_cast<const float*>(p)[i];
+    if (dtype == P3D_F16) return (float)reinterpret_cast<const _Float16*>(p)[i];
+    return (float)reinterpret_cast<const __bf16*>(p)[i];
+}
+
+// Product and difference without contraction, so the rotation rounds
+// exactly as the separate fp32 multiply / subtract of rope.py:44.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+
+// Rotate one channel pair: (x0 c - x1 s, x0 s + x1 c); inverse uses -s.
+__device__ __forceinline__ void rotate_pair(float& x0, float& x1, float c, float s) {
+    float a = sub_rn(mul_rn(x0, c), mul_rn(x1, s));
+    float b = add_rn(mul_rn(x0, s), mul_rn(x1, c));
+    x0 = a;
+    x1 = b;
+}
+
+// ---------------------------------------------------------------- MFMA
+// v_mfma_f32_32x32x{16,16,2}: D[32x32] = A[32xK] B[Kx32] + C.
+// Operand fragments: lane l holds A row (l % 32) / B column (l % 32) and the
+// E contraction elements k = E * (l / 32) + j, j < E.
+// Accumulator: lane l, register r holds D[row][l % 32] with
+//   row = 8 * (r / 4) + 4 * (l / 32) + (r % 4).
+template <typename T>
+struct Mma;
+
+template <>
+struct Mma<__bf16> {
+    static constexpr int E = 8;    // elements per lane per fragment
+    static constexpr int KS = 16;  // contraction length per instruction
+    typedef bf16x8 Frag;
+    __device__ __forceinline__ static f32x16 mfma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mma<_Float16> {
+    static constexpr int E = 8;
+    static constexpr int KS = 16;
+    typedef f16x8 Frag;
+    __device__ __forceinline__ static f32x16 mfma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mma<float> {
+    static constexpr int E = 1;
+    static constexpr int KS = 2;
+    typedef float Frag;
+    __device__ __forceinline__ static f32x16 mfma(Frag a, Frag b, f32x16 c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+};
+
+// Row of the 32x32 accumulator held by register r in lane group g = l / 32.
+__device__ __forceinline__ constexpr int acc_row(int r, int g) { return 8 * (r / 4) + 4 * g + (r % 4); }
+
+// Key order inside a 32-key tile.  When the score tile S^T = K Q^T is used
+// directly as the B operand of O^T = V^T P^T, register r of lane group g
+// contributes contraction index kappa = (r / E) * KS + E * g + (r % E).  Loading
+// K row rho from key kperm(rho) makes kappa the key index, so V can stay in
+// natural key order.
+template <int E, int KS>
+__device__ __forceinline__ constexpr int kperm(int rho) {
+    int g = (rho >> 2) & 1;
+    int r = 4 * (rho >> 3) + (rho & 3);
+    return (r / E) * KS + E * g + (r % E);
+}
+
+// --------------------------------------------------------------- wave
+// Value held by lane l ^ 32.
+__device__ __forceinline__ float swap_half(float x) { return __shfl_xor(x, 32); }
+
+__device__ __forceinline__ float wave_max(float x) {
+    for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+__device__ __forceinline__ int wave_max_i(int x) {
+    for (int o = 32; o >= 1; o >>= 1) x = max(x, __shfl_xor(x, o));
+    return x;
+}
+
+template <typename T>
+struct Piece {
+    static constexpr int N = 16 / sizeof(T);  // elements per 16-byte piece
+};
+
+template <typename T>
+__device__ __forceinline__ void load_piece(const T* src, float* out) {
+    constexpr int N = Piece<T>::N;
+    typedef __attribute__((ext_vector_type(4))) unsigned int u4;
+    u4 raw = *reinterpret_cast<const u4*>(src);
+    const T* v = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = to_f32(v[e]);
+}
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline int dtype_size(int dt) { return dt == P3D_F32 ? 4 : 2; }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Rows of the view start on 16-byte boundaries.
+inline bool view_ok(const p3d_view& v, int esize) {
+    const int64_t step = 16 / esize;
+    return v.data && aligned16(v.data) && v.sb % step == 0 && v.sh % step == 0 && v.sn % step == 0;
+}
+
+}  // namespace p3d

@@ -1,0 +1,47 @@
+// Axial rotary embedding applied on load (rope.py:15-48 of amilworks/Pack3D).
+#pragma once
+
+#include "common.hpp"
+
+namespace p3d {
+
+struct RopeDev {
+    const float2* table;
+    const int32_t* pairs;  // [D/2][3]: base, stride, axis
+    const int64_t* coords;
+    int packed;
+};
+
+inline RopeDev rope_dev(const p3d_rope& r) {
+    return RopeDev{reinterpret_cast<const float2*>(r.table), r.pairs, r.coords, r.packed};
+}
+
+// Position of packed row n along each axis.
+__device__ __forceinline__ void rope_position(const RopeDev& r, int64_t n, int64_t pos[3]) {
+    if (r.packed) {
+        pos[0] = n;
+        pos[1] = 0;
+        pos[2] = 0;
+    } else {
+        pos[0] = r.coords[3 * n + 0];
+        pos[1] = r.coords[3 * n + 1];
+        pos[2] = r.coords[3 * n + 2];
+    }
+}
+
+// (cos, sin) of rotary pair j at position pos.
+__device__ __forceinline__ float2 rope_cs(const RopeDev& r, int j, const int64_t pos[3]) {
+    const int32_t* p = r.pairs + 3 * j;
+    return r.table[p[0] + (int64_t)p[1] * pos[p[2]]];
+}
+
+// Rotate a contiguous run of `count` channels starting at even channel c0.
+__device__ __forceinline__ void rope_apply(const RopeDev& r, const int64_t pos[3], int c0, float* x, int count,
+                                           bool inverse = false) {
+    for (int e = 0; e < count; e += 2) {
+        float2 cs = rope_cs(r, (c0 + e) >> 1, pos);
+        rotate_pair(x[e], x[e + 1], cs.x, inverse ? -cs.y : cs.y);
+    }
+}
+
+}  // namespace p3d

@@ -1,0 +1,343 @@
+"""Geometry objects of the PACK3D operator, built and validated on the GPU.
+
+Mirrors ``src/pack3d/geometry.py`` of amilworks/Pack3D -- same classes,
+arguments, error classes and messages -- but constructs the tables with the
+integer HIP kernels of ``libpack3d_hip.so``:
+
+* ``build_layout``      -> ``p3d_build_layout`` + ``p3d_reverse_adjacency``
+  (geometry.py:223-266)
+* ``prepare_geometry``  -> ``p3d_geometry_check`` + ``p3d_reverse_adjacency``
+  (geometry.py:53-101)
+* ``TokenLayout.repack`` -> ``p3d_repack`` + ``p3d_reverse_adjacency``
+  (geometry.py:189-220)
+
+All tables are bit-exact with the reference construction.  Geometry lives
+on a HIP device; ``.to("cpu")`` copies it out for inspection.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field, replace
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_SEAL = object()
+
+
+def _device(t=None):
+    if t is not None and t.device.type == "cuda":
+        return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("pack3d_amd geometry is built on a HIP device and none is available")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _versions_of(tensors):
+    return tuple(t._version for t in tensors if t is not None)
+
+
+@dataclass(frozen=True)
+class Pack3DGeometry:
+    """Validated neighbour table, reverse adjacency and fine-block membership.
+
+    ``_grid`` is ``(grid_shape, radius)`` when the neighbour table is the
+    complete coordinate stencil of a grid (set by ``build_layout`` and carried
+    through repacks); ``_raster_to_packed`` maps raster index -> packed row
+    (``None`` = identity).  The grid kernels use these instead of the table.
+    """
+
+    neighbors: Tensor
+    reverse_neighbors: Tensor
+    blocks: Tensor
+    pool_size: int
+    num_tokens: int
+    _seal: object = field(default=None, repr=False)
+    _grid: tuple | None = field(default=None, kw_only=True, repr=False)
+    _raster_to_packed: Tensor | None = field(default=None, kw_only=True, repr=False)
+    _versions: tuple = field(default=(), init=False, repr=False)
+
+    def __post_init__(self):
+        if self._seal is not _SEAL:
+            raise ValueError("Use prepare_geometry() to validate indices before launching kernels")
+        object.__setattr__(self, "_versions", _versions_of(self._all()))
+
+    def _all(self):
+        return (self.neighbors, self.reverse_neighbors, self.blocks, self._raster_to_packed)
+
+    @property
+    def tensors(self):
+        return self.neighbors, self.reverse_neighbors, self.blocks
+
+    @property
+    def num_summaries(self):
+        return math.ceil(self.blocks.shape[0] / self.pool_size)
+
+    @property
+    def _radius_one_grid(self):
+        """The reference's radius-one stencil tag (geometry.py:18)."""
+        if self._grid is not None and tuple(self._grid[1]) == (1, 1, 1):
+            return tuple(self._grid[0])
+        return None
+
+    def check_unmodified(self):
+        if _versions_of(self._all()) != self._versions:
+            raise RuntimeError("Geometry changed after validation; prepare it again")
+
+    @torch.inference_mode(False)
+    def to(self, device):
+        self.check_unmodified()
+        m = self._raster_to_packed
+        return Pack3DGeometry(*(t.to(device) for t in self.tensors), self.pool_size, self.num_tokens,
+                              _SEAL, _grid=self._grid, _raster_to_packed=None if m is None else m.to(device))
+
+
+def _flags(t):
+    return [int(v) for v in t.cpu().tolist()]
+
+
+@torch.inference_mode(False)
+def _reverse(nb32: Tensor, rwidth: int) -> Tensor:
+    n, width = nb32.shape
+    device = nb32.device
+    reverse = torch.empty(n, rwidth, dtype=torch.int32, device=device)
+    cursor = torch.empty(n, dtype=torch.int32, device=device)
+    _lib.call("p3d_reverse_adjacency", nb32.data_ptr(), n, width, cursor.data_ptr(), reverse.data_ptr(),
+              rwidth, _lib.stream_of(device))
+    return reverse
+
+
+@torch.inference_mode(False)
+def prepare_geometry(neighbors: Tensor, blocks: Tensor, pool_size: int) -> Pack3DGeometry:
+    """Validate a local graph and fine-block partition on the GPU (geometry.py:53-101).
+
+    -1 marks padding.  Errors match the reference: out-of-range tokens,
+    duplicate local edges, a partition that misses or repeats a token, an
+    entirely empty coarse group, reverse degree above 128.
+    """
+    for name, value in (("neighbors", neighbors), ("blocks", blocks)):
+        if value.ndim != 2 or value.dtype not in (torch.int32, torch.int64):
+            raise ValueError(f"{name} must be a rank-two integer tensor")
+        if min(value.shape) == 0:
+            raise ValueError(f"{name} must be nonempty")
+    if type(pool_size) is not int or not 1 <= pool_size <= 32:
+        raise ValueError("pool_size must be an integer in [1,32]")
+    n, width = neighbors.shape
+    fine, slots = blocks.shape
+    if width > 128 or slots > 64:
+        raise ValueError("at most 128 neighbors and 64 fine-block slots are supported")
+    if max(neighbors.numel(), blocks.numel()) >= 2 ** 31:
+        raise ValueError("geometry exceeds the 32-bit kernel indexing limit")
+    device = _device(neighbors)
+    nb_in = neighbors.detach().to(device).contiguous()
+    bl_in = blocks.detach().to(device).contiguous()
+    nb32 = torch.empty(n, width, dtype=torch.int32, device=device)
+    bl32 = torch.empty(fine, slots, dtype=torch.int32, device=device)
+    degree = torch.empty(n, dtype=torch.int32, device=device)
+    cover = torch.empty(n, dtype=torch.int32, device=device)
+    flags = torch.empty(8, dtype=torch.int32, device=device)
+    _lib.call("p3d_geometry_check", nb_in.data_ptr(), int(nb_in.dtype == torch.int64), n, width,
+              bl_in.data_ptr(), int(bl_in.dtype == torch.int64), fine, slots, pool_size,
+              nb32.data_ptr(), bl32.data_ptr(), degree.data_ptr(), cover.data_ptr(), flags.data_ptr(),
+              _lib.stream_of(device))
+    f = _flags(flags)
+    if f[0]:
+        raise ValueError("neighbors contains an out-of-range token")
+    if f[1]:
+        raise ValueError("blocks contains an out-of-range token")
+    if f[2]:
+        raise ValueError("duplicate local edges are not supported")
+    if f[3]:
+        raise ValueError("fine blocks must partition every token exactly once")
+    if f[4]:
+        raise ValueError("an entirely empty coarse group is unsupported")
+    rwidth = max(1, f[5])
+    if rwidth > 128:
+        raise ValueError("reverse local degree exceeds 128")
+    return Pack3DGeometry(nb32, _reverse(nb32, rwidth), bl32, pool_size, n, _SEAL)
+
+
+def _triple(value, name, *, allow_zero=False):
+    """geometry.py:104-109."""
+    values = (value,) * 3 if type(value) is int else tuple(value)
+    low = 0 if allow_zero else 1
+    if len(values) != 3 or any(type(v) is not int or v < low for v in values):
+        raise ValueError(f"{name} must contain three integers >= {low}")
+    return values
+
+
+def grid_coordinates(shape, device=None) -> Tensor:
+    """Raster-order (z, y, x) int64 coordinates [Z*Y*X, 3] (geometry.py:112-115)."""
+    z, y, x = _triple(shape, "shape")
+    axes = [torch.arange(s, device=device) for s in (z, y, x)]
+    return torch.stack(torch.meshgrid(*axes, indexing="ij"), -1).reshape(-1, 3)
+
+
+@dataclass(frozen=True)
+class TokenLayout:
+    """A complete grid stored in an explicit token order (geometry.py:129-220).
+
+    ``order[i]`` is packed row i's raster index and ``coords[i]`` its (z, y, x)
+    coordinate.  Tensors are immutable; ``repack`` transports the graph.
+    """
+
+    grid_shape: tuple
+    order: Tensor
+    coords: Tensor
+    geometry: Pack3DGeometry
+    _trusted: object = field(default=None, repr=False)
+    _versions: tuple = field(default=(), init=False, repr=False)
+
+    def __post_init__(self):
+        shape = _triple(self.grid_shape, "grid_shape")
+        object.__setattr__(self, "grid_shape", shape)
+        n = math.prod(shape)
+        if self.order.shape != (n,) or self.order.dtype != torch.int64:
+            raise ValueError("order must be an int64 permutation of the grid")
+        if self.coords.shape != (n, 3) or self.coords.dtype != torch.int64:
+            raise ValueError("coords must be int64 [tokens, 3]")
+        if n != self.geometry.num_tokens or any(t.device != self.order.device for t in
+                                                (self.coords, *self.geometry.tensors)):
+            raise ValueError("layout and geometry must agree on token count and device")
+        if self._trusted is not _SEAL:
+            self._validate(shape, n)
+        object.__setattr__(self, "_trusted", None)
+        object.__setattr__(self, "_versions", (self.order._version, self.coords._version))
+
+    @torch.inference_mode(False)
+    def _validate(self, shape, n):
+        if self.order.device.type != "cuda":
+            raise ValueError("pack3d_amd layouts live on a HIP device; use build_layout or .to(device)")
+        order, coords = self.order.contiguous(), self.coords.contiguous()
+        scratch = torch.empty(n, dtype=torch.int32, device=order.device)
+        flags = torch.empty(8, dtype=torch.int32, device=order.device)
+        _lib.call("p3d_check_layout", _lib.i64x3(shape), order.data_ptr(), coords.data_ptr(),
+                  scratch.data_ptr(), flags.data_ptr(), _lib.stream_of(order.device))
+        if _flags(flags)[0]:
+            raise ValueError("order must be a permutation whose coordinates agree with the grid")
+
+    def check_unmodified(self):
+        self.geometry.check_unmodified()
+        if self._versions != (self.order._version, self.coords._version):
+            raise RuntimeError("layout changed in place; construct a new layout")
+
+    @torch.inference_mode(False)
+    def to(self, device):
+        """Move metadata to a device (geometry.py:167-172)."""
+        self.check_unmodified()
+        device = torch.device(device)
+        layout = TokenLayout.__new__(TokenLayout)
+        for name, value in (("grid_shape", self.grid_shape), ("order", self.order.to(device)),
+                            ("coords", self.coords.to(device)), ("geometry", self.geometry.to(device)),
+                            ("_trusted", None)):
+            object.__setattr__(layout, name, value)
+        object.__setattr__(layout, "_versions", (layout.order._version, layout.coords._version))
+        return layout
+
+    def pack(self, grid: Tensor) -> Tensor:
+        """[batch, Z, Y, X, channels] -> [batch, tokens, channels] (geometry.py:174-179)."""
+        self.check_unmodified()
+        if grid.ndim != 5 or tuple(grid.shape[1:4]) != self.grid_shape:
+            raise ValueError("input must match [batch,Z,Y,X,channels]")
+        return grid.flatten(1, 3).index_select(1, self.order.to(grid.device))
+
+    def unpack(self, packed: Tensor) -> Tensor:
+        """Inverse of ``pack`` (geometry.py:181-187)."""
+        self.check_unmodified()
+        if packed.ndim != 3 or packed.shape[1] != self.geometry.num_tokens:
+            raise ValueError("packed input must have shape [batch,tokens,channels]")
+        return packed.index_select(1, self.order.argsort().to(packed.device)).reshape(
+            packed.shape[0], *self.grid_shape, packed.shape[-1])
+
+    @torch.inference_mode(False)
+    def repack(self, permutation) -> "TokenLayout":
+        """New row i is old row permutation[i]; the graph is transported (geometry.py:189-220).
+
+        Fine-block rows, slots and coarse groups keep their identity; only
+        token references are relabelled, on the GPU.
+        """
+        self.check_unmodified()
+        geom = self.geometry
+        n = geom.num_tokens
+        p = torch.as_tensor(permutation)
+        if p.dtype not in (torch.int32, torch.int64) or tuple(p.shape) != (n,):
+            raise ValueError("permutation must be an integer vector with one entry per token")
+        device = self.order.device
+        p = p.to(device=device, dtype=torch.int64).contiguous()
+        width = geom.neighbors.shape[1]
+        fine, slots = geom.blocks.shape
+        inverse = torch.empty(n, dtype=torch.int64, device=device)
+        nb = torch.empty_like(geom.neighbors)
+        blocks = torch.empty_like(geom.blocks)
+        order = torch.empty_like(self.order)
+        coords = torch.empty(n, 3, dtype=torch.int64, device=device)
+        tagged = geom._grid is not None
+        mapping = torch.empty(n, dtype=torch.int32, device=device) if tagged else None
+        flags = torch.empty(8, dtype=torch.int32, device=device)
+        _lib.call("p3d_repack", p.data_ptr(), n, geom.neighbors.data_ptr(), width, geom.blocks.data_ptr(),
+                  fine, slots, self.order.contiguous().data_ptr(), self.coords.contiguous().data_ptr(),
+                  _lib.ptr(geom._raster_to_packed) if tagged else None, inverse.data_ptr(), nb.data_ptr(),
+                  blocks.data_ptr(), order.data_ptr(), coords.data_ptr(), _lib.ptr(mapping), flags.data_ptr(),
+                  _lib.stream_of(device))
+        if _flags(flags)[0]:
+            raise ValueError("permutation must contain every token exactly once")
+        # Relabelling preserves every in-degree, so the reverse width is unchanged.
+        new = Pack3DGeometry(nb, _reverse(nb, geom.reverse_neighbors.shape[1]), blocks, geom.pool_size, n, _SEAL)
+        if tagged:
+            identity = torch.equal(mapping, torch.arange(n, dtype=torch.int32, device=device))
+            new = replace(new, _seal=_SEAL, _grid=geom._grid, _raster_to_packed=None if identity else mapping)
+        return TokenLayout(self.grid_shape, order, coords, new, _SEAL)
+
+
+def _stencil_degree(shape, radius):
+    """Largest number of valid offsets of the stencil on the grid (= max in-degree)."""
+    return math.prod(min(2 * r + 1, s) for s, r in zip(shape, radius))
+
+
+@torch.inference_mode(False)
+def build_layout(grid_shape, block_shape=(2, 2, 2), *, radius=1, pool_size=4,
+                 layout="native_block_morton", device=None) -> TokenLayout:
+    """Build a complete-grid layout on the GPU (geometry.py:223-266).
+
+    Each grid extent must be divisible by its block extent.  Native layout
+    uses Morton-ordered blocks and Morton-ordered canonical slots; raster
+    layout groups consecutive raster tokens by block volume.  Local
+    neighbours include the query and all valid offsets within ``radius``.
+    ``device`` defaults to the current HIP device.
+    """
+    shape = _triple(grid_shape, "grid_shape")
+    block = _triple(block_shape, "block_shape")
+    rad = _triple(radius, "radius", allow_zero=True)
+    if any(g % b for g, b in zip(shape, block)):
+        raise ValueError("build_layout requires an unpadded grid divisible by block_shape")
+    if math.prod(block) > 64 or math.prod(2 * r + 1 for r in rad) > 128:
+        raise ValueError("layout exceeds supported block or neighborhood width")
+    if layout not in ("raster_block", "native_block_morton"):
+        raise ValueError("layout must be raster_block or native_block_morton")
+    if type(pool_size) is not int or not 1 <= pool_size <= 32:
+        raise ValueError("pool_size must be an integer in [1,32]")
+    morton = layout == "native_block_morton"
+    if morton and max(max(g // b - 1, b - 1) for g, b in zip(shape, block)).bit_length() > 20:
+        raise ValueError("Morton coordinates exceed the supported int64 range")
+    n = math.prod(shape)
+    volume = math.prod(block)
+    width = math.prod(2 * r + 1 for r in rad)
+    if n * width >= 2 ** 31:
+        raise ValueError("geometry exceeds the 32-bit kernel indexing limit")
+    dev = torch.device(device) if device is not None else _device()
+    if dev.type != "cuda":
+        raise ValueError("pack3d_amd builds layouts on a HIP device")
+    order = torch.empty(n, dtype=torch.int64, device=dev)
+    coords = torch.empty(n, 3, dtype=torch.int64, device=dev)
+    mapping = torch.empty(n, dtype=torch.int32, device=dev) if morton else None
+    nb = torch.empty(n, width, dtype=torch.int32, device=dev)
+    blocks = torch.empty(n // volume, volume, dtype=torch.int32, device=dev)
+    _lib.call("p3d_build_layout", _lib.i64x3(shape), _lib.i64x3(block), _lib.i64x3(rad), int(morton),
+              order.data_ptr(), coords.data_ptr(), _lib.ptr(mapping), nb.data_ptr(), blocks.data_ptr(),
+              _lib.stream_of(dev))
+    rwidth = max(1, _stencil_degree(shape, rad))
+    geom = Pack3DGeometry(nb, _reverse(nb, rwidth), blocks, pool_size, n, _SEAL,
+                          _grid=(shape, rad), _raster_to_packed=mapping)
+    return TokenLayout(shape, order, coords, geom, _SEAL)

@@ -1,0 +1,167 @@
+"""Forward parity of the HIP path with the oracle (reference.py / attention.py restated).
+
+Bars: fp32 max-abs <= 1e-5 on the core output and the reference's
+assert_close(3e-5) (tests/test_triton.py:91-92); fp16/bf16 max-abs <= 2e-2 on
+unit-scale activations and the reference's relative-L2 bars 5e-3 / 3.5e-2
+(tests/test_triton.py:83).  Repacks must permute outputs bit-exactly.
+"""
+import math
+
+import pytest
+import torch
+
+import oracle.pack3d_oracle as ref
+import pack3d_amd as p3d
+from pack3d_amd.rope import axial_rope as hip_axial, packed_rope
+from tests._cases import make_case, max_abs, random_core_inputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+REL = {torch.float32: 3e-5, torch.float16: 5e-3, torch.bfloat16: 3.5e-2}
+ABS = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def _check(got, exp, dtype, what):
+    r, m = rel_l2(got, exp), max_abs(got, exp)
+    print(f"  {what}: rel_l2={r:.3g} max_abs={m:.3g}", flush=True)
+    assert torch.isfinite(got).all(), what
+    assert r < REL[dtype], (what, r)
+    assert m <= ABS[dtype], (what, m)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(37, 16, 2, 4, 2, 4, 3), (131, 64, 1, 8, 2, 16, 2), (19, 32, 1, 2, 2, 3, 1),
+                                   (21, 128, 1, 2, 1, 4, 4), (67, 48, 1, 4, 4, 8, 1)])
+def test_core_custom_graph(gpu, dtype, shape):
+    print(f"core custom {shape} {dtype}", flush=True)
+    inputs, nb, blocks, pool = make_case(*shape, dtype=dtype)
+    og = ref.prepare_geometry(nb, blocks, pool)
+    hg = p3d.prepare_geometry(nb.to(gpu), blocks.to(gpu), pool)
+    got = p3d.pack3d_hip(*(t.to(gpu) for t in inputs), hg, temperature=0.7)
+    exp = ref.pack3d_reference(*inputs, og, temperature=0.7)
+    _check(got, exp, dtype, "y")
+    if dtype == torch.float32:
+        torch.testing.assert_close(got.cpu(), exp, atol=3e-5, rtol=3e-5)
+
+
+GRIDS = [
+    # shape, block, radius, kind, heads, kv_heads, d
+    ((8, 8, 8), (4, 4, 4), 2, "raster_block", 4, 4, 48),
+    ((8, 8, 8), (4, 4, 4), 2, "native_block_morton", 4, 2, 48),
+    ((6, 10, 12), (2, 5, 3), (1, 2, 1), "native_block_morton", 2, 1, 32),
+    ((5, 7, 9), (5, 7, 1), (0, 1, 2), "raster_block", 2, 2, 64),
+    ((4, 16, 12), (2, 2, 2), 1, "raster_block", 4, 1, 16),
+    ((12, 12, 12), (4, 4, 4), 2, "native_block_morton", 2, 2, 128),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape,block,radius,kind,heads,kv_heads,d", GRIDS)
+def test_core_grid(gpu, dtype, shape, block, radius, kind, heads, kv_heads, d):
+    print(f"core grid {shape} {block} {radius} {kind} h{heads} g{kv_heads} d{d} {dtype}", flush=True)
+    lay_h = p3d.build_layout(shape, block, radius=radius, pool_size=1, layout=kind)
+    lay_r = ref.build_layout(shape, block, radius=radius, pool_size=1, layout=kind)
+    n, vol = math.prod(shape), math.prod(block)
+    inputs = random_core_inputs(2, heads, kv_heads, n, d, vol, dtype, seed=n + d)
+    got = p3d.pack3d_hip(*(t.to(gpu) for t in inputs), lay_h.geometry, temperature=0.9)
+    exp = ref.pack3d_reference(*inputs, lay_r.geometry, temperature=0.9)
+    _check(got, exp, dtype, "y")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["raster_block", "native_block_morton"])
+def test_core_rope_fused(gpu, dtype, kind):
+    print(f"core rope fused {kind} {dtype}", flush=True)
+    shape, d = (8, 12, 16), 48
+    lay_h = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout=kind)
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout=kind)
+    n = math.prod(shape)
+    inputs = random_core_inputs(1, 4, 4, n, d, 64, dtype, seed=7)
+    rope = hip_axial(d, shape, lay_h.coords)
+    got = p3d.pack3d_hip_rope(*(t.to(gpu) for t in inputs), lay_h.geometry, rope)
+    rot = [ref.axial_rope(t, lay_r.coords) if i in (0, 1, 3) else t for i, t in enumerate(inputs)]
+    exp = ref.pack3d_reference(*rot, lay_r.geometry)
+    _check(got, exp, dtype, "y")
+    # The same rotation through the custom-graph path (indexed local + rows).
+    plain = p3d.prepare_geometry(lay_h.geometry.neighbors, lay_h.geometry.blocks, 1)
+    got2 = p3d.pack3d_hip_rope(*(t.to(gpu) for t in inputs), plain, rope)
+    _check(got2, exp, dtype, "y (indexed path)")
+    # Packed-position control.
+    prope = packed_rope(d, n, gpu)
+    got3 = p3d.pack3d_hip_rope(*(t.to(gpu) for t in inputs), lay_h.geometry, prope)
+    seq = torch.arange(n)
+    pc = torch.stack((seq, torch.zeros_like(seq), torch.zeros_like(seq)), -1)
+    rot = [ref.axial_rope(t, pc, pairs=(d // 2, 0, 0)) if i in (0, 1, 3) else t for i, t in enumerate(inputs)]
+    _check(got3, ref.pack3d_reference(*rot, lay_r.geometry), dtype, "y (packed rope)")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_layer_matches_oracle(gpu, dtype):
+    print(f"layer {dtype}", flush=True)
+    torch.manual_seed(0)
+    shape = (16, 16, 16) if dtype == torch.float32 else (8, 16, 16)
+    oracle = ref.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    layer.load_state_dict(oracle.state_dict())
+    layer = layer.to(gpu, dtype)
+    oracle = oracle.to(dtype)
+    lay_h = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    x = torch.randn(1, math.prod(shape), 192, generator=torch.Generator().manual_seed(1)).to(dtype)
+    with torch.no_grad():
+        got = layer(x.to(gpu), lay_h)
+        exp = oracle(x, lay_r)
+    # Compare the attention branch (the residual is added exactly by both).
+    if dtype == torch.float32:
+        torch.testing.assert_close(got.cpu(), exp, atol=2e-5, rtol=2e-5)
+    assert rel_l2(got.float().cpu() - x.float(), exp.float() - x.float()) < REL[dtype] * 2
+
+
+def test_repack_permutes_outputs_exactly(gpu):
+    print("repack equivariance", flush=True)
+    shape, d = (8, 12, 16), 48
+    n = math.prod(shape)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1)
+    gen = torch.Generator().manual_seed(3)
+    blocks_perm = torch.randperm(n // 64, generator=gen)
+    slot_perm = torch.stack([torch.randperm(64, generator=gen) for _ in range(n // 64)])
+    p = (blocks_perm[:, None] * 64 + slot_perm).reshape(-1)
+    other = lay.repack(p)
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        inputs = [t.to(gpu) for t in random_core_inputs(1, 4, 4, n, d, 64, dtype, seed=11)]
+        moved = [t[:, :, p.to(gpu)] if i in (0, 1, 2, 3, 4, 7) else t for i, t in enumerate(inputs)]
+        rope_a = hip_axial(d, shape, lay.coords)
+        rope_b = hip_axial(d, shape, other.coords)
+        y = p3d.pack3d_hip_rope(*inputs, lay.geometry, rope_a)
+        yp = p3d.pack3d_hip_rope(*moved, other.geometry, rope_b)
+        assert torch.equal(yp, y[:, :, p.to(gpu)]), dtype
+
+
+def test_full_size_headline_sampled(gpu):
+    """c2: 64^3 bf16, dim 192, 4 heads, d 48, radius 2, 4^3 blocks: sampled rows vs the oracle."""
+    print("full size c2 sampled", flush=True)
+    torch.manual_seed(0)
+    shape = (64, 64, 64)
+    n = math.prod(shape)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    for lin in (layer.to_q, layer.to_kv, layer.to_out):
+        torch.nn.init.xavier_uniform_(lin.weight)
+    with torch.no_grad():
+        layer.pool_weight.zero_()
+        layer.slot_bias.zero_()
+    layer = layer.to(gpu, torch.bfloat16)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1)).to(gpu, torch.bfloat16)
+    with torch.no_grad():
+        q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, lay)
+        y = p3d.pack3d_hip_rope(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate,
+                                layer.local_scale, layer.global_scale, lay.geometry, rope)
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(2))[:1024]
+    rows = torch.cat((rows, torch.tensor([0, n - 1, 63, 64 * 64 - 1])))
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    cpu = [t.cpu() for t in (q, kl, vl, kg, vg)]
+    rot = [ref.axial_rope(t, lay_r.coords) if i in (0, 1, 3) else t for i, t in enumerate(cpu)]
+    params = [t.detach().cpu() for t in (layer.pool_weight, layer.slot_bias)]
+    exp = ref.pack3d_reference(*rot, *params, gate.cpu(), layer.local_scale.detach().cpu(),
+                               layer.global_scale.detach().cpu(), lay_r.geometry, rows=rows, chunk=512)
+    _check(y[:, :, rows.to(gpu)], exp, torch.bfloat16, "c2 sampled y")

@@ -1,0 +1,125 @@
+"""CPU checks of the C-ABI boundary and the host logic (no GPU compute)."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pack3d_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(p3d_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from pack3d_amd import _lib
+    names = _declared()
+    assert len(names) >= 14
+    handle = ctypes.CDLL(_lib.LIB_PATH)
+    for name in names:
+        assert hasattr(handle, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures must cover exactly the header"
+
+
+def test_struct_mirrors_match_c_sizes():
+    from pack3d_amd import _lib
+    out = (ctypes.c_int64 * 4)()
+    assert _lib.lib().p3d_struct_sizes(out) == 0
+    assert list(out) == [ctypes.sizeof(_lib.View), ctypes.sizeof(_lib.Rope), ctypes.sizeof(_lib.PoolArgs),
+                         ctypes.sizeof(_lib.AttnArgs)]
+    assert _lib.lib().p3d_abi_version() == 1
+
+
+def test_entry_points_reject_bad_arguments_before_launch():
+    from pack3d_amd import _lib
+    grid = _lib.i64x3((4, 4, 4))
+    bad_block = _lib.i64x3((3, 4, 4))
+    rad = _lib.i64x3((1, 1, 1))
+    rc = _lib.lib().p3d_build_layout(grid, bad_block, rad, 0, None, None, None, None, None, None)
+    assert rc == 1 and b"divisible" in _lib.lib().p3d_last_error()
+    with pytest.raises(RuntimeError, match="null args"):
+        _lib.call("p3d_pool_fwd", None, None)
+    args = _lib.AttnArgs()
+    with pytest.raises(RuntimeError, match="dtype|counts"):
+        args.dtype = 7
+        _lib.call("p3d_attn_fwd_grid", args, None)
+
+
+def test_import_without_gpu_and_no_oracle_import():
+    code = ("import sys, pack3d_amd; assert 'oracle' not in sys.modules; "
+            "assert not any(m.startswith('oracle') for m in sys.modules)")
+    subprocess.run([sys.executable, "-c", code], check=True, cwd=ROOT)
+
+
+def test_product_sources_never_reference_the_oracle():
+    pkg = os.path.join(ROOT, "pack3d_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in text, f
+
+
+@pytest.mark.parametrize("kwargs", [{"grid_shape": (3, 4, 4)}, {"radius": -1}, {"block_shape": (0, 2, 2)},
+                                    {"layout": "unknown"}, {"pool_size": True}, {"radius": 3},
+                                    {"block_shape": (8, 8, 8), "grid_shape": (8, 8, 8)}])
+def test_build_layout_rejects_before_launch(kwargs):
+    from pack3d_amd import build_layout
+    args = {"grid_shape": (4, 4, 4), **kwargs}
+    with pytest.raises(ValueError):
+        build_layout(**args)
+
+
+def test_prepare_geometry_shape_checks():
+    from pack3d_amd import prepare_geometry
+    with pytest.raises(ValueError, match="rank-two"):
+        prepare_geometry(torch.zeros(3, dtype=torch.int32), torch.zeros(1, 3, dtype=torch.int32), 1)
+    with pytest.raises(ValueError, match="nonempty"):
+        prepare_geometry(torch.zeros(0, 2, dtype=torch.int32), torch.zeros(1, 3, dtype=torch.int32), 1)
+    with pytest.raises(ValueError, match="pool_size"):
+        prepare_geometry(torch.zeros(3, 1, dtype=torch.int32), torch.zeros(1, 3, dtype=torch.int32), 0)
+    with pytest.raises(ValueError, match="at most 128"):
+        prepare_geometry(torch.zeros(3, 129, dtype=torch.int32), torch.zeros(1, 3, dtype=torch.int32), 1)
+
+
+@pytest.mark.parametrize("kwargs", [{"heads": 3}, {"temperature": 0}, {"backend": "auto"},
+                                    {"backend": "reference"}, {"position_encoding": "none"},
+                                    {"head_dim": 40}])
+def test_layer_rejects_unsupported(kwargs):
+    from pack3d_amd import PACK3DAttention
+    with pytest.raises(ValueError):
+        PACK3DAttention(32, **kwargs)
+
+
+def test_layer_parameters_match_reference_names_and_init_stream():
+    from oracle.pack3d_oracle import PACK3DAttention as Oracle
+    from pack3d_amd import PACK3DAttention
+    torch.manual_seed(5)
+    a = PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    torch.manual_seed(5)
+    b = Oracle(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    sa, sb = a.state_dict(), b.state_dict()
+    assert list(sa) == list(sb)
+    for k in sa:
+        assert torch.equal(sa[k], sb[k]), k
+
+
+def test_core_requires_hip_device_no_fallback():
+    from oracle.pack3d_oracle import prepare_geometry as oracle_prepare
+    from pack3d_amd import pack3d_hip
+    from pack3d_amd.geometry import Pack3DGeometry, _SEAL
+    from tests._cases import make_case
+    inputs, nb, blocks, pool = make_case(d=48)
+    og = oracle_prepare(nb, blocks, pool)
+    geom = Pack3DGeometry(og.neighbors, og.reverse_neighbors, og.blocks, pool, og.num_tokens, _SEAL)
+    with pytest.raises(ValueError, match="hip backend requires"):
+        pack3d_hip(*inputs, geom)
+    inputs[0] = inputs[0][..., :40]
+    with pytest.raises(ValueError):
+        pack3d_hip(*inputs, geom)

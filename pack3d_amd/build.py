@@ -18,17 +18,22 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libpack3d_hip.so")
 ARCH = "gfx950"
 
-# Packed fp32 VALU ops are disabled for device code: hipcc forms them from
-# ordinary float code, and this pool has seen wrong results from some forms.
-FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# Packed fp32 VALU ops are disabled for device code: the compiler forms them
+# from ordinary float code, and this pool has seen wrong results from some
+# forms.  The kernels never produce or consume NaN (masked scores are -inf),
+# so NaN-quieting of fmax operands is switched off (non-IEEE mode), which
+# removes a canonicalising v_max per operand from the softmax.
+FLAGS = ["-x", "hip", "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-fno-honor-nans", "-mno-amdgpu-ieee", "-Wno-nan-infinity-disabled"]
 
 
 def _hipcc():
-    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-    if not os.path.exists(path):
-        raise RuntimeError("hipcc not found; the pack3d_amd HIP library cannot be built")
-    return path
+    """The ROCm clang driver (hipcc's own wrapper rejects -mno-amdgpu-ieee)."""
+    for path in ("/opt/rocm/lib/llvm/bin/clang++", shutil.which("amdclang++")):
+        if path and os.path.exists(path):
+            return path
+    raise RuntimeError("ROCm clang++ not found; the pack3d_amd HIP library cannot be built")
 
 
 def _compile(src, hipcc, verbose):
@@ -55,7 +60,8 @@ def build(verbose: bool = False) -> str:
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(lambda s: _compile(s, hipcc, verbose), sources))
     tmp = LIB + ".tmp"
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [hipcc, "--hip-link", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+           "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")

@@ -112,47 +112,103 @@ struct Soft {
     }
 };
 
-// Score tile: S^T[32 keys x 32 queries].  krow points at this lane's key row
-// (already offset by E * g).
-template <typename C, typename T>
-__device__ __forceinline__ f32x16 score_tile(const T* krow, const typename C::Frag* qf) {
-    f32x16 s;
+// Score tile S^T[32 keys x 32 queries] = init + K Q^T from preloaded key
+// fragments; init carries the mask (0 or -inf per score) when there is one.
+template <typename C>
+__device__ __forceinline__ f32x16 score_tile(const typename C::Frag* kf, const typename C::Frag* qf,
+                                             f32x16 init) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-    for (int t = 0; t < C::NT; ++t) s = C::M::mfma(frag_load16<T>(krow + t * C::KS), qf[t], s);
-    return s;
+    for (int t = 0; t < C::NT; ++t) init = C::M::mfma(kf[t], qf[t], init);
+    return init;
 }
 
-// Online-softmax update with the tile's (masked) raw scores s, then
-// acc += V^T P^T.  vload(mb, ks) returns the V fragment of block mb, k-step ks.
-template <typename C, typename VLoad>
-__device__ __forceinline__ void soft_update(Soft<C::MB>& st, const f32x16& s, float scale_log2, VLoad vload) {
-    float tmax = s[0];
+template <typename C>
+__device__ __forceinline__ f32x16 score_tile(const typename C::Frag* kf, const typename C::Frag* qf) {
+    f32x16 zero;
 #pragma unroll
-    for (int r = 1; r < 16; ++r) tmax = fmaxf(tmax, s[r]);
-    tmax = fmaxf(tmax, swap_half(tmax));
-    const float m_new = fmaxf(st.m, tmax * scale_log2);
-    const float base = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(st.m - base);
-    float p[16];
+    for (int r = 0; r < 16; ++r) zero[r] = 0.f;
+    return score_tile<C>(kf, qf, zero);
+}
+
+// Rows [D, 32 * MB) of a transposed V buffer: the ones row (channel D, when
+// the O^T padding holds the denominator) and zero rows.  Written once; the
+// staging only ever writes rows < D, so the fragments need no selects.
+template <typename C>
+__device__ __forceinline__ void init_v_padding(typename C::T_* V, int vstride, int cols) {
+    typedef typename C::T_ T;
+    const int rows = 32 * C::MB - C::D;
+    for (int i = threadIdx.x; i < rows * cols; i += blockDim.x) {
+        const int r = i / cols, c = i - r * cols;
+        V[(C::D + r) * vstride + c] = from_f32<T>((C::ONES && r == 0) ? 1.f : 0.f);
+    }
+}
+
+// Value fragments of block mb / k-step ks for a tile whose key 0 sits at
+// column `col` of a transposed V buffer with 32 * MB rows.
+template <typename C, bool ALIGNED16>
+__device__ __forceinline__ void load_vfrags(const typename C::T_* Vs, int vstride, int col, int lane,
+                                            typename C::Frag* vf) {
+    typedef typename C::T_ T;
+    const int g = lane >> 5, qi = lane & 31;
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int ks = 0; ks < C::KSTEPS; ++ks) {
+            const T* p = Vs + (32 * mb + qi) * vstride + col + ks * C::KS + C::E * g;
+            vf[mb * C::KSTEPS + ks] = ALIGNED16 ? frag_load16<T>(p) : frag_load8<T>(p);
+        }
+}
+
+// Key fragments of one tile; krow points at this lane's key row (offset by E * g).
+template <typename C>
+__device__ __forceinline__ void load_kfrags(const typename C::T_* krow, typename C::Frag* kf) {
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t) kf[t] = frag_load16<typename C::T_>(krow + t * C::KS);
+}
+
+// The running max only moves when a tile's max exceeds it by more than this
+// many log2 units, so the accumulator is rarely rescaled; probabilities are
+// then bounded by 2^kLazy, far inside the fp32 / bf16 / fp16 range.
+constexpr float kLazy = 8.f;
+
+// Online-softmax step for one tile of raw (masked) scores s: updates the
+// running max (lazily), rescales the accumulator when it moved, and returns
+// the unnormalised probabilities p = 2^(s * scale_log2 - m).
+template <typename C>
+__device__ __forceinline__ void soft_probs(Soft<C::MB>& st, const f32x16& s, float scale_log2, float* p) {
+    float tmax = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) tmax = fmaxf(tmax, fmaxf(s[r], s[r + 1]));
+    tmax = fmaxf(tmax, swap_half(tmax)) * scale_log2;
+    const bool move = tmax > st.m + kLazy || (st.m == -INFINITY && tmax > -INFINITY);
+    if (__builtin_amdgcn_ballot_w64(move)) {
+        const float m_new = move ? tmax : st.m;
+        const float alpha = move ? __builtin_amdgcn_exp2f(st.m - m_new) : 1.f;
+#pragma unroll
+        for (int b = 0; b < C::MB; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) st.acc[b][r] *= alpha;
+        if constexpr (!C::ONES) st.l *= alpha;
+        st.m = m_new;
+    }
+    const float base = st.m == -INFINITY ? 0.f : st.m;
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         p[r] = __builtin_amdgcn_exp2f(fmaf(s[r], scale_log2, -base));
         if constexpr (!C::ONES) psum += p[r];
     }
-    st.m = m_new;
-    if constexpr (!C::ONES) st.l = fmaf(st.l, alpha, psum);
-#pragma unroll
-    for (int b = 0; b < C::MB; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) st.acc[b][r] *= alpha;
+    if constexpr (!C::ONES) st.l += psum;
+}
+
+// acc += V^T P^T with preloaded value fragments vf[mb * KSTEPS + ks].
+template <typename C>
+__device__ __forceinline__ void soft_accumulate(Soft<C::MB>& st, const float* p, const typename C::Frag* vf) {
 #pragma unroll
     for (int ks = 0; ks < C::KSTEPS; ++ks) {
         const typename C::Frag pf = frag_from_p<typename C::T_>(p, ks);
 #pragma unroll
-        for (int b = 0; b < C::MB; ++b) st.acc[b] = C::M::mfma(vload(b, ks), pf, st.acc[b]);
+        for (int b = 0; b < C::MB; ++b) st.acc[b] = C::M::mfma(vf[b * C::KSTEPS + ks], pf, st.acc[b]);
     }
 }
 

@@ -23,6 +23,8 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kPlane = 12;                 // plane side for radius <= 2 and an 8 x 8 brick face
 constexpr int kPlaneKeys = kPlane * kPlane;
+// LDS bytes of the rotation window: (cos, sin) for 64 pairs x 12 positions, then 64 axis ids.
+constexpr int kRopeWindowBytes = 64 * kPlane * 8 + 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -48,10 +50,11 @@ struct AttnDev {
 template <typename T>
 __device__ __forceinline__ const T* tp(const char* p) { return reinterpret_cast<const T*>(p); }
 
-// Load and rotate this lane's query channels into score-MFMA B fragments.
-template <typename C>
-__device__ __forceinline__ void load_q(const typename C::T_* row, bool valid, const RopeDev& rope,
-                                       const int64_t pos[3], int g, typename C::Frag* qf) {
+// Load and rotate this lane's query channels into score-MFMA B fragments;
+// rot(j) returns (cos, sin) of rotary pair j for this query.
+template <typename C, typename Rot>
+__device__ __forceinline__ void load_q(const typename C::T_* row, bool valid, Rot rot, int g,
+                                       typename C::Frag* qf) {
     typedef typename C::T_ T;
 #pragma unroll
     for (int t = 0; t < C::NT; ++t) {
@@ -60,7 +63,11 @@ __device__ __forceinline__ void load_q(const typename C::T_* row, bool valid, co
             const int c0 = t * C::KS + 8 * g;
             if (valid) {
                 load_piece<T>(row + c0, x);
-                rope_apply(rope, pos, c0, x, 8);
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const float2 cs = rot((c0 + e) >> 1);
+                    rotate_pair(x[e], x[e + 1], cs.x, cs.y);
+                }
             } else {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) x[j] = 0.f;
@@ -73,39 +80,71 @@ __device__ __forceinline__ void load_q(const typename C::T_* row, bool valid, co
             if (valid) {
                 x[0] = to_f32(row[c0]);
                 x[1] = to_f32(row[c0 + 1]);
-                rope_apply(rope, pos, c0, x, 2);
+                const float2 cs = rot(c0 >> 1);
+                rotate_pair(x[0], x[1], cs.x, cs.y);
             }
             qf[t] = x[g];
         }
     }
 }
 
-// Stage summaries [base, base + 64) of one KV head: K rows (natural order)
-// and V transposed, in LDS.  The padded summary rows of sk / svt are zero.
+// ---------------------------------------------------------------- summaries
+// Summary stages of 64 keys, double-buffered in LDS through registers:
+// K rows (natural order, row stride KSTR) and V transposed (row stride VGS).
 template <typename C>
-__device__ __forceinline__ void stage_summaries(const AttnDev& a, int64_t bg, int base, typename C::T_* Ks,
-                                                typename C::T_* Vs, int vstride) {
+struct StageRegs {
     typedef typename C::T_ T;
-    constexpr int EP = Piece<T>::N;
-    constexpr int D = C::D;
-    const int rows = min(64, a.Mp - base);
-    const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * D;
-    for (int p = threadIdx.x; p < rows * (D / EP); p += 64 * kWaves) {
-        const int r = p / (D / EP), c = (p - r * (D / EP)) * EP;
-        *reinterpret_cast<uint4*>(Ks + r * C::KSTR + c) = *reinterpret_cast<const uint4*>(sk + r * D + c);
-    }
-    const T* svt = tp<T>(a.svt) + ((int64_t)bg * (a.Mp / 32) + base / 32) * D * 32;
-    const int tiles = rows / 32;
-    for (int p = threadIdx.x; p < tiles * D * (32 / EP); p += 64 * kWaves) {
-        const int tt = p / (D * (32 / EP));
-        const int rem = p - tt * D * (32 / EP);
-        const int ch = rem / (32 / EP), k = (rem - ch * (32 / EP)) * EP;
-        *reinterpret_cast<uint4*>(Vs + ch * vstride + 32 * tt + k) =
-            *reinterpret_cast<const uint4*>(svt + ((int64_t)tt * D + ch) * 32 + k);
-    }
-}
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int KPIECES = 64 * (C::D / EP);
+    static constexpr int VPIECES = C::D * (64 / EP);
+    static constexpr int KI = (KPIECES + 64 * kWaves - 1) / (64 * kWaves);
+    static constexpr int VI = (VPIECES + 64 * kWaves - 1) / (64 * kWaves);
+    uint4 k[KI], v[VI];
 
-// One global stage on this wave's two column blocks.
+    __device__ __forceinline__ void load(const AttnDev& a, int64_t bg, int base) {
+#pragma unroll
+        for (int i = 0; i < KI; ++i) k[i] = uint4{0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < VI; ++i) v[i] = uint4{0, 0, 0, 0};
+        const int rows = min(64, a.Mp - base);  // 32 or 64; pad rows of sk / svt are zero
+        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
+        const T* svt = tp<T>(a.svt) + ((int64_t)bg * (a.Mp / 32) + base / 32) * C::D * 32;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
+            if (p < KPIECES && r < rows) k[i] = *reinterpret_cast<const uint4*>(sk + r * C::D + c);
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            const int tt = p / (C::D * (32 / EP));
+            const int rem = p - tt * C::D * (32 / EP);
+            const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
+            if (p < VPIECES && 32 * tt < rows)
+                v[i] = *reinterpret_cast<const uint4*>(svt + ((int64_t)tt * C::D + ch) * 32 + kk);
+        }
+    }
+
+    __device__ __forceinline__ void store(T* Ks, T* Vs, int vstride, int rows) const {
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
+            if (p < KPIECES && r < rows) *reinterpret_cast<uint4*>(Ks + r * C::KSTR + c) = k[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            const int tt = p / (C::D * (32 / EP));
+            const int rem = p - tt * C::D * (32 / EP);
+            const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
+            if (p < VPIECES && 32 * tt < rows) *reinterpret_cast<uint4*>(Vs + ch * vstride + 32 * tt + kk) = v[i];
+        }
+    }
+};
+
+// One summary stage (two 32-key tiles) on this wave's two column blocks.
 template <typename C>
 __device__ __forceinline__ void global_stage(const AttnDev& a, int base, const typename C::T_* Ks,
                                              const typename C::T_* Vs, int vstride,
@@ -116,90 +155,271 @@ __device__ __forceinline__ void global_stage(const AttnDev& a, int base, const t
     for (int tt = 0; tt < 2; ++tt) {
         const int first = base + 32 * tt;
         if (first >= a.M) break;
-        const T* krow = Ks + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g;
-        auto vload = [&](int mb, int ks) -> typename C::Frag {
-            const int ch = 32 * mb + qi;
-            const T* p = Vs + min(ch, C::D - 1) * vstride + 32 * tt + ks * C::KS + C::E * g;
-            typename C::Frag f = frag_load16<T>(p);
-            if (32 * mb + 32 > C::D && ch >= C::D) f = frag_fill<T>((C::ONES && ch == C::D) ? 1.f : 0.f);
-            return f;
-        };
+        typename C::Frag kf[C::NT], vf[C::MB * C::KSTEPS];
+        load_kfrags<C>(Ks + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, kf);
+        load_vfrags<C, true>(Vs, vstride, 32 * tt, lane, vf);
+        f32x16 s[2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            f32x16 s = score_tile<C>(krow, qf[nb]);
-            if (first + 32 > a.M) {
+        for (int nb = 0; nb < 2; ++nb) s[nb] = score_tile<C>(kf, qf[nb]);
+        if (first + 32 > a.M) {
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r)
-                    if (first + kperm<C::E, C::KS>(acc_row(r, g)) >= a.M) s[r] = -INFINITY;
-            }
-            soft_update<C>(st[nb], s, a.scale_log2, vload);
+                    if (first + kperm<C::E, C::KS>(acc_row(r, g)) >= a.M) s[nb][r] = -INFINITY;
         }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            float p[16];
+            soft_probs<C>(st[nb], s[nb], a.scale_log2, p);
+            soft_accumulate<C>(st[nb], p, vf);
+        }
+    }
+}
+
+// The whole summary pathway for this workgroup: all M summaries streamed
+// through a double-buffered LDS region at `lds`.
+template <typename C>
+__device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typename C::T_* lds,
+                                            const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
+    typedef typename C::T_ T;
+    constexpr int EP = Piece<T>::N;
+    constexpr int VGS = 64 + EP;
+    constexpr int STAGE = 64 * C::KSTR + 32 * C::MB * VGS;
+    init_v_padding<C>(lds + 64 * C::KSTR, VGS, 64);
+    init_v_padding<C>(lds + STAGE + 64 * C::KSTR, VGS, 64);
+    StageRegs<C> regs;
+    regs.load(a, bg, 0);
+    regs.store(lds, lds + 64 * C::KSTR, VGS, min(64, a.Mp));
+    __syncthreads();
+    int buf = 0;
+    for (int base = 0; base < a.M; base += 64) {
+        const int next = base + 64;
+        if (next < a.M) regs.load(a, bg, next);
+        T* cur = lds + buf * STAGE;
+        global_stage<C>(a, base, cur, cur + 64 * C::KSTR, VGS, qf, st, lane);
+        if (next < a.M) {
+            T* nxt = lds + (buf ^ 1) * STAGE;
+            regs.store(nxt, nxt + 64 * C::KSTR, VGS, min(64, a.Mp - next));
+        }
+        __syncthreads();
+        buf ^= 1;
     }
 }
 
 // Channels of accumulator register r in lane group g of block mb.
 __device__ __forceinline__ int acc_channel(int mb, int r, int g) { return 32 * mb + acc_row(r, g); }
 
-template <typename C>
-__device__ __forceinline__ void store_quad(typename C::T_* dst, const float* v) {
-    typedef typename C::T_ T;
+template <typename T>
+__device__ __forceinline__ void store_quad(T* dst, const float* v) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dst[i] = from_f32<T>(v[i]);
 }
 
+template <typename T>
+__device__ __forceinline__ void load_quad(const T* src, float* v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = to_f32(src[i]);
+}
+
+// Finish the local state: y <- sl * o_L (storage type; the epilogue adds the
+// global branch), optionally saving o_L and its log-sum-exp.
 template <typename C>
-__device__ __forceinline__ void epilogue(const AttnDev& a, int b, int h, int64_t row, bool valid, int g,
-                                         const Soft<C::MB>& sg_state, const float (*ylocal)[16]) {
+__device__ __forceinline__ void finish_local(const AttnDev& a, int b, int h, int64_t row, bool valid, int g,
+                                             const Soft<C::MB>& st) {
     typedef typename C::T_ T;
-    const float den = soft_denominator<C>(sg_state, g);
+    const float den = soft_denominator<C>(st, g);
+    if (!valid) return;
+    const float inv = den > 0.f ? 1.f / den : 0.f;  // an all-masked row gives 0
+    const int64_t bh = (int64_t)b * a.H + h;
+    T* y = reinterpret_cast<T*>(a.y) + b * a.ysb + h * a.ysh + row * a.ysn;
+    T* ol = a.o_l ? reinterpret_cast<T*>(a.o_l) + (bh * a.N + row) * C::D : nullptr;
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (32 * mb + 8 * q >= C::D) continue;
+            const int ch0 = acc_channel(mb, 4 * q, g);
+            float o[4], yl[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o[i] = st.acc[mb][4 * q + i] * inv;
+                yl[i] = a.sl[ch0 + i] * o[i];
+            }
+            store_quad<T>(y + ch0, yl);
+            if (ol) store_quad<T>(ol + ch0, o);
+        }
+    if (a.lse_l) a.lse_l[bh * a.N + row] = den > 0.f ? st.m * kLn2 + __logf(den) : -INFINITY;
+}
+
+// y = sl * o_L + gate * sg * o_G.  The local term comes from y itself (grid
+// kernel, written by finish_local) or from o_local_in (rows kernel).
+template <typename C, bool LOCAL_FROM_Y>
+__device__ __forceinline__ void epilogue(const AttnDev& a, int b, int h, int64_t row, bool valid, int g,
+                                         const Soft<C::MB>& st) {
+    typedef typename C::T_ T;
+    const float den = soft_denominator<C>(st, g);
     if (!valid) return;
     const float inv = 1.f / den;
     const int64_t bh = (int64_t)b * a.H + h;
     const float gate = load_any(a.gate, b * a.gsb + h * a.gsh + row * a.gsn, a.gate_dtype);
     T* y = reinterpret_cast<T*>(a.y) + b * a.ysb + h * a.ysh + row * a.ysn;
     T* og = a.o_g ? reinterpret_cast<T*>(a.o_g) + (bh * a.N + row) * C::D : nullptr;
+    const float* oli = LOCAL_FROM_Y ? nullptr : a.o_local_in + (bh * a.N + row) * C::D;
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if (32 * mb + 8 * q >= C::D) continue;
             const int ch0 = acc_channel(mb, 4 * q, g);
-            float out[4], o[4];
+            float yl[4], out[4], o[4];
+            if constexpr (LOCAL_FROM_Y) {
+                load_quad<T>(y + ch0, yl);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                o[i] = sg_state.acc[mb][4 * q + i] * inv;
-                out[i] = ylocal[mb][4 * q + i] + gate * a.sg[ch0 + i] * o[i];
+                for (int i = 0; i < 4; ++i) yl[i] = a.sl[ch0 + i] * oli[ch0 + i];
             }
-            store_quad<C>(y + ch0, out);
-            if (og) store_quad<C>(og + ch0, o);
-        }
-    if (a.lse_g) a.lse_g[bh * a.N + row] = sg_state.m * kLn2 + __logf(den);
-}
-
-// Finish the local state: ylocal = sl * o_L; optionally save o_L and its LSE.
-template <typename C>
-__device__ __forceinline__ void finish_local(const AttnDev& a, int b, int h, int64_t row, bool valid, int g,
-                                             const Soft<C::MB>& st, float (*ylocal)[16]) {
-    typedef typename C::T_ T;
-    const float den = soft_denominator<C>(st, g);
-    const float inv = den > 0.f ? 1.f / den : 0.f;  // an all-masked row gives 0
-    const int64_t bh = (int64_t)b * a.H + h;
-    T* ol = (a.o_l && valid) ? reinterpret_cast<T*>(a.o_l) + (bh * a.N + row) * C::D : nullptr;
-#pragma unroll
-    for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            if (32 * mb + 8 * q >= C::D) continue;
-            const int ch0 = acc_channel(mb, 4 * q, g);
-            float o[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 o[i] = st.acc[mb][4 * q + i] * inv;
-                ylocal[mb][4 * q + i] = a.sl[ch0 + i] * o[i];
+                out[i] = yl[i] + gate * a.sg[ch0 + i] * o[i];
             }
-            if (ol) store_quad<C>(ol + ch0, o);
+            store_quad<T>(y + ch0, out);
+            if (og) store_quad<T>(og + ch0, o);
         }
-    if (a.lse_l && valid) a.lse_l[bh * a.N + row] = den > 0.f ? st.m * kLn2 + __logf(den) : -INFINITY;
+    if (a.lse_g) a.lse_g[bh * a.N + row] = st.m * kLn2 + __logf(den);
+}
+
+// ------------------------------------------------------------------- grid
+// Rotations of the workgroup's coordinate window, staged once in LDS: for
+// rotary pair j, entry j * kPlane + w holds (cos, sin) at coordinate
+// origin[axis(j)] + w of the pair's axis, w < kPlane; axis(j) is kept too.
+// The window origin is (Z0 - rz, Y0 - ry, X0 - rx), covering every query and
+// halo key of the brick.  Packed positions (row indices) do not fit a window
+// and use the global table.
+struct RopeWindow {
+    float2* cs;
+    int* axis;
+    __device__ __forceinline__ float2 at(int j, int wz, int wy, int wx) const {
+        const int ax = axis[j];
+        return cs[j * kPlane + (ax == 0 ? wz : (ax == 1 ? wy : wx))];
+    }
+};
+
+__device__ __forceinline__ void build_rope_window(const AttnDev& a, int D, int oz, int oy, int ox, RopeWindow w) {
+    const int pairs = D / 2;
+    for (int i = threadIdx.x; i < pairs * kPlane; i += blockDim.x) {
+        const int j = i / kPlane, k = i - j * kPlane;
+        const int32_t* d = a.rope.pairs + 3 * j;
+        const int ax = d[2];
+        const int origin = ax == 0 ? oz : (ax == 1 ? oy : ox);
+        const int extent = ax == 0 ? a.Z : (ax == 1 ? a.Y : a.X);
+        const int c = origin + k;
+        w.cs[i] = (c >= 0 && c < extent) ? a.rope.table[d[0] + (int64_t)d[1] * c] : float2{1.f, 0.f};
+        if (k == 0) w.axis[j] = ax;
+    }
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs.  Give each XCD a
+// contiguous run of bricks (raster brick order) so that the bricks an XCD
+// runs together are neighbours and share halo rows in its L2.
+__device__ __forceinline__ int xcd_brick(int id, int bricks) {
+    const int q = bricks / 8, r = bricks % 8;
+    const int xcd = id % 8, slot = id / 8;
+    return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
+
+// Local-pathway plane staging.  A task is one channel piece of 4 x-adjacent
+// keys of a plane row, handled as two halves of 2 keys whose loads are issued
+// before they are consumed; K is rotated on the way and V is written
+// transposed with one 2-key store per channel.
+template <typename C>
+struct PlaneStager {
+    typedef typename C::T_ T;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int PPR = C::D / EP;                       // pieces per key row
+    static constexpr int TASKS = kPlane * (kPlane / 4) * PPR;   // 4-key groups x pieces
+    static constexpr int ITERS = (TASKS + 64 * kWaves - 1) / (64 * kWaves);
+    typedef __attribute__((ext_vector_type(2))) T T2;
+
+    __device__ __forceinline__ void stage(const AttnDev& a, const T* KL, const T* VL, int hz, int gz, int Y0,
+                                          int X0, const RopeWindow& win, T* Kp, T* Vp, int vps) const {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+            const int task = threadIdx.x + it * 64 * kWaves;
+            if (task >= TASKS) break;
+            const int piece = task % PPR, grp = task / PPR;
+            const int ky = grp / (kPlane / 4), kx0 = 4 * (grp % (kPlane / 4));
+            const int gy = Y0 - a.ry + ky;
+            const bool row_in = gz >= 0 && gz < a.Z && gy >= 0 && gy < a.Y && ky < 8 + 2 * a.ry;
+            // Two halves of 2 keys: loads of a half are issued before it is consumed.
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint4 kraw[2], vraw[2];
+                float2 cs[2][EP / 2];
+                bool in[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int kx = kx0 + 2 * half + i, gx = X0 - a.rx + kx;
+                    in[i] = row_in && gx >= 0 && gx < a.X && kx < 8 + 2 * a.rx;
+                    kraw[i] = vraw[i] = uint4{0, 0, 0, 0};
+                    if (in[i]) {
+                        const int64_t raster = ((int64_t)gz * a.Y + gy) * a.X + gx;
+                        const int64_t row = a.map ? (int64_t)a.map[raster] : raster;
+                        kraw[i] = *reinterpret_cast<const uint4*>(KL + row * a.ksn + piece * EP);
+                        vraw[i] = *reinterpret_cast<const uint4*>(VL + row * a.vsn + piece * EP);
+                        if (a.rope.packed) {
+                            const int64_t pos[3] = {row, 0, 0};
+#pragma unroll
+                            for (int e = 0; e < EP / 2; ++e) cs[i][e] = rope_cs(a.rope, piece * EP / 2 + e, pos);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < EP / 2; ++e) cs[i][e] = win.at(piece * EP / 2 + e, hz, ky, kx);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const T* kv = reinterpret_cast<const T*>(&kraw[i]);
+                    T kt[EP];
+#pragma unroll
+                    for (int e = 0; e < EP; e += 2) {
+                        float x0 = to_f32(kv[e]), x1 = to_f32(kv[e + 1]);
+                        if (in[i]) rotate_pair(x0, x1, cs[i][e / 2].x, cs[i][e / 2].y);
+                        kt[e] = from_f32<T>(x0);
+                        kt[e + 1] = from_f32<T>(x1);
+                    }
+                    *reinterpret_cast<uint4*>(Kp + (ky * kPlane + kx0 + 2 * half + i) * C::KSTR + piece * EP) =
+                        *reinterpret_cast<const uint4*>(kt);
+                }
+#pragma unroll
+                for (int e = 0; e < EP; ++e) {
+                    T2 col;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) col[i] = reinterpret_cast<const T*>(&vraw[i])[e];
+                    *reinterpret_cast<T2*>(Vp + (piece * EP + e) * vps + ky * kPlane + kx0 + 2 * half) = col;
+                }
+            }
+        }
+    }
+};
+
+// 16-bit mask of the valid keys of chunk c among this lane's 16 scores:
+// the (2ry+1) x (2rx+1) stencil in y and x around query (qy, qx) of the wave
+// footprint, clipped to the grid.  The z condition is applied per plane.
+template <typename C>
+__device__ __forceinline__ uint32_t stencil_mask(const AttnDev& a, int c, int g, int qy, int qx, int Yw, int Xw) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int kr = kperm<C::E, C::KS>(acc_row(r, g));
+        const int ky = 4 * c + kr / 8, kx = kr % 8;  // within the wave footprint
+        const int gy = Yw - a.ry + ky, gx = Xw - a.rx + kx;
+        const bool ok = (unsigned)(ky - qy) <= (unsigned)(2 * a.ry) && (unsigned)(kx - qx) <= (unsigned)(2 * a.rx) &&
+                        (unsigned)gy < (unsigned)a.Y && (unsigned)gx < (unsigned)a.X;
+        m |= (ok ? 1u : 0u) << r;
+    }
+    return m;
 }
 
 template <typename T, int D>
@@ -207,22 +427,23 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     typedef Cfg<T, D> C;
     constexpr int EP = Piece<T>::N;
     constexpr int VPS = kPlaneKeys + EP;  // plane V row stride (elements)
-    constexpr int VGS = 64 + EP;          // summary V row stride (elements)
     extern __shared__ __align__(16) unsigned char smem[];
-    T* Kp = reinterpret_cast<T*>(smem);
+    RopeWindow win{reinterpret_cast<float2*>(smem), reinterpret_cast<int*>(smem + kRopeWindowBytes - 256)};
+    T* Kp = reinterpret_cast<T*>(smem + kRopeWindowBytes);
     T* Vp = Kp + kPlaneKeys * C::KSTR;
-    T* Ks = reinterpret_cast<T*>(smem);  // global stages reuse the plane buffer
-    T* Vs = Ks + 64 * C::KSTR;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, qi = lane & 31;
     const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.G);
     const int64_t bg = (int64_t)b * a.G + kvh;
-    const int brick = blockIdx.x;
+    const int brick = xcd_brick(blockIdx.x, gridDim.x);
     const int Z0 = 4 * (brick / (a.bricks_y * a.bricks_x));
     const int Y0 = 8 * ((brick / a.bricks_x) % a.bricks_y);
     const int X0 = 8 * (brick % a.bricks_x);
     const int wy = wave >> 1, wx = wave & 1;
     const int qy = (qi >> 2) & 3, qx = qi & 3;  // within the wave footprint
+
+    if (!a.rope.packed) build_rope_window(a, D, Z0 - a.rz, Y0 - a.ry, X0 - a.rx, win);
+    __syncthreads();
 
     // ---- queries
     typename C::Frag qf[2][C::NT];
@@ -230,119 +451,92 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     bool qok[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        const int gz = Z0 + 2 * nb + (qi >> 4), gy = Y0 + 4 * wy + qy, gx = X0 + 4 * wx + qx;
+        const int qz = 2 * nb + (qi >> 4);
+        const int gz = Z0 + qz, gy = Y0 + 4 * wy + qy, gx = X0 + 4 * wx + qx;
         qok[nb] = gz < a.Z && gy < a.Y && gx < a.X;
         const int64_t raster = ((int64_t)gz * a.Y + gy) * a.X + gx;
         qrow[nb] = qok[nb] ? (a.map ? (int64_t)a.map[raster] : raster) : 0;
-        int64_t pos[3] = {gz, gy, gx};
-        if (a.rope.packed) pos[0] = qrow[nb], pos[1] = 0, pos[2] = 0;
         const T* row = tp<T>(a.q) + b * a.qsb + h * a.qsh + qrow[nb] * a.qsn;
-        load_q<C>(row, qok[nb], a.rope, pos, g, qf[nb]);
+        if (a.rope.packed) {
+            const int64_t pos[3] = {qrow[nb], 0, 0};
+            load_q<C>(row, qok[nb], [&](int j) { return rope_cs(a.rope, j, pos); }, g, qf[nb]);
+        } else {
+            const int wz = qz + a.rz, wy_ = 4 * wy + qy + a.ry, wx_ = 4 * wx + qx + a.rx;
+            load_q<C>(row, qok[nb], [&](int j) { return win.at(j, wz, wy_, wx_); }, g, qf[nb]);
+        }
     }
 
     Soft<C::MB> st[2];
     st[0].reset();
     st[1].reset();
 
-    // ---- local pathway
+    // ---- local pathway: halo planes z = Z0 - rz .. Z0 + 3 + rz
     const T* KL = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
     const T* VL = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
+    const uint32_t kmask[2] = {stencil_mask<C>(a, 0, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx),
+                               stencil_mask<C>(a, 1, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx)};
+    init_v_padding<C>(Vp, VPS, kPlaneKeys);
+    const PlaneStager<C> stager;
     const int planes = 4 + 2 * a.rz;
     for (int hz = 0; hz < planes; ++hz) {
-        __syncthreads();
         const int gz = Z0 - a.rz + hz;
-        // Stage the 12 x 12 plane: K rotated, V transposed; keys outside the
-        // grid or the footprint are zero (they are masked below).
-        for (int p = tid; p < kPlaneKeys * (D / EP); p += 64 * kWaves) {
-            const int key = p / (D / EP), c0 = (p - key * (D / EP)) * EP;
-            const int ky = key / kPlane, kx = key - ky * kPlane;
-            const int gy = Y0 - a.ry + ky, gx = X0 - a.rx + kx;
-            const bool in = gz >= 0 && gz < a.Z && gy >= 0 && gy < a.Y && gx >= 0 && gx < a.X &&
-                            ky < 8 + 2 * a.ry && kx < 8 + 2 * a.rx;
-            float kv[EP], vv[EP];
-            if (in) {
-                const int64_t raster = ((int64_t)gz * a.Y + gy) * a.X + gx;
-                const int64_t row = a.map ? (int64_t)a.map[raster] : raster;
-                load_piece<T>(KL + row * a.ksn + c0, kv);
-                load_piece<T>(VL + row * a.vsn + c0, vv);
-                int64_t pos[3] = {gz, gy, gx};
-                if (a.rope.packed) pos[0] = row, pos[1] = 0, pos[2] = 0;
-                rope_apply(a.rope, pos, c0, kv, EP);
-            } else {
-#pragma unroll
-                for (int e = 0; e < EP; ++e) kv[e] = vv[e] = 0.f;
-            }
-            T kt[EP];
-#pragma unroll
-            for (int e = 0; e < EP; ++e) {
-                kt[e] = from_f32<T>(kv[e]);
-                Vp[(c0 + e) * VPS + key] = from_f32<T>(vv[e]);
-            }
-            *reinterpret_cast<uint4*>(Kp + key * C::KSTR + c0) = *reinterpret_cast<const uint4*>(kt);
-        }
+        if (hz) __syncthreads();
+        stager.stage(a, KL, VL, hz, gz, Y0, X0, win, Kp, Vp, VPS);
         __syncthreads();
+        if ((unsigned)gz >= (unsigned)a.Z) continue;  // plane outside the grid: nothing to attend
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const int qz = 2 * nb + (qi >> 4);
-            if (hz < 2 * nb || hz > 2 * nb + 1 + 2 * a.rz) continue;  // plane out of reach
-            const bool zok = hz - qz >= 0 && hz - qz <= 2 * a.rz;
+        for (int c = 0; c < 2; ++c) {
+            if (4 * c >= 4 + 2 * a.ry) continue;
+            const int kap = kperm<C::E, C::KS>(qi);
+            typename C::Frag kf[C::NT], vf[C::MB * C::KSTEPS];
+            load_kfrags<C>(Kp + ((4 * wy + 4 * c + kap / 8) * kPlane + 4 * wx + kap % 8) * C::KSTR + C::E * g, kf);
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                if (4 * c >= 4 + 2 * a.ry) continue;
-                const int kap = kperm<C::E, C::KS>(qi);
-                const T* krow = Kp + ((4 * wy + 4 * c + kap / 8) * kPlane + 4 * wx + kap % 8) * C::KSTR + C::E * g;
-                f32x16 s = score_tile<C>(krow, qf[nb]);
+            for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int kr = kperm<C::E, C::KS>(acc_row(r, g));
-                    const int ky = 4 * c + kr / 8, kx = kr % 8;  // within the wave footprint
-                    const int dy = ky - qy, dx = kx - qx;
-                    const int gy = Y0 + 4 * wy - a.ry + ky, gx = X0 + 4 * wx - a.rx + kx;
-                    const bool ok = zok && (unsigned)dy <= (unsigned)(2 * a.ry) &&
-                                    (unsigned)dx <= (unsigned)(2 * a.rx) && (unsigned)gy < (unsigned)a.Y &&
-                                    (unsigned)gx < (unsigned)a.X && (unsigned)gz < (unsigned)a.Z;
-                    if (!ok) s[r] = -INFINITY;
+                for (int ks = 0; ks < C::KSTEPS; ++ks) {
+                    const int k0 = ks * C::KS + C::E * g;  // chunk key (4c + k0/8, k0 % 8) of the footprint
+                    vf[mb * C::KSTEPS + ks] = frag_load8<T>(Vp + (32 * mb + qi) * VPS +
+                                                            (4 * wy + 4 * c + k0 / 8) * kPlane + 4 * wx + k0 % 8);
                 }
-                auto vload = [&](int mb, int ks) -> typename C::Frag {
-                    const int ch = 32 * mb + qi;
-                    const int k0 = ks * C::KS + C::E * g;
-                    const T* p = Vp + min(ch, D - 1) * VPS + (4 * wy + 4 * c + k0 / 8) * kPlane + 4 * wx + k0 % 8;
-                    typename C::Frag f = frag_load8<T>(p);
-                    if (32 * mb + 32 > D && ch >= D) f = frag_fill<T>((C::ONES && ch == D) ? 1.f : 0.f);
-                    return f;
-                };
-                soft_update<C>(st[nb], s, a.scale_log2, vload);
+            f32x16 bias;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) bias[r] = (kmask[c] >> r) & 1 ? 0.f : -INFINITY;
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                // Column block nb holds query planes 2nb and 2nb + 1.
+                if (hz < 2 * nb || hz > 2 * nb + 1 + 2 * a.rz) continue;
+                f32x16 s = score_tile<C>(kf, qf[nb], bias);
+                if (hz == 2 * nb || hz == 2 * nb + 1 + 2 * a.rz) {  // only one of the two query planes reaches
+                    const int qz = 2 * nb + (qi >> 4);
+                    if ((unsigned)(hz - qz) > (unsigned)(2 * a.rz)) {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) s[r] = -INFINITY;
+                    }
+                }
+                float p[16];
+                soft_probs<C>(st[nb], s, a.scale_log2, p);
+                soft_accumulate<C>(st[nb], p, vf);
             }
         }
     }
-
-    float ylocal[2][C::MB][16];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        finish_local<C>(a, b, h, qrow[nb], qok[nb], g, st[nb], ylocal[nb]);
+        finish_local<C>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
         st[nb].reset();
     }
+    __syncthreads();  // the summary stages reuse the plane buffer
 
-    // ---- global pathway
-    for (int base = 0; base < a.M; base += 64) {
-        __syncthreads();
-        stage_summaries<C>(a, bg, base, Ks, Vs, VGS);
-        __syncthreads();
-        global_stage<C>(a, base, Ks, Vs, VGS, qf, st, lane);
-    }
-
+    // ---- global pathway (the rotation window is no longer needed)
+    global_pass<C>(a, bg, Kp, qf, st, lane);
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) epilogue<C>(a, b, h, qrow[nb], qok[nb], g, st[nb], ylocal[nb]);
+    for (int nb = 0; nb < 2; ++nb) epilogue<C, true>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
 }
 
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_rows(AttnDev a) {
     typedef Cfg<T, D> C;
-    constexpr int EP = Piece<T>::N;
-    constexpr int VGS = 64 + EP;
     extern __shared__ __align__(16) unsigned char smem[];
-    T* Ks = reinterpret_cast<T*>(smem);
-    T* Vs = Ks + 64 * C::KSTR;
+    T* lds = reinterpret_cast<T*>(smem);
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, qi = lane & 31;
     const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.G);
@@ -351,7 +545,6 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_rows(AttnDev a) {
     typename C::Frag qf[2][C::NT];
     int64_t qrow[2];
     bool qok[2];
-    float ylocal[2][C::MB][16];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         const int64_t row = (int64_t)blockIdx.x * 64 * kWaves + 64 * wave + 32 * nb + qi;
@@ -359,30 +552,15 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_rows(AttnDev a) {
         qrow[nb] = qok[nb] ? row : 0;
         int64_t pos[3];
         rope_position(a.rope, qrow[nb], pos);
-        load_q<C>(tp<T>(a.q) + b * a.qsb + h * a.qsh + qrow[nb] * a.qsn, qok[nb], a.rope, pos, g, qf[nb]);
-        const float* ol = a.o_local_in + (((int64_t)b * a.H + h) * a.N + qrow[nb]) * D;
-#pragma unroll
-        for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (32 * mb + 8 * q >= D) continue;
-                const int ch0 = acc_channel(mb, 4 * q, g);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ylocal[nb][mb][4 * q + i] = qok[nb] ? a.sl[ch0 + i] * ol[ch0 + i] : 0.f;
-            }
+        load_q<C>(tp<T>(a.q) + b * a.qsb + h * a.qsh + qrow[nb] * a.qsn, qok[nb],
+                  [&](int j) { return rope_cs(a.rope, j, pos); }, g, qf[nb]);
     }
-
     Soft<C::MB> st[2];
     st[0].reset();
     st[1].reset();
-    for (int base = 0; base < a.M; base += 64) {
-        __syncthreads();
-        stage_summaries<C>(a, bg, base, Ks, Vs, VGS);
-        __syncthreads();
-        global_stage<C>(a, base, Ks, Vs, VGS, qf, st, lane);
-    }
+    global_pass<C>(a, bg, lds, qf, st, lane);
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) epilogue<C>(a, b, h, qrow[nb], qok[nb], g, st[nb], ylocal[nb]);
+    for (int nb = 0; nb < 2; ++nb) epilogue<C, false>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
 }
 
 // Indexed local attention on VALU: one wave per (batch, head, query row);
@@ -472,38 +650,38 @@ int fill_dev(const p3d_attn_args& x, AttnDev& d) {
     return P3D_OK;
 }
 
-template <int D>
-size_t lds_grid(int es) {
-    const int ep = 16 / es;
-    const size_t plane = (size_t)kPlaneKeys * (D + ep) + (size_t)D * (kPlaneKeys + ep);
-    const size_t stage = (size_t)64 * (D + ep) + (size_t)D * (64 + ep);
-    return (plane > stage ? plane : stage) * es;
+template <typename T, int D>
+size_t lds_grid() {
+    typedef Cfg<T, D> C;
+    constexpr int ep = Piece<T>::N;
+    const size_t plane = (size_t)kPlaneKeys * C::KSTR + (size_t)32 * C::MB * (kPlaneKeys + ep);
+    const size_t stages = 2 * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep));
+    return kRopeWindowBytes + (plane > stages ? plane : stages) * sizeof(T);
 }
 
-template <int D>
-size_t lds_rows(int es) {
-    const int ep = 16 / es;
-    return ((size_t)64 * (D + ep) + (size_t)D * (64 + ep)) * es;
+template <typename T, int D>
+size_t lds_rows() {
+    typedef Cfg<T, D> C;
+    constexpr int ep = Piece<T>::N;
+    return 2 * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(T);
 }
 
 template <int D>
 int launch_grid(const AttnDev& d, int dtype, dim3 grid, hipStream_t s) {
-    const size_t smem = lds_grid<D>(dtype_size(dtype));
     switch (dtype) {
-        case P3D_F32: k_attn_grid<float, D><<<grid, 64 * kWaves, smem, s>>>(d); break;
-        case P3D_F16: k_attn_grid<_Float16, D><<<grid, 64 * kWaves, smem, s>>>(d); break;
-        default: k_attn_grid<__bf16, D><<<grid, 64 * kWaves, smem, s>>>(d); break;
+        case P3D_F32: k_attn_grid<float, D><<<grid, 64 * kWaves, lds_grid<float, D>(), s>>>(d); break;
+        case P3D_F16: k_attn_grid<_Float16, D><<<grid, 64 * kWaves, lds_grid<_Float16, D>(), s>>>(d); break;
+        default: k_attn_grid<__bf16, D><<<grid, 64 * kWaves, lds_grid<__bf16, D>(), s>>>(d); break;
     }
     return check_launch("p3d_attn_fwd_grid");
 }
 
 template <int D>
 int launch_rows(const AttnDev& d, int dtype, dim3 grid, hipStream_t s) {
-    const size_t smem = lds_rows<D>(dtype_size(dtype));
     switch (dtype) {
-        case P3D_F32: k_attn_rows<float, D><<<grid, 64 * kWaves, smem, s>>>(d); break;
-        case P3D_F16: k_attn_rows<_Float16, D><<<grid, 64 * kWaves, smem, s>>>(d); break;
-        default: k_attn_rows<__bf16, D><<<grid, 64 * kWaves, smem, s>>>(d); break;
+        case P3D_F32: k_attn_rows<float, D><<<grid, 64 * kWaves, lds_rows<float, D>(), s>>>(d); break;
+        case P3D_F16: k_attn_rows<_Float16, D><<<grid, 64 * kWaves, lds_rows<_Float16, D>(), s>>>(d); break;
+        default: k_attn_rows<__bf16, D><<<grid, 64 * kWaves, lds_rows<__bf16, D>(), s>>>(d); break;
     }
     return check_launch("p3d_attn_fwd_rows");
 }

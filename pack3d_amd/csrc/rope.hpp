@@ -29,10 +29,15 @@ __device__ __forceinline__ void rope_position(const RopeDev& r, int64_t n, int64
     }
 }
 
+// Coordinate along `axis` (selects, not an indexed array, so it stays in registers).
+__device__ __forceinline__ int64_t pick_axis(const int64_t pos[3], int axis) {
+    return axis == 0 ? pos[0] : (axis == 1 ? pos[1] : pos[2]);
+}
+
 // (cos, sin) of rotary pair j at position pos.
 __device__ __forceinline__ float2 rope_cs(const RopeDev& r, int j, const int64_t pos[3]) {
     const int32_t* p = r.pairs + 3 * j;
-    return r.table[p[0] + (int64_t)p[1] * pos[p[2]]];
+    return r.table[p[0] + (int64_t)p[1] * pick_axis(pos, p[2])];
 }
 
 // Rotate a contiguous run of `count` channels starting at even channel c0.

@@ -106,12 +106,19 @@ int p3d_check_layout(const int64_t grid[3], const int64_t* order, const int64_t*
 
 /* Two-stage summary pooling with the key rotation fused (compression.py:28-44,
  * kernels.py:12-40).  Outputs, for M summaries padded to Mp = ceil(M/32)*32:
- *   sk  [B, G, Mp, D]           pooled rotated keys (dtype), pad rows zero
- *   svt [B, G, Mp/32, D, 32]    pooled values, transposed per 32 summaries */
+ *   sk  [B, G, Mp, D]           pooled rotated keys times key_scale (dtype),
+ *                               pad rows zero
+ *   svt [B, G, Mp/32, D, 32]    pooled values, transposed per 32 summaries
+ *   sk_norm_max [B, G, 64] (fp32)  maxima of the 2-norms of the stored
+ *                               (rounded) sk rows, summary m reducing into
+ *                               slot m % 64; their max bounds every summary
+ *                               score of a query (Cauchy-Schwarz) */
 typedef struct p3d_pool_args {
     int32_t batch, kv_heads, tokens, head_dim, dtype;
     int32_t fine_blocks, slots, pool_size, summaries;
     float temperature;
+    float key_scale;            /* sk is stored multiplied by this (the attention
+                                   kernels pass log2(e)/sqrt(d)) */
     p3d_view kg, vg;
     const int32_t* blocks;      /* [F, V] */
     const float* weight;        /* [D] fp32 */
@@ -119,6 +126,7 @@ typedef struct p3d_pool_args {
     p3d_rope rope;
     void* sk;
     void* svt;
+    float* sk_norm_max;
 } p3d_pool_args;
 int p3d_pool_fwd(const p3d_pool_args* args, void* stream);
 
@@ -144,6 +152,7 @@ typedef struct p3d_attn_args {
     const float* global_scale;  /* [D] fp32 */
     const void* sk;             /* from p3d_pool_fwd */
     const void* svt;
+    const float* sk_norm_max;   /* from p3d_pool_fwd */
     p3d_rope rope;
     int32_t grid[3];            /* grid kernel: (Z, Y, X) */
     int32_t radius[3];          /* grid kernel: per-axis radius, each <= 2 */

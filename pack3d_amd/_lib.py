@@ -30,9 +30,10 @@ class Rope(ctypes.Structure):
 class PoolArgs(ctypes.Structure):
     _fields_ = [("batch", c_int32), ("kv_heads", c_int32), ("tokens", c_int32), ("head_dim", c_int32),
                 ("dtype", c_int32), ("fine_blocks", c_int32), ("slots", c_int32), ("pool_size", c_int32),
-                ("summaries", c_int32), ("temperature", c_float), ("kg", View), ("vg", View),
+                ("summaries", c_int32), ("temperature", c_float), ("key_scale", c_float),
+                ("kg", View), ("vg", View),
                 ("blocks", c_void_p), ("weight", c_void_p), ("bias", c_void_p), ("rope", Rope),
-                ("sk", c_void_p), ("svt", c_void_p)]
+                ("sk", c_void_p), ("svt", c_void_p), ("sk_norm_max", c_void_p)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -40,6 +41,7 @@ class AttnArgs(ctypes.Structure):
                 ("head_dim", c_int32), ("dtype", c_int32), ("summaries", c_int32), ("gate_dtype", c_int32),
                 ("q", View), ("kl", View), ("vl", View), ("gate", View),
                 ("local_scale", c_void_p), ("global_scale", c_void_p), ("sk", c_void_p), ("svt", c_void_p),
+                ("sk_norm_max", c_void_p),
                 ("rope", Rope), ("grid", c_int32 * 3), ("radius", c_int32 * 3),
                 ("raster_to_packed", c_void_p), ("o_local_in", c_void_p), ("y", View),
                 ("lse_local", c_void_p), ("lse_global", c_void_p), ("o_local", c_void_p),

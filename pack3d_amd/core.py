@@ -96,13 +96,17 @@ class ForwardPlan:
         mp = -(-m // 32) * 32
         self.sk = torch.empty(b, g, mp, d, dtype=q.dtype, device=dev)
         self.svt = torch.empty(b, g, mp // 32, d, 32, dtype=q.dtype, device=dev)
+        self.sk_norm_max = torch.empty(b * g * 64, dtype=torch.float32, device=dev)
         self._keep = [q, kl, vl, kg, vg, geometry, rope, pool_rope]
         w32 = weight.detach().float().contiguous()
         b32 = bias.detach().float().contiguous()
+        # The attention kernels score against summaries stored pre-multiplied
+        # by log2(e)/sqrt(d), so a score is already in the exp2 domain.
+        self.key_scale = math.log2(math.e) / math.sqrt(d)
         self.pool_args = _lib.PoolArgs(b, g, n, d, dt, f, slots, geometry.pool_size, m, float(temperature),
-                                       _lib.view(kg), _lib.view(vg), geometry.blocks.data_ptr(),
+                                       self.key_scale, _lib.view(kg), _lib.view(vg), geometry.blocks.data_ptr(),
                                        w32.data_ptr(), b32.data_ptr(), pool_rope.struct(),
-                                       self.sk.data_ptr(), self.svt.data_ptr())
+                                       self.sk.data_ptr(), self.svt.data_ptr(), self.sk_norm_max.data_ptr())
         self.y = torch.empty(b, n, h, d, dtype=q.dtype, device=dev).transpose(1, 2)
         sl32, sg32 = sl.detach().float().contiguous(), sg.detach().float().contiguous()
         if gate.dtype not in _lib.DTYPES:
@@ -120,6 +124,7 @@ class ForwardPlan:
         a.gate = _lib.view3(gate)
         a.local_scale, a.global_scale = sl32.data_ptr(), sg32.data_ptr()
         a.sk, a.svt = self.sk.data_ptr(), self.svt.data_ptr()
+        a.sk_norm_max = self.sk_norm_max.data_ptr()
         a.y = _lib.view(self.y)
         a.lse_local = _lib.ptr(self.saved.get("lse_local"))
         a.lse_global = _lib.ptr(self.saved.get("lse_global"))

@@ -201,6 +201,38 @@ __device__ __forceinline__ void soft_probs(Soft<C::MB>& st, const f32x16& s, flo
     if constexpr (!C::ONES) st.l += psum;
 }
 
+// Softmax step against a fixed reference point st.m that bounds every score
+// of the query (st.m >= scale_log2 * max score): p = 2^(s * scale_log2 - m)
+// <= 1, with no running max, rescale or branch.  Exact as long as the bound
+// is not so loose that every p underflows, which the caller checks.
+// s already holds score * scale_log2 - m (the score MFMA starts from -m).
+template <typename C>
+__device__ __forceinline__ void soft_probs_bounded(Soft<C::MB>& st, const f32x16& s, float* p) {
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        p[r] = __builtin_amdgcn_exp2f(s[r]);
+        if constexpr (!C::ONES) psum += p[r];
+    }
+    if constexpr (!C::ONES) st.l += psum;
+}
+
+// Squared 2-norm of this lane's query (both lane groups hold half the channels).
+template <typename C>
+__device__ __forceinline__ float q_norm(const typename C::Frag* qf) {
+    float sq = 0.f;
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t) {
+        if constexpr (C::E == 1) {
+            sq += qf[t] * qf[t];
+        } else {
+#pragma unroll
+            for (int j = 0; j < C::E; ++j) sq += to_f32(qf[t][j]) * to_f32(qf[t][j]);
+        }
+    }
+    return sqrtf(sq + swap_half(sq));
+}
+
 // acc += V^T P^T with preloaded value fragments vf[mb * KSTEPS + ks].
 template <typename C>
 __device__ __forceinline__ void soft_accumulate(Soft<C::MB>& st, const float* p, const typename C::Frag* vf) {

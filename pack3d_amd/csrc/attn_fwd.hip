@@ -37,6 +37,7 @@ struct AttnDev {
     int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, gsb, gsh, gsn;
     const float *sl, *sg;
     const char *sk, *svt;
+    const float* sk_norm_max;
     RopeDev rope;
     const int32_t* map;
     const float* o_local_in;
@@ -145,10 +146,11 @@ struct StageRegs {
 };
 
 // One summary stage (two 32-key tiles) on this wave's two column blocks.
-template <typename C>
+template <typename C, bool BOUND>
 __device__ __forceinline__ void global_stage(const AttnDev& a, int base, const typename C::T_* Ks,
                                              const typename C::T_* Vs, int vstride,
-                                             const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
+                                             const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st,
+                                             const f32x16* negm, int lane) {
     typedef typename C::T_ T;
     const int g = lane >> 5, qi = lane & 31;
 #pragma unroll
@@ -160,7 +162,7 @@ __device__ __forceinline__ void global_stage(const AttnDev& a, int base, const t
         load_vfrags<C, true>(Vs, vstride, 32 * tt, lane, vf);
         f32x16 s[2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) s[nb] = score_tile<C>(kf, qf[nb]);
+        for (int nb = 0; nb < 2; ++nb) s[nb] = BOUND ? score_tile<C>(kf, qf[nb], negm[nb]) : score_tile<C>(kf, qf[nb]);
         if (first + 32 > a.M) {
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb)
@@ -171,17 +173,24 @@ __device__ __forceinline__ void global_stage(const AttnDev& a, int base, const t
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             float p[16];
-            soft_probs<C>(st[nb], s[nb], a.scale_log2, p);
+            if constexpr (BOUND)
+                soft_probs_bounded<C>(st[nb], s[nb], p);
+            else
+                soft_probs<C>(st[nb], s[nb], 1.f, p);  // summary keys carry the log2(e)/sqrt(d) scale
             soft_accumulate<C>(st[nb], p, vf);
         }
     }
 }
 
-// The whole summary pathway for this workgroup: all M summaries streamed
-// through a double-buffered LDS region at `lds`.
-template <typename C>
-__device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typename C::T_* lds,
-                                            const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
+// All M summaries streamed through a double-buffered LDS region at `lds`.
+template <typename C, bool BOUND>
+__device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typename C::T_* lds,
+                                             const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
+    f32x16 negm[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) negm[nb][r] = -st[nb].m;
     typedef typename C::T_ T;
     constexpr int EP = Piece<T>::N;
     constexpr int VGS = 64 + EP;
@@ -197,13 +206,39 @@ __device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typena
         const int next = base + 64;
         if (next < a.M) regs.load(a, bg, next);
         T* cur = lds + buf * STAGE;
-        global_stage<C>(a, base, cur, cur + 64 * C::KSTR, VGS, qf, st, lane);
+        global_stage<C, BOUND>(a, base, cur, cur + 64 * C::KSTR, VGS, qf, st, negm, lane);
         if (next < a.M) {
             T* nxt = lds + (buf ^ 1) * STAGE;
             regs.store(nxt, nxt + 64 * C::KSTR, VGS, min(64, a.Mp - next));
         }
         __syncthreads();
         buf ^= 1;
+    }
+}
+
+// The summary pathway for this workgroup.  Summary keys are stored scaled by
+// log2(e)/sqrt(d), so scores are in the exp2 domain.  Every score of a query
+// is bounded by |q| max_j |sk_j| (Cauchy-Schwarz); that bound is the fixed
+// softmax reference point, fed to the score MFMA as its initial accumulator.
+// If it is so loose that a query's denominator underflows, the workgroup
+// redoes the sweep with the exact online softmax.
+template <typename C>
+__device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typename C::T_* lds,
+                                            const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
+    const float kmax = wave_max(a.sk_norm_max[bg * 64 + lane]);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        st[nb].reset();
+        st[nb].m = q_norm<C>(qf[nb]) * kmax;
+    }
+    global_sweep<C, true>(a, bg, lds, qf, st, lane);
+    bool weak = false;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) weak = weak || !(soft_denominator<C>(st[nb], lane >> 5) > 0x1p-60f);
+    if (__syncthreads_or(weak)) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) st[nb].reset();
+        global_sweep<C, false>(a, bg, lds, qf, st, lane);
     }
 }
 
@@ -628,7 +663,8 @@ int fill_dev(const p3d_attn_args& x, AttnDev& d) {
     P3D_REQUIRE(x.summaries >= 1, "need at least one summary");
     P3D_REQUIRE(view_ok(x.q, es) && view_ok(x.kl, es) && view_ok(x.vl, es) && view_ok(x.y, es),
                 "q/k/v/y rows must be 16-byte aligned");
-    P3D_REQUIRE(x.gate.data && x.local_scale && x.global_scale && x.sk && x.svt, "null pointer argument");
+    P3D_REQUIRE(x.gate.data && x.local_scale && x.global_scale && x.sk && x.svt && x.sk_norm_max,
+                "null pointer argument");
     P3D_REQUIRE(x.rope.table && x.rope.pairs && (x.rope.packed || x.rope.coords), "bad rope arguments");
     d = AttnDev{};
     d.B = x.batch, d.H = x.heads, d.G = x.kv_heads, d.N = x.tokens, d.M = x.summaries;
@@ -640,6 +676,7 @@ int fill_dev(const p3d_attn_args& x, AttnDev& d) {
     d.gate = (const char*)x.gate.data, d.gsb = x.gate.sb, d.gsh = x.gate.sh, d.gsn = x.gate.sn;
     d.sl = x.local_scale, d.sg = x.global_scale;
     d.sk = (const char*)x.sk, d.svt = (const char*)x.svt;
+    d.sk_norm_max = x.sk_norm_max;
     d.rope = rope_dev(x.rope);
     d.map = x.raster_to_packed;
     d.o_local_in = x.o_local_in;

@@ -15,10 +15,13 @@ namespace p3d {
 namespace {
 
 constexpr int kPoolWaves = 4;
+// Summary-norm maxima are spread over this many slots per (batch, kv head) so
+// that the atomics of different waves rarely meet on one address.
+constexpr int kNormSlots = 64;
 
 struct PoolDev {
     int B, G, N, D, F, V, P, M, Mp;
-    float inv_tau;
+    float inv_tau, key_scale;
     const char *kg, *vg;
     int64_t ksb, ksh, ksn, vsb, vsh, vsn;
     const int32_t* blocks;
@@ -27,6 +30,7 @@ struct PoolDev {
     RopeDev rope;
     void* sk;
     void* svt;
+    float* sk_norm_max;
 };
 
 template <typename T>
@@ -116,19 +120,30 @@ __global__ __launch_bounds__(64 * kPoolWaves) void k_pool_fwd(PoolDev a) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
     }
-    const float inv = count ? 1.f / (float)count : 0.f;
     T* sk = reinterpret_cast<T*>(a.sk) + ((int64_t)bg * a.Mp + m) * D;
     T* svt = reinterpret_cast<T*>(a.svt) + (((int64_t)bg * (a.Mp / 32) + m / 32) * D) * 32 + (m & 31);
+    float sq = 0.f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int c = lane + 64 * h;
         if (c < D) {
             // The coarse stage divides the group sum by the count (compression.py:42-43).
-            sk[c] = from_f32<T>(count ? sumk[h] / (float)count : 0.f);
+            const T kq = from_f32<T>(count ? sumk[h] / (float)count * a.key_scale : 0.f);
+            sk[c] = kq;
             svt[c * 32] = from_f32<T>(count ? sumv[h] / (float)count : 0.f);
+            sq += to_f32(kq) * to_f32(kq);
         }
     }
-    (void)inv;
+    // Norm of the stored (rounded) summary key; non-negative floats order
+    // like their bit patterns, so an integer max is an exact float max.
+    const float norm = sqrtf(wave_sum(sq)) * (1.f + 1e-6f);
+    if (lane == 0 && m < a.M)
+        atomicMax(reinterpret_cast<int*>(a.sk_norm_max) + bg * kNormSlots + (m % kNormSlots), __float_as_int(norm));
+}
+
+__global__ void k_zero_f32(float* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.f;
 }
 
 struct RotDev {
@@ -177,10 +192,11 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     P3D_REQUIRE(a.slots >= 1 && a.slots <= 64 && a.pool_size >= 1 && a.pool_size <= 32, "bad pooling shape");
     P3D_REQUIRE(a.summaries == (a.fine_blocks + a.pool_size - 1) / a.pool_size, "summaries != ceil(F/P)");
     P3D_REQUIRE(view_ok(a.kg, es) && view_ok(a.vg, es), "kg/vg rows must be 16-byte aligned");
-    P3D_REQUIRE(a.sk && a.svt && a.blocks && a.weight && a.bias && a.rope.table && a.rope.pairs,
+    P3D_REQUIRE(a.sk && a.svt && a.sk_norm_max && a.blocks && a.weight && a.bias && a.rope.table && a.rope.pairs,
                 "null pointer argument");
     P3D_REQUIRE(a.rope.packed || a.rope.coords, "rope needs coords unless packed");
     P3D_REQUIRE(a.temperature > 0.f, "temperature must be positive");
+    P3D_REQUIRE(a.key_scale > 0.f, "key_scale must be positive");
     PoolDev d{};
     d.B = a.batch;
     d.G = a.kv_heads;
@@ -192,6 +208,7 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     d.M = a.summaries;
     d.Mp = (int)cdiv(a.summaries, 32) * 32;
     d.inv_tau = 1.f / a.temperature;
+    d.key_scale = a.key_scale;
     d.kg = (const char*)a.kg.data;
     d.vg = (const char*)a.vg.data;
     d.ksb = a.kg.sb, d.ksh = a.kg.sh, d.ksn = a.kg.sn;
@@ -202,6 +219,7 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     d.rope = rope_dev(a.rope);
     d.sk = a.sk;
     d.svt = a.svt;
+    d.sk_norm_max = a.sk_norm_max;
     const int64_t items = (int64_t)d.B * d.G * d.Mp;
     const int ep = 16 / es;
     // Each wave stages 64 rows of K and V; keep a block within 64 KiB of LDS.
@@ -210,6 +228,8 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     const size_t smem = per_wave * waves;
     const unsigned blocks = (unsigned)cdiv(items, waves);
     hipStream_t s = as_stream(stream);
+    const int bgn = a.batch * a.kv_heads * kNormSlots;
+    k_zero_f32<<<(unsigned)cdiv(bgn, 256), 256, 0, s>>>(a.sk_norm_max, bgn);
     switch (a.dtype) {
         case P3D_F32: k_pool_fwd<float><<<blocks, 64 * waves, smem, s>>>(d); break;
         case P3D_F16: k_pool_fwd<_Float16><<<blocks, 64 * waves, smem, s>>>(d); break;

@@ -165,3 +165,27 @@ def test_full_size_headline_sampled(gpu):
     exp = ref.pack3d_reference(*rot, *params, gate.cpu(), layer.local_scale.detach().cpu(),
                                layer.global_scale.detach().cpu(), lay_r.geometry, rows=rows, chunk=512)
     _check(y[:, :, rows.to(gpu)], exp, torch.bfloat16, "c2 sampled y")
+
+
+@pytest.mark.parametrize("grid", [False, True])
+def test_core_loose_bound_takes_exact_path(gpu, grid):
+    """A summary key far larger than any score it produces (orthogonal to
+    every query) makes the Cauchy-Schwarz reference point useless; the
+    kernels must fall back to the exact online softmax and still match."""
+    print(f"loose bound grid={grid}", flush=True)
+    shape, d = (8, 8, 8), 48
+    n = math.prod(shape)
+    inputs = random_core_inputs(1, 2, 2, n, d, 64, torch.float32, seed=5)
+    inputs[0][..., d // 2:] = 0                        # queries live in channels 0..23
+    inputs[3][:, :, :64] = 0
+    inputs[3][:, :, :64, d // 2:] = 40.0               # block 0: a huge key in channels 24..47
+    inputs[5] = torch.zeros(d)                         # mean pooling
+    inputs[6] = torch.zeros(64)
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    exp = ref.pack3d_reference(*inputs, lay_r.geometry)
+    if grid:
+        geom = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block").geometry
+    else:
+        geom = p3d.prepare_geometry(lay_r.geometry.neighbors, lay_r.geometry.blocks, 1)
+    got = p3d.pack3d_hip(*(t.to(gpu) for t in inputs), geom)
+    _check(got, exp, torch.float32, "y")

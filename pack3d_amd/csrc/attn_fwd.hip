@@ -92,29 +92,27 @@ __device__ __forceinline__ void load_q(const typename C::T_* row, bool valid, Ro
 // ---------------------------------------------------------------- summaries
 // Summary stages of 64 keys, double-buffered in LDS through registers:
 // K rows (natural order, row stride KSTR) and V transposed (row stride VGS).
+// A stage is one contiguous block of sk ([64][D]) and one of svt
+// ([2][D][32]), so a thread's piece p sits at element offset p * EP in both;
+// the LDS offsets of its pieces are fixed and computed once.
 template <typename C>
 struct StageRegs {
     typedef typename C::T_ T;
     static constexpr int EP = Piece<T>::N;
+    static constexpr int VGS = 64 + EP;
     static constexpr int KPIECES = 64 * (C::D / EP);
     static constexpr int VPIECES = C::D * (64 / EP);
     static constexpr int KI = (KPIECES + 64 * kWaves - 1) / (64 * kWaves);
     static constexpr int VI = (VPIECES + 64 * kWaves - 1) / (64 * kWaves);
     uint4 k[KI], v[VI];
+    int klds[KI], vlds[VI];
 
-    __device__ __forceinline__ void load(const AttnDev& a, int64_t bg, int base) {
-#pragma unroll
-        for (int i = 0; i < KI; ++i) k[i] = uint4{0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < VI; ++i) v[i] = uint4{0, 0, 0, 0};
-        const int rows = min(64, a.Mp - base);  // 32 or 64; pad rows of sk / svt are zero
-        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
-        const T* svt = tp<T>(a.svt) + ((int64_t)bg * (a.Mp / 32) + base / 32) * C::D * 32;
+    __device__ __forceinline__ StageRegs() {
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
             const int p = threadIdx.x + i * 64 * kWaves;
             const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
-            if (p < KPIECES && r < rows) k[i] = *reinterpret_cast<const uint4*>(sk + r * C::D + c);
+            klds[i] = r * C::KSTR + c;
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
@@ -122,26 +120,35 @@ struct StageRegs {
             const int tt = p / (C::D * (32 / EP));
             const int rem = p - tt * C::D * (32 / EP);
             const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
-            if (p < VPIECES && 32 * tt < rows)
-                v[i] = *reinterpret_cast<const uint4*>(svt + ((int64_t)tt * C::D + ch) * 32 + kk);
+            vlds[i] = 64 * C::KSTR + ch * VGS + 32 * tt + kk;
         }
     }
 
-    __device__ __forceinline__ void store(T* Ks, T* Vs, int vstride, int rows) const {
+    // Stage [base, base + 64) (32 or 64 valid rows; pad rows of sk / svt are zero).
+    __device__ __forceinline__ void load(const AttnDev& a, int64_t bg, int base) {
+        const int limit = min(64, a.Mp - base) * C::D;  // elements present in each block
+        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
+        const T* svt = tp<T>(a.svt) + ((int64_t)bg * a.Mp + base) * C::D;
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
-            const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
-            if (p < KPIECES && r < rows) *reinterpret_cast<uint4*>(Ks + r * C::KSTR + c) = k[i];
+            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
+            k[i] = off < limit ? *reinterpret_cast<const uint4*>(sk + off) : uint4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
-            const int tt = p / (C::D * (32 / EP));
-            const int rem = p - tt * C::D * (32 / EP);
-            const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
-            if (p < VPIECES && 32 * tt < rows) *reinterpret_cast<uint4*>(Vs + ch * vstride + 32 * tt + kk) = v[i];
+            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
+            v[i] = off < limit ? *reinterpret_cast<const uint4*>(svt + off) : uint4{0, 0, 0, 0};
         }
+    }
+
+    // Write the staged pieces into a stage buffer (K rows then V rows).
+    __device__ __forceinline__ void store(T* stage) const {
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            if (threadIdx.x + i * 64 * kWaves < KPIECES) *reinterpret_cast<uint4*>(stage + klds[i]) = k[i];
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+            if (threadIdx.x + i * 64 * kWaves < VPIECES) *reinterpret_cast<uint4*>(stage + vlds[i]) = v[i];
     }
 };
 
@@ -199,7 +206,7 @@ __device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typen
     init_v_padding<C>(lds + STAGE + 64 * C::KSTR, VGS, 64);
     StageRegs<C> regs;
     regs.load(a, bg, 0);
-    regs.store(lds, lds + 64 * C::KSTR, VGS, min(64, a.Mp));
+    regs.store(lds);
     __syncthreads();
     int buf = 0;
     for (int base = 0; base < a.M; base += 64) {
@@ -207,10 +214,7 @@ __device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typen
         if (next < a.M) regs.load(a, bg, next);
         T* cur = lds + buf * STAGE;
         global_stage<C, BOUND>(a, base, cur, cur + 64 * C::KSTR, VGS, qf, st, negm, lane);
-        if (next < a.M) {
-            T* nxt = lds + (buf ^ 1) * STAGE;
-            regs.store(nxt, nxt + 64 * C::KSTR, VGS, min(64, a.Mp - next));
-        }
+        if (next < a.M) regs.store(lds + (buf ^ 1) * STAGE);
         __syncthreads();
         buf ^= 1;
     }

@@ -66,6 +66,39 @@ def time_events(fn, iters, stream):
     return start.elapsed_time(end) / iters
 
 
+def kernel_times_in_layer(layer, x, layout, steps, stream):
+    """Mean durations (ms) of the pool and attention launches within layer steps."""
+    from pack3d_amd.core import ForwardPlan
+
+    marks = []
+    orig_pool, orig_attn = ForwardPlan.pool, ForwardPlan.attention
+
+    def mark():
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record(stream)
+        marks.append(ev)
+
+    def pool(self):
+        mark()
+        orig_pool(self)
+        mark()
+
+    def attention(self):
+        mark()
+        orig_attn(self)
+        mark()
+
+    ForwardPlan.pool, ForwardPlan.attention = pool, attention
+    try:
+        for _ in range(steps):
+            layer(x, layout)
+    finally:
+        ForwardPlan.pool, ForwardPlan.attention = orig_pool, orig_attn
+    torch.cuda.synchronize()
+    spans = [marks[i].elapsed_time(marks[i + 1]) for i in range(0, len(marks), 2)]
+    return sum(spans[0::2]) / steps, sum(spans[1::2]) / steps
+
+
 def cpu_baseline(shape, threads):
     """The oracle (a restatement of the reference CPU path) on a bounded sample.
 
@@ -103,12 +136,56 @@ def cpu_baseline(shape, threads):
                        f"{times[sizes[1]]:.2f}s); extrapolated linearly in rows to {n}")}
 
 
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_c2.md")
+
+
 def load_traffic():
-    path = os.path.join(ROOT, "profiles", "traffic_attn_fwd_grid_c2.json")
-    if os.path.exists(path):
-        with open(path) as f:
-            return json.load(f).get("bytes_per_launch")
-    return None
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE.
+
+    The summary holds one fenced ``json`` block written from two ``--pmc``
+    passes over ``bench.py --traffic-probe``; each counter is scaled by what
+    it reads for an elementwise copy of known size in the same process.
+    """
+    if not os.path.exists(TRAFFIC_SUMMARY):
+        return {}
+    text = open(TRAFFIC_SUMMARY).read()
+    start = text.find("```json")
+    if start < 0:
+        return {}
+    body = text[start + len("```json"):text.find("```", start + 7)]
+    return json.loads(body)
+
+
+def traffic_probe():
+    """Launch sequence profiled for HBM traffic (run under rocprofv3 --pmc).
+
+    A 1 GiB fill evicts the caches, an elementwise add over 256 MiB gives the
+    counter calibration (268,435,456 bytes read and written), then the pool
+    and attention kernels of the c2 workload run three times each.
+    """
+    import pack3d_amd as p3d
+    from pack3d_amd.core import ForwardPlan
+
+    dev = torch.device("cuda:0")
+    n = math.prod(SHAPE)
+    layer = build_layer(dev, torch.bfloat16)
+    layout = p3d.build_layout(SHAPE, BLOCK, radius=RADIUS, pool_size=1, layout="raster_block", device=dev)
+    x = torch.randn(1, n, DIM, generator=torch.Generator().manual_seed(1)).to(dev, torch.bfloat16)
+    flush = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)
+    src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    with torch.inference_mode():
+        q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, layout)
+        plan = ForwardPlan(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate, layer.local_scale,
+                           layer.global_scale, layout.geometry, layer.temperature, rope, rope)
+        for _ in range(3):
+            flush.fill_(0.0)
+            torch.add(src, 1.0, out=dst)
+            flush.fill_(0.0)
+            plan.pool()
+            plan.attention()
+    torch.cuda.synchronize()
+    print("traffic probe done", flush=True)
 
 
 def main():
@@ -118,6 +195,8 @@ def main():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="only run the launch sequence that the HBM traffic counters are collected over")
     a = p.parse_args()
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
@@ -125,6 +204,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
         sys.exit(2)
+    if a.traffic_probe:
+        traffic_probe()
+        return
 
     import pack3d_amd as p3d
     from pack3d_amd.core import ForwardPlan
@@ -147,15 +229,15 @@ def main():
         torch.cuda.synchronize()
         ms_layer = 1000.0 * (time.perf_counter() - t0) / a.steps
 
-        # Per-kernel durations with HIP events on the launch stream.
+        # Per-kernel durations inside the same layer steps: HIP events on the
+        # launch stream around the pool and attention launches of each step
+        # (a second pass over the steps, so the first one runs without them).
+        ms_pool, ms_attn = kernel_times_in_layer(layer, x, layout, a.steps, stream)
         q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, layout)
         plan = ForwardPlan(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate, layer.local_scale,
                            layer.global_scale, layout.geometry, layer.temperature, rope, rope)
         plan.run()
-        iters = max(5, a.steps)
-        ms_pool = time_events(plan.pool, iters, stream)
-        ms_attn = time_events(plan.attention, iters, stream)
-        ms_core = time_events(plan.run, iters, stream)
+        ms_core = time_events(plan.run, max(5, a.steps), stream)
 
     m = layout.geometry.num_summaries
     edges = valid_edges(SHAPE, RADIUS)
@@ -165,6 +247,7 @@ def main():
     pool_bytes = 2 * KV_HEADS * n * HEAD_DIM * 2 + 2 * KV_HEADS * m * HEAD_DIM * 2
     pool_gbs = pool_bytes / (ms_pool * 1e-3) / 1e9
     cpu = None if a.no_cpu_baseline else cpu_baseline(SHAPE, a.cpu_threads)
+    traffic = load_traffic()
     out = {
         "metric": METRIC, "value": round(ms_layer, 4), "unit": "ms", "n_gpus": 1, "steps": a.steps,
         "warmup": a.warmup, "ms_per_step": round(ms_layer, 4), "higher_is_better": False, "scaling": "weak",
@@ -177,10 +260,11 @@ def main():
                    "ms_attn_kernel": round(ms_attn, 4), "parallelism": "single GPU"},
         "roofline": {"kernel": "k_attn_grid (fused local+global forward)", "bound": "mfma",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": load_traffic(),
+                     "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get("attn_bytes_per_launch"),
                      "algorithmic_flops": flops_summary + flops_local},
         "roofline_pool": {"kernel": "k_pool_fwd", "bound": "hbm", "achieved": round(pool_gbs, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(pool_gbs / PEAK_HBM_GBS, 4),
+                          "traffic": traffic.get("pool_bytes_per_launch"),
                           "algorithmic_bytes": pool_bytes},
         "cpu_baseline": cpu,
     }

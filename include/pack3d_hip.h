@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 1
+#define P3D_ABI_VERSION 2
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -50,7 +50,7 @@ typedef struct p3d_rope {
     const int32_t* pairs;   /* [head_dim/2][3] */
     const int64_t* coords;  /* [N, 3] (z, y, x) or NULL when packed != 0 */
     int32_t packed;
-    int32_t pad_;
+    int32_t table_entries;  /* number of float2 entries in table */
 } p3d_rope;
 
 const char* p3d_last_error(void);

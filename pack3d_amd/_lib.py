@@ -22,9 +22,12 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
+ABI_VERSION = 2  # P3D_ABI_VERSION in include/pack3d_hip.h
+
+
 class Rope(ctypes.Structure):
     _fields_ = [("table", c_void_p), ("pairs", c_void_p), ("coords", c_void_p),
-                ("packed", c_int32), ("pad_", c_int32)]
+                ("packed", c_int32), ("table_entries", c_int32)]
 
 
 class PoolArgs(ctypes.Structure):
@@ -87,7 +90,7 @@ def lib():
                     fn = getattr(handle, name)
                     fn.argtypes = args
                     fn.restype = res
-                if handle.p3d_abi_version() != 1:
+                if handle.p3d_abi_version() != ABI_VERSION:
                     raise RuntimeError("pack3d_amd HIP library ABI mismatch; rebuild it")
                 _lib = handle
     return _lib

@@ -1,12 +1,16 @@
 // Summary pooling (compression.py:28-44 of amilworks/Pack3D) and the
 // standalone rotation (rotary.py:10-45).
 //
-// One wave pools one coarse summary of one (batch, kv head): for each of its
-// fine blocks the wave stages the member rows of K (rotated on load and
-// rounded to the storage type, as the reference pools rotated keys stored
-// in that type) and V in LDS with coalesced 16-byte loads, computes the slot
-// logits, the slot softmax and the weighted sums, and accumulates the fine
-// summaries; the coarse mean divides by the number of non-empty fine blocks.
+// One wave pools one coarse summary of one (batch, kv head).  For each of its
+// fine blocks the wave issues every 16-byte load of the block's K and V rows
+// at once (lane l holds pieces l, l + 64, ... of the 64 x D/EP piece grid)
+// and writes the K rows to LDS with 16-byte stores.  Then one lane per slot
+// reads its K row (conflict-free 16-byte reads), rotates it, rounds it to the
+// storage type (the reference pools rotated keys stored in that type), writes
+// it back and forms the slot logit; the slot softmax is a wave reduction.  The
+// weighted sums are column reads of the K rows, then of the V rows staged in
+// the same buffer.  The coarse mean divides by the number of non-empty fine
+// blocks.
 #include <algorithm>
 
 #include "rope.hpp"
@@ -14,13 +18,12 @@
 namespace p3d {
 namespace {
 
-constexpr int kPoolWaves = 4;
 // Summary-norm maxima are spread over this many slots per (batch, kv head) so
 // that the atomics of different waves rarely meet on one address.
 constexpr int kNormSlots = 64;
 
 struct PoolDev {
-    int B, G, N, D, F, V, P, M, Mp;
+    int B, G, N, F, V, P, M, Mp;
     float inv_tau, key_scale;
     const char *kg, *vg;
     int64_t ksb, ksh, ksn, vsb, vsh, vsn;
@@ -28,110 +31,130 @@ struct PoolDev {
     const float* weight;
     const float* bias;
     RopeDev rope;
+    int table_entries;  // rope table entries (float2); staged in LDS when it fits
     void* sk;
     void* svt;
     float* sk_norm_max;
 };
 
-template <typename T>
-__global__ __launch_bounds__(64 * kPoolWaves) void k_pool_fwd(PoolDev a) {
-    const int waves = blockDim.x >> 6;
-    constexpr int EP = Piece<T>::N;
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int D = a.D;
-    const int stride = D + EP;  // LDS row stride in elements (keeps 16-byte alignment)
-    T* lk = reinterpret_cast<T*>(smem_raw) + (size_t)wave * 2 * 64 * stride;
-    T* lv = lk + 64 * stride;
-    float* la = reinterpret_cast<float*>(reinterpret_cast<T*>(smem_raw) + (size_t)waves * 2 * 64 * stride) +
-                wave * 64;
+// LDS plan of one wave: one buffer of 64 rows (row stride D + EP elements)
+// that holds the block's K rows and then its V rows, plus the 64 slot
+// weights.  For the column sums lane (h, u) owns column dword u of the slots
+// h, h + S, h + 2S, ...; the row stride is 4 dwords more than a row, so the
+// S lane groups read disjoint banks when S rows fit in 64 banks.
+template <typename T, int D>
+struct PoolCfg {
+    static constexpr int EP = Piece<T>::N;        // elements per 16-byte piece
+    static constexpr int PPR = D / EP;             // pieces per row (and per lane, per tensor)
+    static constexpr int CPD = 4 / sizeof(T);      // channels per dword
+    static constexpr int RD = (D + EP) / CPD;      // row stride in dwords
+    static constexpr int DW = D / CPD;             // payload dwords per row
+    static constexpr int LW = DW <= 8 ? 8 : (DW <= 16 ? 16 : (DW <= 32 ? 32 : 64));  // lanes per slot group
+    static constexpr int S = 64 / LW;              // slot groups
+    static constexpr int SJ = (DW + 63) / 64;      // column dwords per lane
+    static constexpr int WAVE_DW = 64 * RD + 64;   // rows + slot weights
+};
 
-    const int64_t total = (int64_t)a.B * a.G * a.Mp;
-    const int64_t item = (int64_t)blockIdx.x * waves + wave;
-    if (item >= total) return;  // whole wave leaves; waves never synchronise with each other
-    const int m = (int)(item % a.Mp);
-    const int64_t bg = item / a.Mp;
-    const int b = (int)(bg / a.G), g = (int)(bg % a.G);
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-    float sumk[2] = {0.f, 0.f}, sumv[2] = {0.f, 0.f};
-    int count = 0;
-    if (m < a.M) {
-        const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
-        const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
-        const int ppr = D / EP;  // pieces per row
-        const int f_end = min(a.F, (m + 1) * a.P);
-        for (int f = m * a.P; f < f_end; ++f) {
-            const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
-            if (__ballot(idx >= 0) == 0) continue;  // empty fine block: no mass, no count
-            ++count;
-            for (int q = lane; q < 64 * ppr; q += 64) {
-                const int s = q / ppr, piece = q - s * ppr;
-                const int t = __shfl(idx, s);
-                float kx[EP], vx[EP];
-                if (t >= 0) {
-                    load_piece<T>(K + t * a.ksn + piece * EP, kx);
-                    load_piece<T>(Vv + t * a.vsn + piece * EP, vx);
-                    int64_t pos[3];
-                    rope_position(a.rope, t, pos);
-                    rope_apply(a.rope, pos, piece * EP, kx, EP);
-                } else {
+// Store a tensor's pieces (lane l holds pieces l, l + 64, ... of the 64 x PPR
+// grid) as rows of the LDS buffer.
+template <typename C>
+__device__ __forceinline__ void stage_rows(uint32_t* rows, const uint4 (&r)[C::PPR], int lane) {
 #pragma unroll
-                    for (int e = 0; e < EP; ++e) kx[e] = vx[e] = 0.f;
-                }
+    for (int i = 0; i < C::PPR; ++i) {
+        const int q = i * 64 + lane, s = q / C::PPR, p = q - s * C::PPR;
+        *reinterpret_cast<uint4*>(rows + s * C::RD + p * 4) = r[i];
+    }
+}
+
+// sum_s w_s * row_s, column by column; every lane ends with the totals of its
+// column dwords (lane % LW, + 64, ...).  w is the slot weight held by lane s;
+// it is broadcast with readlane, so the loop issues only row reads to LDS.
+template <typename C, typename T>
+__device__ __forceinline__ void column_sums(const uint32_t* rows, float w, int lane, float (&out)[C::SJ][C::CPD]) {
+    const int h = lane / C::LW, u0 = lane % C::LW;
+    float part[C::SJ][C::CPD];
 #pragma unroll
-                for (int e = 0; e < EP; ++e) {
-                    lk[s * stride + piece * EP + e] = from_f32<T>(kx[e]);
-                    lv[s * stride + piece * EP + e] = from_f32<T>(vx[e]);
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            // Slot logits (compression.py:31-35): (k . w) / tau + bias_s.
-            float logit = -INFINITY;
-            if (idx >= 0) {
-                float dot = 0.f;
-                for (int c = 0; c < D; ++c) dot += to_f32(lk[lane * stride + c]) * a.weight[c];
-                logit = dot * a.inv_tau + a.bias[lane];
-            }
-            const float mx = wave_max(logit);
-            const float e = idx >= 0 ? expf(logit - mx) : 0.f;
-            const float den = wave_sum(e);
-            la[lane] = e / den;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int j = 0; j < C::SJ; ++j)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int c = lane + 64 * h;
-                if (c < D) {
-                    float fk = 0.f, fv = 0.f;
-                    for (int s = 0; s < a.V; ++s) {
-                        const float w = la[s];
-                        fk += w * to_f32(lk[s * stride + c]);
-                        fv += w * to_f32(lv[s * stride + c]);
-                    }
-                    sumk[h] += fk;
-                    sumv[h] += fv;
-                }
+        for (int c = 0; c < C::CPD; ++c) part[j][c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64 / C::S; ++i) {
+        float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i * C::S));
+#pragma unroll
+        for (int hh = 1; hh < C::S; ++hh) {
+            const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i * C::S + hh));
+            ws = h == hh ? o : ws;
+        }
+        const int s = i * C::S + h;
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j) {
+            const int u = u0 + 64 * j;
+            if (u < C::DW) {
+                const uint32_t raw = rows[s * C::RD + u];
+                const T* x = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+                for (int c = 0; c < C::CPD; ++c) part[j][c] += ws * to_f32(x[c]);
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
     }
+#pragma unroll
+    for (int o = C::LW; o < 64; o <<= 1)
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+            for (int c = 0; c < C::CPD; ++c) part[j][c] += __shfl_xor(part[j][c], o);
+#pragma unroll
+    for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+        for (int c = 0; c < C::CPD; ++c) out[j][c] += part[j][c];
+}
+
+// Rotate a run of EP channels starting at c0 with (cos, sin) from `tab`
+// (the rope table, in LDS or in global memory); meta[j] = {base, stride, axis}
+// of rotary pair j, staged in LDS.
+template <int EP>
+__device__ __forceinline__ void rotate_piece(const int4* meta, const float2* tab, const int pos[3], int c0, float* x) {
+#pragma unroll
+    for (int e = 0; e < EP; e += 2) {
+        const int4 p = meta[(c0 + e) >> 1];
+        const int coord = p.z == 0 ? pos[0] : (p.z == 1 ? pos[1] : pos[2]);
+        const float2 cs = tab[p.x + p.y * coord];
+        rotate_pair(x[e], x[e + 1], cs.x, cs.y);
+    }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void write_summary(const PoolDev& a, int64_t item, int lane, int count,
+                                              const float (&acck)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD],
+                                              const float (&accv)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD]) {
+    typedef PoolCfg<T, D> C;
+    const int g = (int)(item % a.G);
+    const int64_t bm = item / a.G;
+    const int m = (int)(bm % a.Mp), b = (int)(bm / a.Mp);
+    const int64_t bg = (int64_t)b * a.G + g;
+    // The coarse stage divides the group sum by the count (compression.py:42-43).
     T* sk = reinterpret_cast<T*>(a.sk) + ((int64_t)bg * a.Mp + m) * D;
     T* svt = reinterpret_cast<T*>(a.svt) + (((int64_t)bg * (a.Mp / 32) + m / 32) * D) * 32 + (m & 31);
     float sq = 0.f;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int c = lane + 64 * h;
-        if (c < D) {
-            // The coarse stage divides the group sum by the count (compression.py:42-43).
-            const T kq = from_f32<T>(count ? sumk[h] / (float)count * a.key_scale : 0.f);
-            sk[c] = kq;
-            svt[c * 32] = from_f32<T>(count ? sumv[h] / (float)count : 0.f);
-            sq += to_f32(kq) * to_f32(kq);
+    for (int j = 0; j < C::SJ; ++j) {
+        const int u = lane + 64 * j;
+        if (lane < C::LW && u < C::DW) {
+            uint32_t word;
+            T* x = reinterpret_cast<T*>(&word);
+#pragma unroll
+            for (int c = 0; c < C::CPD; ++c) {
+                x[c] = from_f32<T>(count ? acck[j][c] / (float)count * a.key_scale : 0.f);
+                sq += to_f32(x[c]) * to_f32(x[c]);
+                svt[(u * C::CPD + c) * 32] = from_f32<T>(count ? accv[j][c] / (float)count : 0.f);
+            }
+            *reinterpret_cast<uint32_t*>(sk + u * C::CPD) = word;
         }
     }
     // Norm of the stored (rounded) summary key; non-negative floats order
@@ -139,6 +162,116 @@ __global__ __launch_bounds__(64 * kPoolWaves) void k_pool_fwd(PoolDev a) {
     const float norm = sqrtf(wave_sum(sq)) * (1.f + 1e-6f);
     if (lane == 0 && m < a.M)
         atomicMax(reinterpret_cast<int*>(a.sk_norm_max) + bg * kNormSlots + (m % kNormSlots), __float_as_int(norm));
+}
+
+// Persistent: wave w of block k takes items k * waves + w, + waves * grid, ...
+// Items run kv head fastest, so the waves of a block read the neighbouring
+// head slices of the same token rows together and each row's kg / vg span is
+// fetched from HBM once and in one piece.  With TAB_LDS the block first
+// copies the rope table into LDS, so the per-slot (cos, sin) gathers of the
+// rotation are LDS reads.
+template <typename T, int D, bool TAB_LDS>
+__global__ __launch_bounds__(256) void k_pool_fwd(PoolDev a) {
+    typedef PoolCfg<T, D> C;
+    constexpr int EP = C::EP, PPR = C::PPR, CPD = C::CPD;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const int waves = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // LDS: pair metadata [D/2] int4, weights [D], biases [64], the rope table
+    // (TAB_LDS), then one row buffer per wave.
+    int4* meta = reinterpret_cast<int4*>(smem_raw);
+    float* lweight = reinterpret_cast<float*>(meta + D / 2);
+    float* lbias = lweight + D;
+    float2* ltab = reinterpret_cast<float2*>(lbias + 64);
+    const int tab_dw = TAB_LDS ? ((a.table_entries * 2 + 3) & ~3) : 0;
+    uint32_t* rows = reinterpret_cast<uint32_t*>(ltab) + tab_dw + wave * C::WAVE_DW;
+    for (int j = threadIdx.x; j < D / 2; j += blockDim.x)
+        meta[j] = int4{a.rope.pairs[3 * j], a.rope.pairs[3 * j + 1], a.rope.pairs[3 * j + 2], 0};
+    for (int c = threadIdx.x; c < D; c += blockDim.x) lweight[c] = a.weight[c];
+    for (int c = threadIdx.x; c < 64; c += blockDim.x) lbias[c] = c < a.V ? a.bias[c] : 0.f;
+    const float2* tab = a.rope.table;
+    if (TAB_LDS) {
+        for (int e = threadIdx.x; e < a.table_entries; e += blockDim.x) ltab[e] = a.rope.table[e];
+        tab = ltab;
+    }
+    __syncthreads();
+
+    const int64_t total = (int64_t)a.B * a.G * a.Mp;
+    const int64_t stride = (int64_t)gridDim.x * waves;
+    for (int64_t item = (int64_t)blockIdx.x * waves + wave; item < total; item += stride) {
+        const int g = (int)(item % a.G);
+        const int64_t bm = item / a.G;
+        const int m = (int)(bm % a.Mp), b = (int)(bm / a.Mp);
+        float acck[C::SJ][CPD], accv[C::SJ][CPD];
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+            for (int c = 0; c < CPD; ++c) acck[j][c] = accv[j][c] = 0.f;
+        int count = 0;
+        const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
+        const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
+        const int f_end = m < a.M ? min(a.F, (m + 1) * a.P) : 0;
+        for (int f = m * a.P; f < f_end; ++f) {
+            const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
+            if (__ballot(idx >= 0) == 0) continue;  // empty fine block: no mass, no count
+            ++count;
+            // Every load of the block is in flight before any is used; empty
+            // slots read row 0 and are zeroed afterwards (straight-line code).
+            int pos[3];
+            rope_position32(a.rope, max(idx, 0), pos);
+            uint4 kr[PPR], vr[PPR];
+            int tok[PPR];
+#pragma unroll
+            for (int i = 0; i < PPR; ++i) tok[i] = __shfl(idx, (i * 64 + lane) / PPR);
+#pragma unroll
+            for (int i = 0; i < PPR; ++i) {
+                const int q = i * 64 + lane, p = q - (q / PPR) * PPR;
+                const int t = max(tok[i], 0);
+                kr[i] = *reinterpret_cast<const uint4*>(K + (int64_t)t * a.ksn + p * EP);
+                vr[i] = *reinterpret_cast<const uint4*>(Vv + (int64_t)t * a.vsn + p * EP);
+            }
+#pragma unroll
+            for (int i = 0; i < PPR; ++i) {
+                if (tok[i] < 0) kr[i] = vr[i] = uint4{0u, 0u, 0u, 0u};
+            }
+            stage_rows<C>(rows, kr, lane);
+            wave_lds_sync();
+            // One lane per slot: rotate the slot's K row in place, round it to
+            // the storage type, and form its logit (compression.py:31-35):
+            // (k . w) / tau + bias_s.  Rotary pair metadata is wave-uniform here.
+            float logit = -INFINITY;
+            if (idx >= 0) {
+                float dot = 0.f;
+#pragma unroll 1  // one piece at a time keeps the table reads from occupying registers
+                for (int p = 0; p < PPR; ++p) {
+                    uint4 raw = *reinterpret_cast<const uint4*>(rows + lane * C::RD + p * 4);
+                    T* kt = reinterpret_cast<T*>(&raw);
+                    float kx[EP];
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) kx[e] = to_f32(kt[e]);
+                    rotate_piece<EP>(meta, tab, pos, p * EP, kx);
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) {
+                        kt[e] = from_f32<T>(kx[e]);
+                        dot += to_f32(kt[e]) * lweight[p * EP + e];
+                    }
+                    *reinterpret_cast<uint4*>(rows + lane * C::RD + p * 4) = raw;
+                }
+                logit = dot * a.inv_tau + lbias[lane];
+            }
+            const float mx = wave_max(logit);
+            const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
+            const float w = ex / wave_sum(ex);
+            wave_lds_sync();  // rotated rows are read across lanes below
+            column_sums<C, T>(rows, w, lane, acck);
+            wave_lds_sync();
+            stage_rows<C>(rows, vr, lane);
+            wave_lds_sync();
+            column_sums<C, T>(rows, w, lane, accv);
+            wave_lds_sync();  // the next fine block overwrites the rows
+        }
+        write_summary<T, D>(a, item, lane, count, acck, accv);
+    }
 }
 
 __global__ void k_zero_f32(float* p, int n) {
@@ -177,6 +310,45 @@ __global__ void k_rotate(RotDev a) {
     for (int i = 0; i < EP; ++i) y[i] = from_f32<T>(x[i]);
 }
 
+// Rope tables up to this size are staged in LDS by every pool block.
+constexpr int kTableLdsBytes = 32768;
+
+template <typename T, int D>
+void launch_pool_t(const PoolDev& d, int64_t items, hipStream_t s) {
+    // Four waves (four kv heads of a summary) per block; a persistent grid of
+    // as many blocks as stay resident, each striding over the items.
+    constexpr int waves = 4;
+    const bool tab_lds = d.table_entries * 8 <= kTableLdsBytes;
+    const size_t tab_bytes = tab_lds ? (size_t)((d.table_entries * 2 + 3) & ~3) * 4 : 0;
+    const size_t fixed = (size_t)(D / 2) * 16 + (size_t)D * 4 + 64 * 4;
+    const size_t smem = fixed + tab_bytes + (size_t)PoolCfg<T, D>::WAVE_DW * 4 * waves;
+    int dev = 0, cus = 0, per_cu = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (tab_lds)
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_fwd<T, D, true>, 64 * waves, smem);
+    else
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_fwd<T, D, false>, 64 * waves, smem);
+    const int64_t resident = (int64_t)std::max(1, cus) * std::max(1, per_cu);
+    const int64_t needed = cdiv(items, waves);
+    // Equal shares: the fewest rounds that cover every item, spread evenly.
+    const int64_t rounds = cdiv(needed, resident);
+    const unsigned blocks = (unsigned)cdiv(needed, rounds);
+    if (tab_lds)
+        k_pool_fwd<T, D, true><<<blocks, 64 * waves, smem, s>>>(d);
+    else
+        k_pool_fwd<T, D, false><<<blocks, 64 * waves, smem, s>>>(d);
+}
+
+template <int D>
+void launch_pool(const PoolDev& d, int dtype, int64_t items, hipStream_t s) {
+    switch (dtype) {
+        case P3D_F32: launch_pool_t<float, D>(d, items, s); break;
+        case P3D_F16: launch_pool_t<_Float16, D>(d, items, s); break;
+        default: launch_pool_t<__bf16, D>(d, items, s); break;
+    }
+}
+
 }  // namespace
 }  // namespace p3d
 
@@ -187,21 +359,21 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     const p3d_pool_args& a = *args;
     const int es = dtype_size(a.dtype);
     P3D_REQUIRE(a.dtype >= P3D_F32 && a.dtype <= P3D_BF16, "unknown dtype");
-    P3D_REQUIRE(a.head_dim >= 2 && a.head_dim <= 128 && a.head_dim % (16 / es) == 0,
-                "head_dim must be a multiple of the 16-byte piece and at most 128");
+    P3D_REQUIRE(a.head_dim == 16 || a.head_dim == 32 || a.head_dim == 48 || a.head_dim == 64 || a.head_dim == 128,
+                "head_dim must be 16, 32, 48, 64 or 128");
     P3D_REQUIRE(a.slots >= 1 && a.slots <= 64 && a.pool_size >= 1 && a.pool_size <= 32, "bad pooling shape");
     P3D_REQUIRE(a.summaries == (a.fine_blocks + a.pool_size - 1) / a.pool_size, "summaries != ceil(F/P)");
     P3D_REQUIRE(view_ok(a.kg, es) && view_ok(a.vg, es), "kg/vg rows must be 16-byte aligned");
     P3D_REQUIRE(a.sk && a.svt && a.sk_norm_max && a.blocks && a.weight && a.bias && a.rope.table && a.rope.pairs,
                 "null pointer argument");
     P3D_REQUIRE(a.rope.packed || a.rope.coords, "rope needs coords unless packed");
+    P3D_REQUIRE(a.rope.table_entries >= 1, "rope table_entries must be positive");
     P3D_REQUIRE(a.temperature > 0.f, "temperature must be positive");
     P3D_REQUIRE(a.key_scale > 0.f, "key_scale must be positive");
     PoolDev d{};
     d.B = a.batch;
     d.G = a.kv_heads;
     d.N = a.tokens;
-    d.D = a.head_dim;
     d.F = a.fine_blocks;
     d.V = a.slots;
     d.P = a.pool_size;
@@ -217,23 +389,20 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     d.weight = a.weight;
     d.bias = a.bias;
     d.rope = rope_dev(a.rope);
+    d.table_entries = a.rope.table_entries;
     d.sk = a.sk;
     d.svt = a.svt;
     d.sk_norm_max = a.sk_norm_max;
-    const int64_t items = (int64_t)d.B * d.G * d.Mp;
-    const int ep = 16 / es;
-    // Each wave stages 64 rows of K and V; keep a block within 64 KiB of LDS.
-    const size_t per_wave = (size_t)2 * 64 * (d.D + ep) * es + 64 * sizeof(float);
-    const int waves = (int)std::max<size_t>(1, std::min<size_t>(kPoolWaves, 65536 / per_wave));
-    const size_t smem = per_wave * waves;
-    const unsigned blocks = (unsigned)cdiv(items, waves);
     hipStream_t s = as_stream(stream);
     const int bgn = a.batch * a.kv_heads * kNormSlots;
     k_zero_f32<<<(unsigned)cdiv(bgn, 256), 256, 0, s>>>(a.sk_norm_max, bgn);
-    switch (a.dtype) {
-        case P3D_F32: k_pool_fwd<float><<<blocks, 64 * waves, smem, s>>>(d); break;
-        case P3D_F16: k_pool_fwd<_Float16><<<blocks, 64 * waves, smem, s>>>(d); break;
-        default: k_pool_fwd<__bf16><<<blocks, 64 * waves, smem, s>>>(d); break;
+    const int64_t items = (int64_t)d.B * d.G * d.Mp;
+    switch (a.head_dim) {
+        case 16: launch_pool<16>(d, a.dtype, items, s); break;
+        case 32: launch_pool<32>(d, a.dtype, items, s); break;
+        case 48: launch_pool<48>(d, a.dtype, items, s); break;
+        case 64: launch_pool<64>(d, a.dtype, items, s); break;
+        default: launch_pool<128>(d, a.dtype, items, s); break;
     }
     return check_launch("p3d_pool_fwd");
 }

@@ -49,4 +49,29 @@ __device__ __forceinline__ void rope_apply(const RopeDev& r, const int64_t pos[3
     }
 }
 
+// 32-bit forms for kernels that keep positions of many rows in registers.
+// Table indices are base + stride * coordinate < 2^31: coordinates are below
+// the token count and the hosts validate rows * head_dim < 2^31.
+__device__ __forceinline__ void rope_position32(const RopeDev& r, int n, int pos[3]) {
+    if (r.packed) {
+        pos[0] = n;
+        pos[1] = 0;
+        pos[2] = 0;
+    } else {
+        pos[0] = (int)r.coords[3 * (int64_t)n + 0];
+        pos[1] = (int)r.coords[3 * (int64_t)n + 1];
+        pos[2] = (int)r.coords[3 * (int64_t)n + 2];
+    }
+}
+
+__device__ __forceinline__ void rope_apply32(const RopeDev& r, const int pos[3], int c0, float* x, int count) {
+    for (int e = 0; e < count; e += 2) {
+        const int32_t* p = r.pairs + 3 * ((c0 + e) >> 1);
+        const int axis = p[2];
+        const int coord = axis == 0 ? pos[0] : (axis == 1 ? pos[1] : pos[2]);
+        const float2 cs = r.table[p[0] + p[1] * coord];
+        rotate_pair(x[e], x[e + 1], cs.x, cs.y);
+    }
+}
+
 }  // namespace p3d

@@ -33,7 +33,8 @@ class RopeSpec:
 
     def struct(self):
         return _lib.Rope(self.table.data_ptr(), self.pairs.data_ptr(),
-                         None if self.coords is None else self.coords.data_ptr(), self.packed, 0)
+                         None if self.coords is None else self.coords.data_ptr(), self.packed,
+                         self.table.shape[0])
 
 
 _cache: "OrderedDict[tuple, tuple]" = OrderedDict()

@@ -33,7 +33,9 @@ def test_struct_mirrors_match_c_sizes():
     assert _lib.lib().p3d_struct_sizes(out) == 0
     assert list(out) == [ctypes.sizeof(_lib.View), ctypes.sizeof(_lib.Rope), ctypes.sizeof(_lib.PoolArgs),
                          ctypes.sizeof(_lib.AttnArgs)]
-    assert _lib.lib().p3d_abi_version() == 1
+    header = open(os.path.join(ROOT, "include", "pack3d_hip.h")).read()
+    version = int(re.search(r"#define P3D_ABI_VERSION (\d+)", header).group(1))
+    assert _lib.lib().p3d_abi_version() == version == _lib.ABI_VERSION
 
 
 def test_entry_points_reject_bad_arguments_before_launch():

@@ -137,34 +137,81 @@ def test_repack_permutes_outputs_exactly(gpu):
         assert torch.equal(yp, y[:, :, p.to(gpu)]), dtype
 
 
-def test_full_size_headline_sampled(gpu):
-    """c2: 64^3 bf16, dim 192, 4 heads, d 48, radius 2, 4^3 blocks: sampled rows vs the oracle."""
-    print("full size c2 sampled", flush=True)
+def _xavier_layer(shape, batch, dtype, gpu):
+    """The benchmark layer of the BASELINE configs: Xavier projections from
+    seed 0, mean pooling (w = b = 0), tokens ~ N(0, 1) from seed 1."""
     torch.manual_seed(0)
-    shape = (64, 64, 64)
-    n = math.prod(shape)
     layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
     for lin in (layer.to_q, layer.to_kv, layer.to_out):
         torch.nn.init.xavier_uniform_(lin.weight)
     with torch.no_grad():
         layer.pool_weight.zero_()
         layer.slot_bias.zero_()
-    layer = layer.to(gpu, torch.bfloat16)
-    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
-    x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1)).to(gpu, torch.bfloat16)
+    x = torch.randn(batch, math.prod(shape), 192, generator=torch.Generator().manual_seed(1))
+    return layer.to(gpu, dtype), x.to(gpu, dtype)
+
+
+def _core_sampled_vs_oracle(layer, x, lay, shape, kind, dtype, what, nrows=1024):
+    """Core output of the layer at full size; 1024 random rows plus corner rows
+    are compared with the oracle evaluated on those rows only."""
     with torch.no_grad():
-        q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, lay)
+        core = layer.core_inputs(x, lay)
+        q, kl, vl, kg, vg, gate, rope = core
         y = p3d.pack3d_hip_rope(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate,
                                 layer.local_scale, layer.global_scale, lay.geometry, rope)
-    rows = torch.randperm(n, generator=torch.Generator().manual_seed(2))[:1024]
-    rows = torch.cat((rows, torch.tensor([0, n - 1, 63, 64 * 64 - 1])))
-    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    n = math.prod(shape)
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(2))[:nrows]
+    rows = torch.cat((rows, torch.tensor([0, n - 1, shape[2] - 1, shape[1] * shape[2] - 1])))
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout=kind)
     cpu = [t.cpu() for t in (q, kl, vl, kg, vg)]
     rot = [ref.axial_rope(t, lay_r.coords) if i in (0, 1, 3) else t for i, t in enumerate(cpu)]
     params = [t.detach().cpu() for t in (layer.pool_weight, layer.slot_bias)]
     exp = ref.pack3d_reference(*rot, *params, gate.cpu(), layer.local_scale.detach().cpu(),
                                layer.global_scale.detach().cpu(), lay_r.geometry, rows=rows, chunk=512)
-    _check(y[:, :, rows.to(gpu)], exp, torch.bfloat16, "c2 sampled y")
+    _check(y[:, :, rows.to(y.device)], exp, dtype, what)
+    return y, core
+
+
+def test_full_size_headline_sampled(gpu):
+    """c2: 64^3 bf16, batch 1, raster: sampled rows vs the oracle."""
+    print("full size c2 sampled", flush=True)
+    shape = (64, 64, 64)
+    layer, x = _xavier_layer(shape, 1, torch.bfloat16, gpu)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    _core_sampled_vs_oracle(layer, x, lay, shape, "raster_block", torch.bfloat16, "c2 sampled y")
+
+
+def test_full_size_c1_sampled(gpu):
+    """c1: 16 x 64 x 64 bf16, batch 2, raster: sampled rows vs the oracle."""
+    print("full size c1 sampled", flush=True)
+    shape = (16, 64, 64)
+    layer, x = _xavier_layer(shape, 2, torch.bfloat16, gpu)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    _core_sampled_vs_oracle(layer, x, lay, shape, "raster_block", torch.bfloat16, "c1 sampled y")
+
+
+def test_full_size_c3_morton_repack(gpu):
+    """c3: 64^3 fp16 in Morton order: sampled rows vs the oracle, then a seeded
+    pure repack (block permutation + slot shuffle) must permute the core
+    output bit for bit."""
+    print("full size c3 morton + repack", flush=True)
+    shape = (64, 64, 64)
+    n = math.prod(shape)
+    layer, x = _xavier_layer(shape, 1, torch.float16, gpu)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="native_block_morton")
+    y, (q, kl, vl, kg, vg, gate, _) = _core_sampled_vs_oracle(layer, x, lay, shape, "native_block_morton",
+                                                              torch.float16, "c3 sampled y")
+    gen = torch.Generator().manual_seed(3)
+    fine = n // 64
+    slots = torch.argsort(torch.rand(fine, 64, generator=gen), dim=1)
+    p = (torch.randperm(fine, generator=gen)[:, None] * 64 + slots).reshape(-1)
+    other = lay.repack(p)
+    pg = p.to(gpu)
+    moved = [t[:, :, pg] for t in (q, kl, vl, kg, vg)]
+    with torch.no_grad():
+        yp = p3d.pack3d_hip_rope(*moved, layer.pool_weight, layer.slot_bias, gate[:, :, pg], layer.local_scale,
+                                 layer.global_scale, other.geometry, hip_axial(48, shape, other.coords))
+    assert torch.equal(yp, y[:, :, pg])
 
 
 @pytest.mark.parametrize("grid", [False, True])

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 2
+#define P3D_ABI_VERSION 3
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -180,6 +180,73 @@ int p3d_local_fwd_indexed(const p3d_attn_args* args, const int32_t* neighbors, i
 int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tokens,
                int32_t head_dim, int32_t dtype, const p3d_rope* rope, int32_t inverse, void* stream);
 
+/* ---- backward (replaces kernels.py:313-356, autograd.py:19-28) --------- */
+
+/* Shared argument block of the backward passes.  q and kl are the ROTATED
+ * inputs (the host rotates them once); sk / svt / lse / o_* are the forward's
+ * outputs.  Every buffer is caller-owned device memory; [B,H,N,D] buffers are
+ * contiguous unless given as a p3d_view. */
+typedef struct p3d_bwd_args {
+    int32_t batch, heads, kv_heads, tokens, head_dim, dtype;
+    int32_t summaries, gate_dtype;
+    int32_t parts;              /* p3d_mix_bwd: blocks, rows of dsl_part / dsg_part */
+    int32_t splits;             /* p3d_global_bwd: query splits of the summary dK/dV */
+    p3d_view q, kl, vl;         /* rotated q [B,H,N,D]; rotated kl, vl [B,G,N,D] */
+    p3d_view gate;              /* [B,H,N] of gate_dtype */
+    const float* local_scale;   /* [D] fp32 */
+    const float* global_scale;  /* [D] fp32 */
+    const void* sk;             /* [B,G,Mp,D] pooled keys times key_scale */
+    const void* svt;            /* [B,G,Mp/32,D,32] */
+    float key_scale;
+    int32_t pad_;
+    const void* o_local;        /* [B,H,N,D] saved o_L (dtype) */
+    const void* o_global;       /* [B,H,N,D] saved o_G (dtype) */
+    const float* lse_local;     /* [B,H,N] natural-log lse of the local softmax */
+    const float* lse_global;    /* [B,H,N] */
+    p3d_view dy;                /* upstream gradient [B,H,N,D] (dtype) */
+    void* dol;                  /* out of mix: dy * sl rounded (dtype) */
+    void* dog;                  /* out of mix: dy * gate * sg rounded (dtype) */
+    float* delta_local;         /* out of mix: [B,H,N] sum dO_L o_L */
+    float* delta_global;        /* out of mix: [B,H,N] sum dO_G o_G */
+    void* dgate;                /* out of mix: [B,H,N] of gate_dtype */
+    float* dsl_part;            /* out of mix: [parts, D] partial dsl */
+    float* dsg_part;            /* out of mix: [parts, D] partial dsg */
+    void* sv_rows;              /* workspace [B,G,Mp,D] (dtype) */
+    void* skt;                  /* workspace [B,G,Mp/32,D,32] (dtype) */
+    float* dq_local;            /* out: [B,H,N,D] fp32, rotated space */
+    float* dq_global;           /* out: [B,H,N,D] fp32, rotated space */
+    float* dk_local;            /* out: [B,G,N,D] fp32, rotated space */
+    void* dv_local;             /* out: [B,G,N,D] (dtype) */
+    float* dsk_part;            /* out: [splits,B,G,Mp,D] fp32, true key units */
+    float* dsv_part;            /* out: [splits,B,G,Mp,D] fp32 */
+} p3d_bwd_args;
+
+/* Fusion step (kernels.py:106-127): dO_L = round(dy sl), dO_G = round(dy gate
+ * sg), Delta_L = sum dO_L o_L, Delta_G = sum dO_G o_G, dgate = sum dy sg o_G,
+ * and per-block partial sums of dsl = sum dy o_L, dsg = sum dy gate o_G. */
+int p3d_mix_bwd(const p3d_bwd_args* args, void* stream);
+
+/* Local pathway backward for any validated graph (kernels.py:130-181): dq_local
+ * over the neighbour rows, dk_local / dv_local over the reverse adjacency. */
+int p3d_local_bwd_indexed(const p3d_bwd_args* args, const int32_t* neighbors, int32_t width,
+                          const int32_t* reverse, int32_t rwidth, void* stream);
+
+/* Summary pathway backward (kernels.py:184-237): dq_global and the split
+ * partials dsk_part / dsv_part (sv_rows and skt are filled first). */
+int p3d_global_bwd(const p3d_bwd_args* args, void* stream);
+
+/* dq = R^T round(round(dq_local) + round(dq_global)) and dkl = R^T round(dk_local)
+ * (kernels.py:202-206 rounding; R^T the inverse rotation of rope), both
+ * [B,*,N,D] contiguous in dtype. */
+int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, void* dq, void* dkl, void* stream);
+
+/* Pooling backward (kernels.py:240-270): from the split partials of dsk / dsv,
+ * writes dkg (gradient of the UNROTATED kg: R^T applied) and dvg, both
+ * [B,G,N,D] contiguous in dtype, and per-summary partials dw_part
+ * [B*G*Mp, D] and db_part [B*G*Mp, slots]. */
+int p3d_pool_bwd(const p3d_pool_args* pool, const float* dsk_part, const float* dsv_part, int32_t splits,
+                 void* dkg, void* dvg, float* dw_part, float* db_part, void* stream);
+
 /* ---- self-tests (no counterpart in the reference) ---------------------- */
 
 /* One MFMA of the kind the attention kernels issue for dtype (32x32x16 bf16 /
@@ -189,8 +256,8 @@ int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tok
  * matmul to pin that layout on the device. */
 int p3d_selftest_mfma(int32_t dtype, const void* a, const void* b, float* d, void* stream);
 
-/* sizeof of p3d_view, p3d_rope, p3d_pool_args, p3d_attn_args into out[4], so
- * a binding can check its struct mirrors. */
+/* sizeof of p3d_view, p3d_rope, p3d_pool_args, p3d_attn_args, p3d_bwd_args
+ * into out[5], so a binding can check its struct mirrors. */
 int p3d_struct_sizes(int64_t* out);
 
 #ifdef __cplusplus

@@ -22,7 +22,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 2  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 3  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -51,6 +51,20 @@ class AttnArgs(ctypes.Structure):
                 ("o_global", c_void_p)]
 
 
+class BwdArgs(ctypes.Structure):
+    _fields_ = [("batch", c_int32), ("heads", c_int32), ("kv_heads", c_int32), ("tokens", c_int32),
+                ("head_dim", c_int32), ("dtype", c_int32), ("summaries", c_int32), ("gate_dtype", c_int32),
+                ("parts", c_int32), ("splits", c_int32),
+                ("q", View), ("kl", View), ("vl", View), ("gate", View),
+                ("local_scale", c_void_p), ("global_scale", c_void_p), ("sk", c_void_p), ("svt", c_void_p),
+                ("key_scale", c_float), ("pad_", c_int32),
+                ("o_local", c_void_p), ("o_global", c_void_p), ("lse_local", c_void_p), ("lse_global", c_void_p),
+                ("dy", View), ("dol", c_void_p), ("dog", c_void_p), ("delta_local", c_void_p),
+                ("delta_global", c_void_p), ("dgate", c_void_p), ("dsl_part", c_void_p), ("dsg_part", c_void_p),
+                ("sv_rows", c_void_p), ("skt", c_void_p), ("dq_local", c_void_p), ("dq_global", c_void_p),
+                ("dk_local", c_void_p), ("dv_local", c_void_p), ("dsk_part", c_void_p), ("dsv_part", c_void_p)]
+
+
 _P = c_void_p
 SIGNATURES = {
     "p3d_last_error": ([], ctypes.c_char_p),
@@ -70,6 +84,11 @@ SIGNATURES = {
     "p3d_struct_sizes": ([_P], c_int32),
     "p3d_rotate": ([View, View, c_int32, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(Rope), c_int32, _P],
                    c_int32),
+    "p3d_mix_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
+    "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),
+    "p3d_global_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
+    "p3d_finish_bwd": ([ctypes.POINTER(BwdArgs), ctypes.POINTER(Rope), _P, _P, _P], c_int32),
+    "p3d_pool_bwd": ([ctypes.POINTER(PoolArgs), _P, _P, c_int32, _P, _P, _P, _P, _P], c_int32),
 }
 
 _lock = threading.Lock()

@@ -13,6 +13,7 @@ from __future__ import annotations
 import math
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from . import _lib
 from .rope import RopeSpec, identity_rope
@@ -202,15 +203,125 @@ def forward(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature
 
 
 class _Pack3DHip(torch.autograd.Function):
+    """First-order autograd of the core (autograd.py:8-28 of amilworks/Pack3D).
+
+    The forward saves the inputs, the summaries (sk, svt, norm slots), o_L,
+    o_G and the two log-sum-exps; nothing of size N x M.  The backward
+    refuses a geometry mutated since the forward.
+    """
+
     @staticmethod
     def forward(ctx, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope):
-        y, _ = forward(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope,
-                       save_state=False)
+        plan = ForwardPlan(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope,
+                           save_state=True)
+        y, saved = plan.run()
+        ctx.save_for_backward(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, saved["sk"], saved["svt"],
+                              plan.sk_norm_max, saved["o_local"], saved["o_global"], saved["lse_local"],
+                              saved["lse_global"])
+        ctx.geometry, ctx.temperature, ctx.rope, ctx.pool_rope = geometry, temperature, rope, pool_rope
+        ctx.key_scale = plan.key_scale
         return y
 
     @staticmethod
+    @once_differentiable
     def backward(ctx, dy):
-        raise NotImplementedError("the hip backward is not available yet")
+        ctx.geometry.check_unmodified()
+        grads = backward(dy, *ctx.saved_tensors, ctx.geometry, ctx.temperature, ctx.rope, ctx.pool_rope,
+                         ctx.key_scale)
+        return (*grads, None, None, None, None)
+
+
+def _mix_parts(rows):
+    return max(1, min(2048, -(-rows // 256)))
+
+
+def _splits(n, m, bg):
+    """Query splits of the summary dK/dV pass: enough workgroups to fill the
+    GPU, each split at least 1024 queries."""
+    blocks = -(-m // 128) * bg
+    return max(1, min(64, -(-2048 // blocks), -(-n // 1024)))
+
+
+def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm_max, o_local, o_global,
+             lse_local, lse_global, geometry, temperature, rope, pool_rope, key_scale):
+    """The ten gradients of the core (kernels.py:313-356 of amilworks/Pack3D):
+    dq, dkl, dkg with respect to the unrotated inputs (the rotation's backward
+    is fused), dvl, dvg, dweight, dbias, dgate, dsl, dsg."""
+    b, h, n, d = q.shape
+    g = kl.shape[1]
+    dev, dt = q.device, _lib.DTYPES[q.dtype]
+    f, slots = geometry.blocks.shape
+    m = geometry.num_summaries
+    mp = -(-m // 32) * 32
+    stream = _lib.stream_of(dev)
+    q, kl, vl, kg, vg = (_kernel_view(t) for t in (q, kl, vl, kg, vg))
+    dy = _kernel_view(dy if dy.dtype == q.dtype else dy.to(q.dtype))
+    keep = []
+    if rope.identity:
+        qr, klr = q, kl
+    else:
+        qr = torch.empty(q.shape, dtype=q.dtype, device=dev)
+        klr = torch.empty(kl.shape, dtype=kl.dtype, device=dev)
+        for src, dst, heads in ((q, qr, h), (kl, klr, g)):
+            _lib.call("p3d_rotate", _lib.view(src), _lib.view(dst), b, heads, n, d, dt, rope.struct(), 0, stream)
+    gate_k = gate if gate.dtype in _lib.DTYPES else gate.float()
+    sl32, sg32 = sl.detach().float().contiguous(), sg.detach().float().contiguous()
+    parts = _mix_parts(b * h * n)
+    splits = _splits(n, m, b * g)
+
+    def empty(*shape, dtype=q.dtype):
+        return torch.empty(*shape, dtype=dtype, device=dev)
+
+    f32 = torch.float32
+    bufs = dict(dol=empty(b, h, n, d), dog=empty(b, h, n, d), dl=empty(b, h, n, dtype=f32),
+                dg=empty(b, h, n, dtype=f32), dgate=empty(b, h, n, dtype=gate_k.dtype),
+                dslp=empty(parts, d, dtype=f32), dsgp=empty(parts, d, dtype=f32),
+                sv_rows=empty(b, g, mp, d), skt=empty(b, g, mp // 32, d, 32),
+                dql=empty(b, h, n, d, dtype=f32), dqg=empty(b, h, n, d, dtype=f32),
+                dkl=empty(b, g, n, d, dtype=f32), dvl=empty(b, g, n, d),
+                dskp=empty(splits, b, g, mp, d, dtype=f32), dsvp=empty(splits, b, g, mp, d, dtype=f32))
+    a = _lib.BwdArgs()
+    a.batch, a.heads, a.kv_heads, a.tokens, a.head_dim, a.dtype = b, h, g, n, d, dt
+    a.summaries, a.gate_dtype, a.parts, a.splits = m, _lib.DTYPES[gate_k.dtype], parts, splits
+    a.q, a.kl, a.vl, a.gate = _lib.view(qr), _lib.view(klr), _lib.view(vl), _lib.view3(gate_k)
+    a.local_scale, a.global_scale = sl32.data_ptr(), sg32.data_ptr()
+    a.sk, a.svt, a.key_scale = sk.data_ptr(), svt.data_ptr(), float(key_scale)
+    a.o_local, a.o_global = o_local.data_ptr(), o_global.data_ptr()
+    a.lse_local, a.lse_global = lse_local.data_ptr(), lse_global.data_ptr()
+    a.dy = _lib.view(dy)
+    a.dol, a.dog, a.delta_local, a.delta_global = (bufs[k].data_ptr() for k in ("dol", "dog", "dl", "dg"))
+    a.dgate, a.dsl_part, a.dsg_part = (bufs[k].data_ptr() for k in ("dgate", "dslp", "dsgp"))
+    a.sv_rows, a.skt = bufs["sv_rows"].data_ptr(), bufs["skt"].data_ptr()
+    a.dq_local, a.dq_global, a.dk_local = (bufs[k].data_ptr() for k in ("dql", "dqg", "dkl"))
+    a.dv_local, a.dsk_part, a.dsv_part = (bufs[k].data_ptr() for k in ("dvl", "dskp", "dsvp"))
+    keep += [qr, klr, gate_k, sl32, sg32, dy]
+
+    _lib.call("p3d_mix_bwd", a, stream)
+    nb, rev = geometry.neighbors, geometry.reverse_neighbors
+    _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)
+    _lib.call("p3d_global_bwd", a, stream)
+    dq = empty(b, h, n, d)
+    dkl = empty(b, g, n, d)
+    _lib.call("p3d_finish_bwd", a, rope.struct(), dq.data_ptr(), dkl.data_ptr(), stream)
+
+    w32 = weight.detach().float().contiguous()
+    b32 = bias.detach().float().contiguous()
+    pool_args = _lib.PoolArgs(b, g, n, d, dt, f, slots, geometry.pool_size, m, float(temperature), float(key_scale),
+                              _lib.view(kg), _lib.view(vg), geometry.blocks.data_ptr(), w32.data_ptr(),
+                              b32.data_ptr(), pool_rope.struct(), sk.data_ptr(), svt.data_ptr(),
+                              sk_norm_max.data_ptr())
+    dkg, dvg = empty(b, g, n, d), empty(b, g, n, d)
+    dwp = empty(b * g * mp, d, dtype=f32)
+    dbp = empty(b * g * mp, slots, dtype=f32)
+    _lib.call("p3d_pool_bwd", pool_args, bufs["dskp"].data_ptr(), bufs["dsvp"].data_ptr(), splits,
+              dkg.data_ptr(), dvg.data_ptr(), dwp.data_ptr(), dbp.data_ptr(), stream)
+    keep += [w32, b32]
+    dweight = dwp.sum(0).to(weight.dtype)
+    dbias = dbp.sum(0).to(bias.dtype)
+    dsl = bufs["dslp"].sum(0).to(sl.dtype)
+    dsg = bufs["dsgp"].sum(0).to(sg.dtype)
+    dgate = bufs["dgate"] if bufs["dgate"].dtype == gate.dtype else bufs["dgate"].to(gate.dtype)
+    return dq, dkl, bufs["dvl"], dkg, dvg, dweight, dbias, dgate, dsl, dsg
 
 
 def _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope):

@@ -1,0 +1,864 @@
+// PACK3D core backward: the vector-Jacobian product of
+// y = sl * o_L + gate * sg * o_G (reference.py:16-31 of amilworks/Pack3D),
+// split into the same passes as the reference's GPU backward
+// (backends/triton/kernels.py:106-356): the fusion step, local dQ, local
+// dK/dV through the reverse adjacency, global dQ, and global dK/dV in query
+// splits (reduced, with the pooling backward, in pool.hip).
+//
+// Rounding points follow the reference: dO_L = dy * sl and dO_G = dy * gate * sg
+// are rounded to the storage type before Delta is formed (kernels.py:118-120),
+// dS is rounded to the storage type before the global dQ / dK products, and
+// dQ = round(round(dQ_L) + round(dQ_G)) (kernels.py:202-206), rotated back
+// with R^T and rounded again (the rotation's own backward).
+//
+// All q / k inputs here are already rotated (the host rotates them once);
+// summary keys are stored times log2(e)/sqrt(d) as in the forward.
+#include "attn_common.hpp"
+
+namespace p3d {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct BwdDev {
+    int B, H, G, N, M, Mp;
+    int gate_dtype, parts, splits;
+    const char *q, *kl, *vl, *gate;
+    int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn, gsb, gsh, gsn;
+    const float *sl, *sg;
+    const char *sk, *svt;
+    float key_scale;
+    const char *o_l, *o_g;
+    const float *lse_l, *lse_g;
+    const char* dy;
+    int64_t dsb, dsh, dsn;
+    char *dol, *dog;
+    float *dl, *dg;
+    char* dgate;
+    float *dsl_part, *dsg_part;
+    char *sv_rows, *skt;
+    float *dq_l, *dq_g, *dk_l;
+    char* dv_l;
+    float *dsk_part, *dsv_part;
+};
+
+template <typename T>
+__device__ __forceinline__ const T* tp(const char* p) { return reinterpret_cast<const T*>(p); }
+
+template <typename T>
+__device__ __forceinline__ void store_piece(T* dst, const float* x) {
+    constexpr int N = Piece<T>::N;
+    uint4 raw;
+    T* v = reinterpret_cast<T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < N; ++e) v[e] = from_f32<T>(x[e]);
+    *reinterpret_cast<uint4*>(dst) = raw;
+}
+
+template <typename T>
+__device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
+
+// ------------------------------------------------------------------- fusion
+// dO_L, dO_G (rounded), Delta_L = sum dO_L o_L, Delta_G = sum dO_G o_G,
+// dgate = sum dy sg o_G, and per-block partial sums of dsl = sum dy o_L and
+// dsg = sum dy gate o_G (kernels.py:106-127).  LG lanes per row, one
+// 16-byte piece per lane; blocks stride over the rows.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_mix_bwd(BwdDev a) {
+    constexpr int EP = Piece<T>::N, PPR = D / EP;
+    constexpr int LG = PPR <= 2 ? 2 : (PPR <= 4 ? 4 : (PPR <= 8 ? 8 : (PPR <= 16 ? 16 : 32)));
+    static_assert(PPR <= 32, "a row must fit in half a wave");
+    constexpr int RPW = 64 / LG;
+    __shared__ float red[2][kWaves][D];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane % LG, grp = lane / LG;
+    const bool act = sub < PPR;
+    const int c0 = (act ? sub : 0) * EP;
+    float sl[EP], sg[EP], psl[EP], psg[EP];
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+        sl[e] = a.sl[c0 + e];
+        sg[e] = a.sg[c0 + e];
+        psl[e] = psg[e] = 0.f;
+    }
+    const int64_t rows = (int64_t)a.B * a.H * a.N;
+    const int64_t step = (int64_t)gridDim.x * kWaves * RPW;
+    for (int64_t r = ((int64_t)blockIdx.x * kWaves + wave) * RPW + grp; r < rows; r += step) {
+        const int64_t bh = r / a.N, n = r - bh * a.N;
+        const int b = (int)(bh / a.H), h = (int)(bh - (int64_t)b * a.H);
+        float dy[EP], ol[EP], og[EP];
+        load_piece<T>(tp<T>(a.dy) + b * a.dsb + h * a.dsh + n * a.dsn + c0, dy);
+        load_piece<T>(tp<T>(a.o_l) + r * D + c0, ol);
+        load_piece<T>(tp<T>(a.o_g) + r * D + c0, og);
+        const float gate = load_any(a.gate, b * a.gsb + h * a.gsh + n * a.gsn, a.gate_dtype);
+        float dol[EP], dog[EP], sdl = 0.f, sdg = 0.f, sgt = 0.f;
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+            dol[e] = round_to<T>(dy[e] * sl[e]);
+            dog[e] = round_to<T>(dy[e] * gate * sg[e]);
+            sdl += dol[e] * ol[e];
+            sdg += dog[e] * og[e];
+            sgt += dy[e] * og[e] * sg[e];
+            if (act) {
+                psl[e] += dy[e] * ol[e];
+                psg[e] += dy[e] * og[e] * gate;
+            }
+        }
+        if (act) {
+            store_piece<T>(reinterpret_cast<T*>(a.dol) + r * D + c0, dol);
+            store_piece<T>(reinterpret_cast<T*>(a.dog) + r * D + c0, dog);
+        }
+        if (!act) sdl = sdg = sgt = 0.f;
+#pragma unroll
+        for (int o = 1; o < LG; o <<= 1) {
+            sdl += __shfl_xor(sdl, o);
+            sdg += __shfl_xor(sdg, o);
+            sgt += __shfl_xor(sgt, o);
+        }
+        if (sub == 0) {
+            a.dl[r] = sdl;
+            a.dg[r] = sdg;
+            switch (a.gate_dtype) {
+                case P3D_F32: reinterpret_cast<float*>(a.dgate)[r] = sgt; break;
+                case P3D_F16: reinterpret_cast<_Float16*>(a.dgate)[r] = (_Float16)sgt; break;
+                default: reinterpret_cast<__bf16*>(a.dgate)[r] = (__bf16)sgt; break;
+            }
+        }
+    }
+    // Partial dsl / dsg of this block: over the row groups of each wave, then the waves.
+#pragma unroll
+    for (int o = LG; o < 64; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+            psl[e] += __shfl_xor(psl[e], o);
+            psg[e] += __shfl_xor(psg[e], o);
+        }
+    if (grp == 0 && act)
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+            red[0][wave][c0 + e] = psl[e];
+            red[1][wave][c0 + e] = psg[e];
+        }
+    __syncthreads();
+    for (int c = threadIdx.x; c < D; c += blockDim.x) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            s0 += red[0][w][c];
+            s1 += red[1][w][c];
+        }
+        a.dsl_part[(int64_t)blockIdx.x * D + c] = s0;
+        a.dsg_part[(int64_t)blockIdx.x * D + c] = s1;
+    }
+}
+
+// ------------------------------------------------------------ local (VALU)
+// Local dQ for one (batch, head, query row): recompute the local scores over
+// the neighbour row, P = exp(s - lse_L), dS = P (dO_L . v - Delta_L) / sqrt(d),
+// dQ = sum dS k (kernels.py:130-151).  Lanes own neighbour columns, then
+// channels.
+template <typename T>
+__global__ __launch_bounds__(64) void k_local_dq(BwdDev a, const int32_t* nb, int W, int D, float scale) {
+    __shared__ float qs[128], dos[128], dss[128];
+    __shared__ int ids[128];
+    const int lane = threadIdx.x;
+    const int64_t item = blockIdx.x;
+    const int64_t row = item % a.N, bh = item / a.N;
+    const int b = (int)(bh / a.H), h = (int)(bh % a.H), kvh = h / (a.H / a.G);
+    const T* q = tp<T>(a.q) + b * a.qsb + h * a.qsh + row * a.qsn;
+    const T* dol = tp<T>(a.dol) + (bh * a.N + row) * D;
+    for (int c = lane; c < D; c += 64) {
+        qs[c] = to_f32(q[c]);
+        dos[c] = to_f32(dol[c]);
+    }
+    const float lse = a.lse_l[bh * a.N + row], delta = a.dl[bh * a.N + row];
+    int idx[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int w = lane + 64 * j;
+        idx[j] = w < W ? nb[row * W + w] : -1;
+        ids[w] = idx[j];
+    }
+    __syncthreads();
+    const T* K = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
+    const T* V = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        float ds = 0.f;
+        if (idx[j] >= 0 && lse != -INFINITY) {
+            const T* k = K + idx[j] * a.ksn;
+            const T* v = V + idx[j] * a.vsn;
+            float s = 0.f, dp = 0.f;
+            for (int c = 0; c < D; ++c) {
+                s += qs[c] * to_f32(k[c]);
+                dp += dos[c] * to_f32(v[c]);
+            }
+            ds = expf(s * scale - lse) * (dp - delta) * scale;
+        }
+        dss[lane + 64 * j] = ds;
+    }
+    __syncthreads();
+    float* dq = a.dq_l + (bh * a.N + row) * D;
+    for (int c = lane; c < D; c += 64) {
+        float acc = 0.f;
+        for (int w = 0; w < W; ++w) {
+            const int t = ids[w];
+            if (t >= 0) acc += dss[w] * to_f32(K[t * a.ksn + c]);
+        }
+        dq[c] = acc;
+    }
+}
+
+// Local dK, dV for one (batch, kv head, key row j): the queries that list j
+// come from the reverse adjacency; every query head of the kv group
+// contributes (kernels.py:154-181).
+template <typename T>
+__global__ __launch_bounds__(64) void k_local_dkv(BwdDev a, const int32_t* rev, int RW, int D, float scale) {
+    __shared__ float ks[128], vs[128], ps[128], dss[128];
+    __shared__ int ids[128];
+    const int lane = threadIdx.x;
+    const int64_t item = blockIdx.x;
+    const int64_t row = item % a.N, bg = item / a.N;
+    const int b = (int)(bg / a.G), g = (int)(bg % a.G), rep = a.H / a.G;
+    const T* k = tp<T>(a.kl) + b * a.ksb + g * a.ksh + row * a.ksn;
+    const T* v = tp<T>(a.vl) + b * a.vsb + g * a.vsh + row * a.vsn;
+    for (int c = lane; c < D; c += 64) {
+        ks[c] = to_f32(k[c]);
+        vs[c] = to_f32(v[c]);
+    }
+    int idx[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int w = lane + 64 * j;
+        idx[j] = w < RW ? rev[row * RW + w] : -1;
+        ids[w] = idx[j];
+    }
+    float dk[2] = {0.f, 0.f}, dv[2] = {0.f, 0.f};
+    for (int hh = 0; hh < rep; ++hh) {
+        const int h = g * rep + hh;
+        const int64_t bh = (int64_t)b * a.H + h;
+        const T* Q = tp<T>(a.q) + b * a.qsb + h * a.qsh;
+        const T* DO = tp<T>(a.dol) + bh * a.N * D;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float p = 0.f, ds = 0.f;
+            const int i = idx[j];
+            if (i >= 0) {
+                const float lse = a.lse_l[bh * a.N + i];
+                if (lse != -INFINITY) {
+                    float s = 0.f, dp = 0.f;
+                    for (int c = 0; c < D; ++c) {
+                        s += to_f32(Q[i * a.qsn + c]) * ks[c];
+                        dp += to_f32(DO[(int64_t)i * D + c]) * vs[c];
+                    }
+                    p = expf(s * scale - lse);
+                    ds = p * (dp - a.dl[bh * a.N + i]) * scale;
+                }
+            }
+            ps[lane + 64 * j] = p;
+            dss[lane + 64 * j] = ds;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const int c = lane + 64 * cc;
+            if (c >= D) continue;
+            for (int w = 0; w < RW; ++w) {
+                const int i = ids[w];
+                if (i >= 0) {
+                    dk[cc] += dss[w] * to_f32(Q[i * a.qsn + c]);
+                    dv[cc] += ps[w] * to_f32(DO[(int64_t)i * D + c]);
+                }
+            }
+        }
+    }
+    float* dko = a.dk_l + (bg * a.N + row) * D;
+    T* dvo = reinterpret_cast<T*>(a.dv_l) + (bg * a.N + row) * D;
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+        const int c = lane + 64 * cc;
+        if (c < D) {
+            dko[c] = dk[cc];
+            dvo[c] = from_f32<T>(dv[cc]);
+        }
+    }
+}
+
+// ------------------------------------------------------------ summaries
+// sv rows [B,G,Mp,D] from svt, and skt [B,G,Mp/32,D,32] from sk (both the
+// storage type; tiny).
+template <typename T>
+__global__ void k_summary_transpose(BwdDev a, int D) {
+    const int64_t total = (int64_t)a.B * a.G * a.Mp * D;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= total) return;
+    const int c = (int)(e % D);
+    const int64_t bm = e / D;  // bg * Mp + m
+    const int m = (int)(bm % a.Mp);
+    const int64_t bg = bm / a.Mp;
+    const int64_t t_off = ((bg * (a.Mp / 32) + m / 32) * D + c) * 32 + (m & 31);
+    reinterpret_cast<T*>(a.sv_rows)[e] = tp<T>(a.svt)[t_off];
+    reinterpret_cast<T*>(a.skt)[t_off] = tp<T>(a.sk)[e];
+}
+
+// Stages of SK summaries (64, or 32 when two stages of 64 would not fit in
+// LDS) for the global dQ pass: sk rows and sv rows (row stride KSTR) and sk
+// transposed (row stride SK + EP, zero padding rows up to 32 * MB),
+// double-buffered through registers.
+template <typename C, int SK>
+struct DqStage {
+    typedef typename C::T_ T;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int TGS = SK + EP;
+    static constexpr int RPIECES = SK * (C::D / EP);   // per row tensor
+    static constexpr int TPIECES = C::D * (SK / EP);   // transposed
+    static constexpr int RI = (RPIECES + 64 * kWaves - 1) / (64 * kWaves);
+    static constexpr int TI = (TPIECES + 64 * kWaves - 1) / (64 * kWaves);
+    static constexpr int SIZE = 2 * SK * C::KSTR + 32 * C::MB * TGS;  // elements
+    uint4 k[RI], v[RI], t[TI];
+
+    __device__ __forceinline__ void load(const BwdDev& a, int64_t bg, int base) {
+        const int limit = min(SK, a.Mp - base) * C::D;
+        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
+        const T* sv = tp<T>(a.sv_rows) + ((int64_t)bg * a.Mp + base) * C::D;
+        const T* skt = tp<T>(a.skt) + ((int64_t)bg * a.Mp + base) * C::D;
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
+            k[i] = off < limit ? *reinterpret_cast<const uint4*>(sk + off) : uint4{0, 0, 0, 0};
+            v[i] = off < limit ? *reinterpret_cast<const uint4*>(sv + off) : uint4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
+            t[i] = off < limit ? *reinterpret_cast<const uint4*>(skt + off) : uint4{0, 0, 0, 0};
+        }
+    }
+
+    __device__ __forceinline__ void store(T* stage) const {
+#pragma unroll
+        for (int i = 0; i < RI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            if (p < RPIECES) {
+                const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
+                *reinterpret_cast<uint4*>(stage + r * C::KSTR + c) = k[i];
+                *reinterpret_cast<uint4*>(stage + SK * C::KSTR + r * C::KSTR + c) = v[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            if (p < TPIECES) {
+                const int tt = p / (C::D * (32 / EP));
+                const int rem = p - tt * C::D * (32 / EP);
+                const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
+                *reinterpret_cast<uint4*>(stage + 2 * SK * C::KSTR + ch * TGS + 32 * tt + kk) = t[i];
+            }
+        }
+    }
+};
+
+// Stage depth: 64 rows when two stages fit in the 160 KiB of LDS, else 32.
+template <typename C, template <typename, int> class Stage>
+constexpr int stage_rows() {
+    return 2 * Stage<C, 64>::SIZE * (int)sizeof(typename C::T_) <= 160 * 1024 ? 64 : 32;
+}
+
+// Zero rows [D, 32 * MB) of a transposed buffer (rows of `stride` elements).
+template <typename C>
+__device__ __forceinline__ void zero_padding_rows(typename C::T_* buf, int stride, int cols) {
+    const int rows = 32 * C::MB - C::D;
+    for (int i = threadIdx.x; i < rows * cols; i += blockDim.x) {
+        const int r = i / cols, c = i - r * cols;
+        buf[(C::D + r) * stride + c] = from_f32<typename C::T_>(0.f);
+    }
+}
+
+// Fragments of one lane's row (query or key) for the score MFMAs, no rotation.
+template <typename C>
+__device__ __forceinline__ void load_row_frags(const typename C::T_* row, bool valid, int g, typename C::Frag* f) {
+    typedef typename C::T_ T;
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t) {
+        if constexpr (C::E == 8) {
+            f[t] = valid ? frag_load16<T>(row + t * C::KS + 8 * g) : frag_fill<T>(0.f);
+        } else {
+            f[t] = valid ? row[t * C::KS + g] : 0.f;
+        }
+    }
+}
+
+// Global dQ: per query, over all summaries, S = q . sk (log2 units), P =
+// 2^(S - lse_G log2 e), dP = dO_G . sv, dS = P (dP - Delta_G), dQ = ln 2 *
+// sum dS sk_stored (sk_stored = sk log2(e)/sqrt(d), so ln 2 * sk_stored =
+// sk / sqrt(d)) (kernels.py:184-206).  Transposed tiles as in the forward:
+// lane = query; dS feeds the dQ^T = sk^T dS^T MFMA as its B operand.
+template <typename T, int D>
+__global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
+    typedef Cfg<T, D> C;
+    constexpr int SK = stage_rows<C, DqStage>();
+    typedef DqStage<C, SK> S;
+    extern __shared__ __align__(16) unsigned char smem[];
+    T* lds = reinterpret_cast<T*>(smem);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, qi = lane & 31;
+    const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.G);
+    const int64_t bg = (int64_t)b * a.G + kvh;
+
+    typename C::Frag qf[2][C::NT], df[2][C::NT];
+    int64_t qrow[2];
+    bool qok[2];
+    float lse2[2], delta[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int64_t row = (int64_t)blockIdx.x * 64 * kWaves + 64 * wave + 32 * nb + qi;
+        qok[nb] = row < a.N;
+        qrow[nb] = qok[nb] ? row : 0;
+        load_row_frags<C>(tp<T>(a.q) + b * a.qsb + h * a.qsh + qrow[nb] * a.qsn, qok[nb], g, qf[nb]);
+        load_row_frags<C>(tp<T>(a.dog) + ((int64_t)bh * a.N + qrow[nb]) * D, qok[nb], g, df[nb]);
+        lse2[nb] = qok[nb] ? a.lse_g[(int64_t)bh * a.N + qrow[nb]] * kLog2e : INFINITY;
+        delta[nb] = qok[nb] ? a.dg[(int64_t)bh * a.N + qrow[nb]] : 0.f;
+    }
+    f32x16 acc[2][C::MB];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[nb][mb][r] = 0.f;
+
+    zero_padding_rows<C>(lds + 2 * SK * C::KSTR, S::TGS, SK);
+    zero_padding_rows<C>(lds + S::SIZE + 2 * SK * C::KSTR, S::TGS, SK);
+    S regs;
+    regs.load(a, bg, 0);
+    regs.store(lds);
+    __syncthreads();
+    int buf = 0;
+    for (int base = 0; base < a.M; base += SK) {
+        const int next = base + SK;
+        if (next < a.M) regs.load(a, bg, next);
+        const T* cur = lds + buf * S::SIZE;
+#pragma unroll
+        for (int tt = 0; tt < SK / 32; ++tt) {
+            const int first = base + 32 * tt;
+            if (first >= a.M) break;
+            typename C::Frag kf[C::NT], vf[C::NT], tf[C::MB * C::KSTEPS];
+            load_kfrags<C>(cur + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, kf);
+            load_kfrags<C>(cur + SK * C::KSTR + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, vf);
+            load_vfrags<C, true>(cur + 2 * SK * C::KSTR, S::TGS, 32 * tt, lane, tf);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const f32x16 s = score_tile<C>(kf, qf[nb]);
+                const f32x16 dp = score_tile<C>(vf, df[nb]);
+                float ds[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const bool live = first + kperm<C::E, C::KS>(acc_row(r, g)) < a.M;
+                    // One summary: P = 1 and dS = 0 exactly (kernels.py:198-199).
+                    ds[r] = (live && a.M > 1) ? __builtin_amdgcn_exp2f(s[r] - lse2[nb]) * (dp[r] - delta[nb]) : 0.f;
+                }
+#pragma unroll
+                for (int ks = 0; ks < C::KSTEPS; ++ks) {
+                    const typename C::Frag pf = frag_from_p<T>(ds, ks);
+#pragma unroll
+                    for (int mb = 0; mb < C::MB; ++mb)
+                        acc[nb][mb] = C::M::mfma(tf[mb * C::KSTEPS + ks], pf, acc[nb][mb]);
+                }
+            }
+        }
+        if (next < a.M) regs.store(lds + (buf ^ 1) * S::SIZE);
+        __syncthreads();
+        buf ^= 1;
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        if (!qok[nb]) continue;
+        float* dq = a.dq_g + ((int64_t)bh * a.N + qrow[nb]) * D;
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int c = 32 * mb + acc_row(r, g);
+                if (c < D) dq[c] = acc[nb][mb][r] * kLn2;
+            }
+    }
+}
+
+// Query stages of SK rows (64, or 32 when two stages of 64 would not fit in
+// LDS) for the global dK/dV pass: q and dO_G rows (row stride KSTR), q and
+// dO_G transposed (row stride SK + EP, zero padding rows), and lse_G (log2
+// units; +inf past the last query) and Delta_G.
+template <typename C, int SK>
+struct KvStage {
+    typedef typename C::T_ T;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int PPR = C::D / EP;
+    static constexpr int TGS = SK + EP;
+    static constexpr int PIECES = SK * PPR;
+    static constexpr int PI = (PIECES + 64 * kWaves - 1) / (64 * kWaves);
+    static constexpr int ROWS = 2 * SK * C::KSTR;                 // q rows, dO rows
+    static constexpr int TRANS = 2 * 32 * C::MB * TGS;            // q^T, dO^T
+    static constexpr int SIZE = ROWS + TRANS + 2 * SK * (int)(sizeof(float) / sizeof(T));  // + lse, delta
+    uint4 q[PI], d[PI];
+    float lse, delta;
+
+    __device__ __forceinline__ void load(const BwdDev& a, int b, int h, int64_t base) {
+        const int64_t bh = (int64_t)b * a.H + h;
+#pragma unroll
+        for (int i = 0; i < PI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            const int r = p / PPR, c = (p - r * PPR) * EP;
+            const int64_t row = base + r;
+            q[i] = d[i] = uint4{0, 0, 0, 0};
+            if (p < PIECES && row < a.N) {
+                q[i] = *reinterpret_cast<const uint4*>(tp<T>(a.q) + b * a.qsb + h * a.qsh + row * a.qsn + c);
+                d[i] = *reinterpret_cast<const uint4*>(tp<T>(a.dog) + (bh * a.N + row) * C::D + c);
+            }
+        }
+        if (threadIdx.x < SK) {
+            const int64_t row = base + threadIdx.x;
+            lse = row < a.N ? a.lse_g[bh * a.N + row] * kLog2e : INFINITY;
+            delta = row < a.N ? a.dg[bh * a.N + row] : 0.f;
+        }
+    }
+
+    __device__ __forceinline__ void store(T* stage) const {
+        T* qt = stage + ROWS;
+        T* dt = qt + 32 * C::MB * TGS;
+#pragma unroll
+        for (int i = 0; i < PI; ++i) {
+            const int p = threadIdx.x + i * 64 * kWaves;
+            if (p < PIECES) {
+                const int r = p / PPR, c = (p - r * PPR) * EP;
+                *reinterpret_cast<uint4*>(stage + r * C::KSTR + c) = q[i];
+                *reinterpret_cast<uint4*>(stage + SK * C::KSTR + r * C::KSTR + c) = d[i];
+                const T* qv = reinterpret_cast<const T*>(&q[i]);
+                const T* dv = reinterpret_cast<const T*>(&d[i]);
+#pragma unroll
+                for (int e = 0; e < EP; ++e) {
+                    qt[(c + e) * TGS + r] = qv[e];
+                    dt[(c + e) * TGS + r] = dv[e];
+                }
+            }
+        }
+        if (threadIdx.x < SK) {
+            float* f = reinterpret_cast<float*>(stage + ROWS + TRANS);
+            f[threadIdx.x] = lse;
+            f[SK + threadIdx.x] = delta;
+        }
+    }
+};
+
+// Global dK / dV of the summaries (kernels.py:209-237): lane = summary (a
+// wave owns 32), queries streamed in stages of 64 over this split's range of
+// every query head of the kv group.  S[q][key] = q . sk (log2 units) with the
+// key fragments resident as the B operand; P = 2^(S - lse log2 e); dP = dO .
+// sv; dS = P (dP - Delta); dK^T += q^T dS, dV^T += dO^T P (dS and P enter as
+// B operands).  Writes fp32 partials [split][bg][m][D]; dK is in true units
+// (divided by sqrt(d)), before the pooling's 1/count.
+template <typename T, int D>
+__global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
+    typedef Cfg<T, D> C;
+    constexpr int SK = stage_rows<C, KvStage>();
+    typedef KvStage<C, SK> S;
+    extern __shared__ __align__(16) unsigned char smem[];
+    T* lds = reinterpret_cast<T*>(smem);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, qi = lane & 31;
+    const int split = blockIdx.y;
+    const int64_t bg = blockIdx.z;
+    const int b = (int)(bg / a.G), kvh = (int)(bg % a.G), rep = a.H / a.G;
+    const int key = blockIdx.x * 32 * kWaves + 32 * wave + qi;
+    const bool kok = key < a.M;
+
+    typename C::Frag kf[C::NT], vf[C::NT];
+    load_row_frags<C>(tp<T>(a.sk) + (bg * a.Mp + (kok ? key : 0)) * D, kok, g, kf);
+    load_row_frags<C>(tp<T>(a.sv_rows) + (bg * a.Mp + (kok ? key : 0)) * D, kok, g, vf);
+    f32x16 acck[C::MB], accv[C::MB];
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acck[mb][r] = accv[mb][r] = 0.f;
+
+    const int64_t per = cdiv(cdiv((int64_t)a.N, SK), a.splits) * SK;  // queries per split
+    const int64_t q0 = split * per, q1 = min((int64_t)a.N, q0 + per);
+    zero_padding_rows<C>(lds + S::ROWS, S::TGS, SK);
+    zero_padding_rows<C>(lds + S::ROWS + 32 * C::MB * S::TGS, S::TGS, SK);
+    zero_padding_rows<C>(lds + S::SIZE + S::ROWS, S::TGS, SK);
+    zero_padding_rows<C>(lds + S::SIZE + S::ROWS + 32 * C::MB * S::TGS, S::TGS, SK);
+    const int64_t stages = q1 > q0 ? cdiv(q1 - q0, SK) : 0;
+    const int64_t total = stages * rep;
+    if (total > 0) {
+        S regs;
+        regs.load(a, b, kvh * rep, q0);
+        regs.store(lds);
+        __syncthreads();
+        int buf = 0;
+        for (int64_t it = 0; it < total; ++it) {
+            const int64_t nx = it + 1;
+            if (nx < total) regs.load(a, b, kvh * rep + (int)(nx / stages), q0 + (nx % stages) * SK);
+            const T* cur = lds + buf * S::SIZE;
+            const float* lse = reinterpret_cast<const float*>(cur + S::ROWS + S::TRANS);
+            const float* dlt = lse + SK;
+#pragma unroll
+            for (int tt = 0; tt < SK / 32; ++tt) {
+                typename C::Frag qa[C::NT], da[C::NT], qt[C::MB * C::KSTEPS], dt[C::MB * C::KSTEPS];
+                load_kfrags<C>(cur + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, qa);
+                load_kfrags<C>(cur + SK * C::KSTR + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, da);
+                load_vfrags<C, true>(cur + S::ROWS, S::TGS, 32 * tt, lane, qt);
+                load_vfrags<C, true>(cur + S::ROWS + 32 * C::MB * S::TGS, S::TGS, 32 * tt, lane, dt);
+                // Register r of lane group g holds query kperm(acc_row(r, g)) of the tile.
+                f32x16 init;
+                float dl[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int qq = 32 * tt + kperm<C::E, C::KS>(acc_row(r, g));
+                    init[r] = -lse[qq];
+                    dl[r] = dlt[qq];
+                }
+                const f32x16 s = score_tile<C>(qa, kf, init);
+                const f32x16 dp = score_tile<C>(da, vf);
+                float p[16], ds[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    p[r] = __builtin_amdgcn_exp2f(s[r]);
+                    ds[r] = a.M > 1 ? p[r] * (dp[r] - dl[r]) : 0.f;  // kernels.py:230-233
+                }
+#pragma unroll
+                for (int ks = 0; ks < C::KSTEPS; ++ks) {
+                    const typename C::Frag dsf = frag_from_p<T>(ds, ks);
+                    const typename C::Frag pf = frag_from_p<T>(p, ks);
+#pragma unroll
+                    for (int mb = 0; mb < C::MB; ++mb) {
+                        acck[mb] = C::M::mfma(qt[mb * C::KSTEPS + ks], dsf, acck[mb]);
+                        accv[mb] = C::M::mfma(dt[mb * C::KSTEPS + ks], pf, accv[mb]);
+                    }
+                }
+            }
+            if (nx < total) regs.store(lds + (buf ^ 1) * S::SIZE);
+            __syncthreads();
+            buf ^= 1;
+        }
+    }
+    if (!kok) return;
+    const float inv_sqrt_d = 1.f / sqrtf((float)D);
+    float* dk = a.dsk_part + (((int64_t)split * a.B * a.G + bg) * a.Mp + key) * D;
+    float* dv = a.dsv_part + (((int64_t)split * a.B * a.G + bg) * a.Mp + key) * D;
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int c = 32 * mb + acc_row(r, g);
+            if (c < D) {
+                dk[c] = acck[mb][r] * inv_sqrt_d;
+                dv[c] = accv[mb][r];
+            }
+        }
+}
+
+// ------------------------------------------------------------------ finish
+// dQ = R^T round(round(dQ_L) + round(dQ_G)) and dK_L = R^T round(dK_L), each
+// rounded to the storage type; one 16-byte piece per thread.
+template <typename T>
+__global__ void k_finish_bwd(BwdDev a, RopeDev rope, int D, T* dq, T* dkl) {
+    constexpr int EP = Piece<T>::N;
+    const int ppr = D / EP;
+    const int64_t qpieces = (int64_t)a.B * a.H * a.N * ppr;
+    const int64_t kpieces = (int64_t)a.B * a.G * a.N * ppr;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= qpieces + kpieces) return;
+    const bool isq = e < qpieces;
+    const int64_t pe = isq ? e : e - qpieces;
+    const int piece = (int)(pe % ppr);
+    const int64_t row = pe / ppr;  // (b, head) * N + n
+    const int64_t n = row % a.N;
+    float x[EP];
+    const int64_t off = row * D + piece * EP;
+#pragma unroll
+    for (int i = 0; i < EP; ++i) {
+        x[i] = isq ? round_to<T>(round_to<T>(a.dq_l[off + i]) + round_to<T>(a.dq_g[off + i]))
+                   : round_to<T>(a.dk_l[off + i]);
+    }
+    int64_t pos[3];
+    rope_position(rope, n, pos);
+    rope_apply(rope, pos, piece * EP, x, EP, true);
+    store_piece<T>((isq ? dq : dkl) + off, x);
+}
+
+int fill_bwd(const p3d_bwd_args& x, BwdDev& d) {
+    const int es = dtype_size(x.dtype);
+    P3D_REQUIRE(x.dtype >= P3D_F32 && x.dtype <= P3D_BF16, "unknown dtype");
+    P3D_REQUIRE(x.head_dim == 16 || x.head_dim == 32 || x.head_dim == 48 || x.head_dim == 64 || x.head_dim == 128,
+                "head_dim must be 16, 32, 48, 64 or 128");
+    P3D_REQUIRE(x.batch >= 1 && x.heads >= 1 && x.kv_heads >= 1 && x.heads % x.kv_heads == 0 && x.tokens >= 1,
+                "bad batch/head/token counts");
+    P3D_REQUIRE(x.summaries >= 1, "need at least one summary");
+    P3D_REQUIRE(view_ok(x.q, es) && view_ok(x.kl, es) && view_ok(x.vl, es) && view_ok(x.dy, es),
+                "q/k/v/dy rows must be 16-byte aligned");
+    d = BwdDev{};
+    d.B = x.batch, d.H = x.heads, d.G = x.kv_heads, d.N = x.tokens, d.M = x.summaries;
+    d.Mp = (int)cdiv(x.summaries, 32) * 32;
+    d.gate_dtype = x.gate_dtype, d.parts = x.parts, d.splits = x.splits;
+    d.q = (const char*)x.q.data, d.qsb = x.q.sb, d.qsh = x.q.sh, d.qsn = x.q.sn;
+    d.kl = (const char*)x.kl.data, d.ksb = x.kl.sb, d.ksh = x.kl.sh, d.ksn = x.kl.sn;
+    d.vl = (const char*)x.vl.data, d.vsb = x.vl.sb, d.vsh = x.vl.sh, d.vsn = x.vl.sn;
+    d.gate = (const char*)x.gate.data, d.gsb = x.gate.sb, d.gsh = x.gate.sh, d.gsn = x.gate.sn;
+    d.sl = x.local_scale, d.sg = x.global_scale;
+    d.sk = (const char*)x.sk, d.svt = (const char*)x.svt;
+    d.key_scale = x.key_scale;
+    d.o_l = (const char*)x.o_local, d.o_g = (const char*)x.o_global;
+    d.lse_l = x.lse_local, d.lse_g = x.lse_global;
+    d.dy = (const char*)x.dy.data, d.dsb = x.dy.sb, d.dsh = x.dy.sh, d.dsn = x.dy.sn;
+    d.dol = (char*)x.dol, d.dog = (char*)x.dog;
+    d.dl = x.delta_local, d.dg = x.delta_global;
+    d.dgate = (char*)x.dgate;
+    d.dsl_part = x.dsl_part, d.dsg_part = x.dsg_part;
+    d.sv_rows = (char*)x.sv_rows, d.skt = (char*)x.skt;
+    d.dq_l = x.dq_local, d.dq_g = x.dq_global, d.dk_l = x.dk_local;
+    d.dv_l = (char*)x.dv_local;
+    d.dsk_part = x.dsk_part, d.dsv_part = x.dsv_part;
+    return P3D_OK;
+}
+
+template <typename C>
+size_t lds_dq() {
+    return (size_t)2 * DqStage<C, stage_rows<C, DqStage>()>::SIZE * sizeof(typename C::T_);
+}
+
+template <typename C>
+size_t lds_dkv() {
+    return (size_t)2 * KvStage<C, stage_rows<C, KvStage>()>::SIZE * sizeof(typename C::T_);
+}
+
+template <int D>
+void launch_mix(const BwdDev& d, int dtype, hipStream_t s) {
+    switch (dtype) {
+        case P3D_F32: k_mix_bwd<float, D><<<d.parts, 64 * kWaves, 0, s>>>(d); break;
+        case P3D_F16: k_mix_bwd<_Float16, D><<<d.parts, 64 * kWaves, 0, s>>>(d); break;
+        default: k_mix_bwd<__bf16, D><<<d.parts, 64 * kWaves, 0, s>>>(d); break;
+    }
+}
+
+template <int D>
+void launch_dq(const BwdDev& d, int dtype, hipStream_t s) {
+    const dim3 grid((unsigned)cdiv(d.N, 64 * kWaves), (unsigned)(d.B * d.H));
+    switch (dtype) {
+        case P3D_F32: k_global_dq<float, D><<<grid, 64 * kWaves, lds_dq<Cfg<float, D>>(), s>>>(d); break;
+        case P3D_F16: k_global_dq<_Float16, D><<<grid, 64 * kWaves, lds_dq<Cfg<_Float16, D>>(), s>>>(d); break;
+        default: k_global_dq<__bf16, D><<<grid, 64 * kWaves, lds_dq<Cfg<__bf16, D>>(), s>>>(d); break;
+    }
+}
+
+template <int D>
+void launch_dkv(const BwdDev& d, int dtype, hipStream_t s) {
+    const dim3 grid((unsigned)cdiv(d.M, 32 * kWaves), (unsigned)d.splits, (unsigned)(d.B * d.G));
+    switch (dtype) {
+        case P3D_F32: k_global_dkv<float, D><<<grid, 64 * kWaves, lds_dkv<Cfg<float, D>>(), s>>>(d); break;
+        case P3D_F16: k_global_dkv<_Float16, D><<<grid, 64 * kWaves, lds_dkv<Cfg<_Float16, D>>(), s>>>(d); break;
+        default: k_global_dkv<__bf16, D><<<grid, 64 * kWaves, lds_dkv<Cfg<__bf16, D>>(), s>>>(d); break;
+    }
+}
+
+#define P3D_BWD_DISPATCH(FN, D_, ...)                      \
+    switch (D_) {                                          \
+        case 16: FN<16>(__VA_ARGS__); break;               \
+        case 32: FN<32>(__VA_ARGS__); break;               \
+        case 48: FN<48>(__VA_ARGS__); break;               \
+        case 64: FN<64>(__VA_ARGS__); break;               \
+        default: FN<128>(__VA_ARGS__); break;              \
+    }
+
+}  // namespace
+}  // namespace p3d
+
+using namespace p3d;
+
+extern "C" int p3d_mix_bwd(const p3d_bwd_args* args, void* stream) {
+    P3D_REQUIRE(args, "null args");
+    BwdDev d;
+    if (int rc = fill_bwd(*args, d)) return rc;
+    P3D_REQUIRE(args->parts >= 1, "parts must be positive");
+    P3D_REQUIRE(args->o_local && args->o_global && args->gate.data && args->local_scale && args->global_scale &&
+                    args->dol && args->dog && args->delta_local && args->delta_global && args->dgate &&
+                    args->dsl_part && args->dsg_part,
+                "null pointer argument");
+    P3D_BWD_DISPATCH(launch_mix, args->head_dim, d, args->dtype, as_stream(stream));
+    return check_launch("p3d_mix_bwd");
+}
+
+extern "C" int p3d_local_bwd_indexed(const p3d_bwd_args* args, const int32_t* neighbors, int32_t width,
+                                     const int32_t* reverse, int32_t rwidth, void* stream) {
+    P3D_REQUIRE(args, "null args");
+    BwdDev d;
+    if (int rc = fill_bwd(*args, d)) return rc;
+    P3D_REQUIRE(neighbors && reverse && width >= 1 && width <= 128 && rwidth >= 1 && rwidth <= 128,
+                "neighbour tables must have 1..128 columns");
+    P3D_REQUIRE(args->dol && args->lse_local && args->delta_local && args->dq_local && args->dk_local &&
+                    args->dv_local,
+                "null pointer argument");
+    const float scale = 1.f / sqrtf((float)args->head_dim);
+    const unsigned qitems = (unsigned)((int64_t)d.B * d.H * d.N);
+    const unsigned kitems = (unsigned)((int64_t)d.B * d.G * d.N);
+    hipStream_t s = as_stream(stream);
+    switch (args->dtype) {
+        case P3D_F32:
+            k_local_dq<float><<<qitems, 64, 0, s>>>(d, neighbors, width, args->head_dim, scale);
+            k_local_dkv<float><<<kitems, 64, 0, s>>>(d, reverse, rwidth, args->head_dim, scale);
+            break;
+        case P3D_F16:
+            k_local_dq<_Float16><<<qitems, 64, 0, s>>>(d, neighbors, width, args->head_dim, scale);
+            k_local_dkv<_Float16><<<kitems, 64, 0, s>>>(d, reverse, rwidth, args->head_dim, scale);
+            break;
+        default:
+            k_local_dq<__bf16><<<qitems, 64, 0, s>>>(d, neighbors, width, args->head_dim, scale);
+            k_local_dkv<__bf16><<<kitems, 64, 0, s>>>(d, reverse, rwidth, args->head_dim, scale);
+            break;
+    }
+    return check_launch("p3d_local_bwd_indexed");
+}
+
+extern "C" int p3d_global_bwd(const p3d_bwd_args* args, void* stream) {
+    P3D_REQUIRE(args, "null args");
+    BwdDev d;
+    if (int rc = fill_bwd(*args, d)) return rc;
+    P3D_REQUIRE(args->splits >= 1, "splits must be positive");
+    P3D_REQUIRE(args->sk && args->svt && args->sv_rows && args->skt && args->dog && args->lse_global &&
+                    args->delta_global && args->dq_global && args->dsk_part && args->dsv_part,
+                "null pointer argument");
+    hipStream_t s = as_stream(stream);
+    const int64_t te = (int64_t)d.B * d.G * d.Mp * args->head_dim;
+    switch (args->dtype) {
+        case P3D_F32: k_summary_transpose<float><<<(unsigned)cdiv(te, 256), 256, 0, s>>>(d, args->head_dim); break;
+        case P3D_F16: k_summary_transpose<_Float16><<<(unsigned)cdiv(te, 256), 256, 0, s>>>(d, args->head_dim); break;
+        default: k_summary_transpose<__bf16><<<(unsigned)cdiv(te, 256), 256, 0, s>>>(d, args->head_dim); break;
+    }
+    P3D_BWD_DISPATCH(launch_dq, args->head_dim, d, args->dtype, s);
+    P3D_BWD_DISPATCH(launch_dkv, args->head_dim, d, args->dtype, s);
+    return check_launch("p3d_global_bwd");
+}
+
+extern "C" int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, void* dq, void* dkl, void* stream) {
+    P3D_REQUIRE(args && rope && dq && dkl, "null argument");
+    BwdDev d;
+    if (int rc = fill_bwd(*args, d)) return rc;
+    P3D_REQUIRE(args->dq_local && args->dq_global && args->dk_local, "null pointer argument");
+    P3D_REQUIRE(rope->table && rope->pairs && (rope->packed || rope->coords), "bad rope arguments");
+    const int ep = 16 / dtype_size(args->dtype);
+    const int64_t pieces = ((int64_t)d.B * d.H * d.N + (int64_t)d.B * d.G * d.N) * (args->head_dim / ep);
+    const unsigned blocks = (unsigned)cdiv(pieces, 256);
+    hipStream_t s = as_stream(stream);
+    const RopeDev r = rope_dev(*rope);
+    switch (args->dtype) {
+        case P3D_F32:
+            k_finish_bwd<float><<<blocks, 256, 0, s>>>(d, r, args->head_dim, (float*)dq, (float*)dkl);
+            break;
+        case P3D_F16:
+            k_finish_bwd<_Float16><<<blocks, 256, 0, s>>>(d, r, args->head_dim, (_Float16*)dq, (_Float16*)dkl);
+            break;
+        default:
+            k_finish_bwd<__bf16><<<blocks, 256, 0, s>>>(d, r, args->head_dim, (__bf16*)dq, (__bf16*)dkl);
+            break;
+    }
+    return check_launch("p3d_finish_bwd");
+}

@@ -150,7 +150,7 @@ __device__ __forceinline__ void load_piece(const T* src, float* out) {
     for (int e = 0; e < N; ++e) out[e] = to_f32(v[e]);
 }
 
-inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline int dtype_size(int dt) { return dt == P3D_F32 ? 4 : 2; }
 

@@ -129,6 +129,55 @@ __device__ __forceinline__ void rotate_piece(const int4* meta, const float2* tab
     }
 }
 
+// The inverse rotation R^T of rotate_piece (rotation by -theta).
+template <int EP>
+__device__ __forceinline__ void rotate_piece_inverse(const int4* meta, const float2* tab, const int pos[3], int c0,
+                                                     float* x) {
+#pragma unroll
+    for (int e = 0; e < EP; e += 2) {
+        const int4 p = meta[(c0 + e) >> 1];
+        const int coord = p.z == 0 ? pos[0] : (p.z == 1 ? pos[1] : pos[2]);
+        const float2 cs = tab[p.x + p.y * coord];
+        rotate_pair(x[e], x[e + 1], cs.x, -cs.y);
+    }
+}
+
+// column_sums with the slot weights read from LDS (w[s] for slot s).
+template <typename C, typename T>
+__device__ __forceinline__ void column_sums_w(const uint32_t* rows, const float* w, int lane,
+                                              float (&out)[C::SJ][C::CPD]) {
+    const int h = lane / C::LW, u0 = lane % C::LW;
+    float part[C::SJ][C::CPD];
+#pragma unroll
+    for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+        for (int c = 0; c < C::CPD; ++c) part[j][c] = 0.f;
+    for (int i = 0; i < 64 / C::S; ++i) {
+        const int s = i * C::S + h;
+        const float ws = w[s];
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j) {
+            const int u = u0 + 64 * j;
+            if (u < C::DW) {
+                const uint32_t raw = rows[s * C::RD + u];
+                const T* x = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+                for (int c = 0; c < C::CPD; ++c) part[j][c] += ws * to_f32(x[c]);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = C::LW; o < 64; o <<= 1)
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+            for (int c = 0; c < C::CPD; ++c) part[j][c] += __shfl_xor(part[j][c], o);
+#pragma unroll
+    for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+        for (int c = 0; c < C::CPD; ++c) out[j][c] += part[j][c];
+}
+
 template <typename T, int D>
 __device__ __forceinline__ void write_summary(const PoolDev& a, int64_t item, int lane, int count,
                                               const float (&acck)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD],
@@ -274,6 +323,185 @@ __global__ __launch_bounds__(256) void k_pool_fwd(PoolDev a) {
     }
 }
 
+// Pooling backward (the VJP of compression.py:28-44; kernels.py:240-270 of
+// amilworks/Pack3D): for summary m with fine blocks f and c non-empty blocks,
+// g_k = dsk_m / c and g_v = dsv_m / c (dsk, dsv summed over the query splits
+// of the global pass), and per slot s of block f, with a the slot softmax:
+//   da_s = g_k . k_s + g_v . v_s,   dl_s = a_s (da_s - sum_s' a_s' da_s'),
+//   dk_s = a_s g_k + dl_s w / tau,  dv_s = a_s g_v,
+//   dw += sum_s dl_s k_s / tau,      db_s += dl_s.
+// k_s is the rotated key rounded to the storage type, as in the forward; dk_s
+// is rounded to the storage type, rotated back (R^T) and rounded again, which
+// is the gradient of the unrotated key.  Fine blocks partition the tokens, so
+// every row of dkg / dvg is written exactly once.
+struct PoolBwdDev {
+    const float *dsk_part, *dsv_part;
+    int splits;
+    char *dkg, *dvg;   // [B, G, N, D] contiguous, storage type
+    float *dw_part;    // [B * G * Mp, D]
+    float *db_part;    // [B * G * Mp, V]
+};
+
+template <typename T, int D, bool TAB_LDS>
+__global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
+    typedef PoolCfg<T, D> C;
+    constexpr int EP = C::EP, PPR = C::PPR, CPD = C::CPD;
+    constexpr int WAVE_DW = 2 * 64 * C::RD + 2 * D + 64;  // K rows, V rows, g_k, g_v, slot weights
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const int waves = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int4* meta = reinterpret_cast<int4*>(smem_raw);
+    float* lweight = reinterpret_cast<float*>(meta + D / 2);
+    float* lbias = lweight + D;
+    float2* ltab = reinterpret_cast<float2*>(lbias + 64);
+    const int tab_dw = TAB_LDS ? ((a.table_entries * 2 + 3) & ~3) : 0;
+    uint32_t* krows = reinterpret_cast<uint32_t*>(ltab) + tab_dw + wave * WAVE_DW;
+    uint32_t* vrows = krows + 64 * C::RD;
+    float* gk = reinterpret_cast<float*>(vrows + 64 * C::RD);
+    float* gv = gk + D;
+    float* lw = gv + D;
+    for (int j = threadIdx.x; j < D / 2; j += blockDim.x)
+        meta[j] = int4{a.rope.pairs[3 * j], a.rope.pairs[3 * j + 1], a.rope.pairs[3 * j + 2], 0};
+    for (int c = threadIdx.x; c < D; c += blockDim.x) lweight[c] = a.weight[c];
+    for (int c = threadIdx.x; c < 64; c += blockDim.x) lbias[c] = c < a.V ? a.bias[c] : 0.f;
+    const float2* tab = a.rope.table;
+    if (TAB_LDS) {
+        for (int e = threadIdx.x; e < a.table_entries; e += blockDim.x) ltab[e] = a.rope.table[e];
+        tab = ltab;
+    }
+    __syncthreads();
+
+    const int64_t total = (int64_t)a.B * a.G * a.Mp;
+    const int64_t stride = (int64_t)gridDim.x * waves;
+    const int64_t slice = (int64_t)a.B * a.G * a.Mp * D;  // one split of the partials
+    for (int64_t item = (int64_t)blockIdx.x * waves + wave; item < total; item += stride) {
+        const int g = (int)(item % a.G);
+        const int64_t bm = item / a.G;
+        const int m = (int)(bm % a.Mp), b = (int)(bm / a.Mp);
+        const int64_t bg = (int64_t)b * a.G + g;
+        const int f0 = m * a.P, f_end = m < a.M ? min(a.F, (m + 1) * a.P) : 0;
+        int count = 0;
+        for (int f = f0; f < f_end; ++f) {
+            const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
+            count += __ballot(idx >= 0) != 0;
+        }
+        float dwacc[C::SJ][CPD];
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+            for (int c = 0; c < CPD; ++c) dwacc[j][c] = 0.f;
+        float dbacc = 0.f;
+        if (count > 0) {
+            const float inv = 1.f / (float)count;
+            for (int c = lane; c < D; c += 64) {
+                float sk = 0.f, sv = 0.f;
+                for (int sp = 0; sp < bd.splits; ++sp) {
+                    sk += bd.dsk_part[sp * slice + (bg * a.Mp + m) * D + c];
+                    sv += bd.dsv_part[sp * slice + (bg * a.Mp + m) * D + c];
+                }
+                gk[c] = sk * inv;
+                gv[c] = sv * inv;
+            }
+        }
+        const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
+        const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
+        T* DK = reinterpret_cast<T*>(bd.dkg) + bg * a.N * D;
+        T* DV = reinterpret_cast<T*>(bd.dvg) + bg * a.N * D;
+        for (int f = f0; f < f_end; ++f) {
+            const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
+            if (__ballot(idx >= 0) == 0) continue;
+            int pos[3];
+            rope_position32(a.rope, max(idx, 0), pos);
+            uint4 kr[PPR], vr[PPR];
+            int tok[PPR];
+#pragma unroll
+            for (int i = 0; i < PPR; ++i) tok[i] = __shfl(idx, (i * 64 + lane) / PPR);
+#pragma unroll
+            for (int i = 0; i < PPR; ++i) {
+                const int q = i * 64 + lane, p = q - (q / PPR) * PPR;
+                const int t = max(tok[i], 0);
+                kr[i] = *reinterpret_cast<const uint4*>(K + (int64_t)t * a.ksn + p * EP);
+                vr[i] = *reinterpret_cast<const uint4*>(Vv + (int64_t)t * a.vsn + p * EP);
+            }
+#pragma unroll
+            for (int i = 0; i < PPR; ++i)
+                if (tok[i] < 0) kr[i] = vr[i] = uint4{0u, 0u, 0u, 0u};
+            stage_rows<C>(krows, kr, lane);
+            stage_rows<C>(vrows, vr, lane);
+            wave_lds_sync();
+            // Lane = slot: rotate and round the K row, its logit, and da_s.
+            float logit = -INFINITY, da = 0.f;
+            if (idx >= 0) {
+                float dot = 0.f;
+#pragma unroll 1
+                for (int p = 0; p < PPR; ++p) {
+                    uint4 raw = *reinterpret_cast<const uint4*>(krows + lane * C::RD + p * 4);
+                    const uint4 vraw = *reinterpret_cast<const uint4*>(vrows + lane * C::RD + p * 4);
+                    T* kt = reinterpret_cast<T*>(&raw);
+                    const T* vt = reinterpret_cast<const T*>(&vraw);
+                    float kx[EP];
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) kx[e] = to_f32(kt[e]);
+                    rotate_piece<EP>(meta, tab, pos, p * EP, kx);
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) {
+                        kt[e] = from_f32<T>(kx[e]);
+                        const float k = to_f32(kt[e]);
+                        dot += k * lweight[p * EP + e];
+                        da += gk[p * EP + e] * k + gv[p * EP + e] * to_f32(vt[e]);
+                    }
+                    *reinterpret_cast<uint4*>(krows + lane * C::RD + p * 4) = raw;
+                }
+                logit = dot * a.inv_tau + lbias[lane];
+            }
+            const float mx = wave_max(logit);
+            const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
+            const float w = ex / wave_sum(ex);
+            const float sa = wave_sum(w * da);
+            const float dl = w * (da - sa);
+            dbacc += dl;
+            lw[lane] = dl * a.inv_tau;
+            // dk_s, dv_s of this lane's slot, rotated back and stored.
+            if (idx >= 0) {
+#pragma unroll 1
+                for (int p = 0; p < PPR; ++p) {
+                    float dk[EP], dv[EP];
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) {
+                        const int c = p * EP + e;
+                        dk[e] = to_f32(from_f32<T>(w * gk[c] + dl * lweight[c] * a.inv_tau));
+                        dv[e] = w * gv[c];
+                    }
+                    rotate_piece_inverse<EP>(meta, tab, pos, p * EP, dk);
+                    uint4 ko, vo;
+                    T* kt = reinterpret_cast<T*>(&ko);
+                    T* vt = reinterpret_cast<T*>(&vo);
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) {
+                        kt[e] = from_f32<T>(dk[e]);
+                        vt[e] = from_f32<T>(dv[e]);
+                    }
+                    *reinterpret_cast<uint4*>(DK + (int64_t)idx * D + p * EP) = ko;
+                    *reinterpret_cast<uint4*>(DV + (int64_t)idx * D + p * EP) = vo;
+                }
+            }
+            wave_lds_sync();  // rotated rows and dl / tau are read across lanes below
+            column_sums_w<C, T>(krows, lw, lane, dwacc);
+            wave_lds_sync();  // the next fine block overwrites the rows
+        }
+        // Partials of this item: dw (column dwords of group 0) and db (one per slot).
+        float* dwp = bd.dw_part + item * D;
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j) {
+            const int u = lane + 64 * j;
+            if (lane < C::LW && u < C::DW)
+#pragma unroll
+                for (int c = 0; c < CPD; ++c) dwp[u * CPD + c] = dwacc[j][c];
+        }
+        if (lane < a.V) bd.db_part[item * a.V + lane] = dbacc;
+    }
+}
+
 __global__ void k_zero_f32(float* p, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = 0.f;
@@ -313,14 +541,22 @@ __global__ void k_rotate(RotDev a) {
 // Rope tables up to this size are staged in LDS by every pool block.
 constexpr int kTableLdsBytes = 32768;
 
+// Waves per pool block: four (the four kv heads of a summary run together)
+// when the block's LDS fits in the 160 KiB of a CU, else two, else one.
+inline int pool_waves(size_t fixed, size_t per_wave) {
+    for (int w = 4; w > 1; w >>= 1)
+        if (fixed + per_wave * w <= 160 * 1024) return w;
+    return 1;
+}
+
 template <typename T, int D>
 void launch_pool_t(const PoolDev& d, int64_t items, hipStream_t s) {
     // Four waves (four kv heads of a summary) per block; a persistent grid of
     // as many blocks as stay resident, each striding over the items.
-    constexpr int waves = 4;
     const bool tab_lds = d.table_entries * 8 <= kTableLdsBytes;
     const size_t tab_bytes = tab_lds ? (size_t)((d.table_entries * 2 + 3) & ~3) * 4 : 0;
     const size_t fixed = (size_t)(D / 2) * 16 + (size_t)D * 4 + 64 * 4;
+    const int waves = pool_waves(fixed + tab_bytes, (size_t)PoolCfg<T, D>::WAVE_DW * 4);
     const size_t smem = fixed + tab_bytes + (size_t)PoolCfg<T, D>::WAVE_DW * 4 * waves;
     int dev = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&dev);
@@ -354,7 +590,11 @@ void launch_pool(const PoolDev& d, int dtype, int64_t items, hipStream_t s) {
 
 using namespace p3d;
 
-extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
+namespace p3d {
+namespace {
+
+// Argument checks and device view shared by the pooling forward and backward.
+int fill_pool(const p3d_pool_args* args, PoolDev& d) {
     P3D_REQUIRE(args, "null args");
     const p3d_pool_args& a = *args;
     const int es = dtype_size(a.dtype);
@@ -370,7 +610,7 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     P3D_REQUIRE(a.rope.table_entries >= 1, "rope table_entries must be positive");
     P3D_REQUIRE(a.temperature > 0.f, "temperature must be positive");
     P3D_REQUIRE(a.key_scale > 0.f, "key_scale must be positive");
-    PoolDev d{};
+    d = PoolDev{};
     d.B = a.batch;
     d.G = a.kv_heads;
     d.N = a.tokens;
@@ -393,6 +633,50 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     d.sk = a.sk;
     d.svt = a.svt;
     d.sk_norm_max = a.sk_norm_max;
+    return P3D_OK;
+}
+
+template <typename T, int D>
+void launch_pool_bwd_t(const PoolDev& d, const PoolBwdDev& bd, int64_t items, hipStream_t s) {
+    const bool tab_lds = d.table_entries * 8 <= kTableLdsBytes;
+    const size_t tab_bytes = tab_lds ? (size_t)((d.table_entries * 2 + 3) & ~3) * 4 : 0;
+    const size_t fixed = (size_t)(D / 2) * 16 + (size_t)D * 4 + 64 * 4;
+    const size_t per_wave = (size_t)(2 * 64 * PoolCfg<T, D>::RD + 2 * D + 64) * 4;
+    const int waves = pool_waves(fixed + tab_bytes, per_wave);
+    const size_t smem = fixed + tab_bytes + per_wave * waves;
+    int dev = 0, cus = 0, per_cu = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (tab_lds)
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_bwd<T, D, true>, 64 * waves, smem);
+    else
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_bwd<T, D, false>, 64 * waves, smem);
+    const int64_t resident = (int64_t)std::max(1, cus) * std::max(1, per_cu);
+    const int64_t needed = cdiv(items, waves);
+    const int64_t rounds = cdiv(needed, resident);
+    const unsigned blocks = (unsigned)cdiv(needed, rounds);
+    if (tab_lds)
+        k_pool_bwd<T, D, true><<<blocks, 64 * waves, smem, s>>>(d, bd);
+    else
+        k_pool_bwd<T, D, false><<<blocks, 64 * waves, smem, s>>>(d, bd);
+}
+
+template <int D>
+void launch_pool_bwd(const PoolDev& d, const PoolBwdDev& bd, int dtype, int64_t items, hipStream_t s) {
+    switch (dtype) {
+        case P3D_F32: launch_pool_bwd_t<float, D>(d, bd, items, s); break;
+        case P3D_F16: launch_pool_bwd_t<_Float16, D>(d, bd, items, s); break;
+        default: launch_pool_bwd_t<__bf16, D>(d, bd, items, s); break;
+    }
+}
+
+}  // namespace
+}  // namespace p3d
+
+extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
+    PoolDev d;
+    if (int rc = fill_pool(args, d)) return rc;
+    const p3d_pool_args& a = *args;
     hipStream_t s = as_stream(stream);
     const int bgn = a.batch * a.kv_heads * kNormSlots;
     k_zero_f32<<<(unsigned)cdiv(bgn, 256), 256, 0, s>>>(a.sk_norm_max, bgn);
@@ -427,4 +711,23 @@ extern "C" int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, 
         default: k_rotate<__bf16><<<g, 256, 0, s>>>(d); break;
     }
     return check_launch("p3d_rotate");
+}
+
+extern "C" int p3d_pool_bwd(const p3d_pool_args* args, const float* dsk_part, const float* dsv_part,
+                            int32_t splits, void* dkg, void* dvg, float* dw_part, float* db_part, void* stream) {
+    PoolDev d;
+    if (int rc = fill_pool(args, d)) return rc;
+    P3D_REQUIRE(dsk_part && dsv_part && dkg && dvg && dw_part && db_part, "null pointer argument");
+    P3D_REQUIRE(splits >= 1, "splits must be positive");
+    PoolBwdDev bd{dsk_part, dsv_part, splits, (char*)dkg, (char*)dvg, dw_part, db_part};
+    const int64_t items = (int64_t)d.B * d.G * d.Mp;
+    hipStream_t s = as_stream(stream);
+    switch (args->head_dim) {
+        case 16: launch_pool_bwd<16>(d, bd, args->dtype, items, s); break;
+        case 32: launch_pool_bwd<32>(d, bd, args->dtype, items, s); break;
+        case 48: launch_pool_bwd<48>(d, bd, args->dtype, items, s); break;
+        case 64: launch_pool_bwd<64>(d, bd, args->dtype, items, s); break;
+        default: launch_pool_bwd<128>(d, bd, args->dtype, items, s); break;
+    }
+    return check_launch("p3d_pool_bwd");
 }

@@ -1,0 +1,175 @@
+"""Backward parity of the HIP path with the oracle's autograd (reference.py restated).
+
+Bars as in the reference's own gradient tests (tests/test_triton.py:72-95):
+relative L2 below 3e-5 / 5e-3 / 3.5e-2 for fp32 / fp16 / bf16 on every
+gradient, and assert_close(3e-5) in fp32.
+"""
+import math
+
+import pytest
+import torch
+
+import oracle.pack3d_oracle as ref
+import pack3d_amd as p3d
+from pack3d_amd.rope import axial_rope as hip_axial
+from tests._cases import make_case, random_core_inputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 3e-5, torch.float16: 5e-3, torch.bfloat16: 3.5e-2}
+NAMES = ["q", "kl", "vl", "kg", "vg", "pool_weight", "slot_bias", "gate", "local_scale", "global_scale"]
+
+
+def _compare(got, exp, dtype, what):
+    for name, a, e in zip(NAMES, got, exp):
+        assert torch.isfinite(a).all(), (what, name)
+        err = rel_l2(a.float().cpu(), e.float())
+        mx = (a.float().cpu() - e.float()).abs().max().item()
+        print(f"  {what} d{name}: rel_l2={err:.3g} max_abs={mx:.3g}", flush=True)
+        assert err < TOL[dtype], (what, name, err)
+        if dtype == torch.float32:
+            torch.testing.assert_close(a.cpu(), e, atol=3e-5, rtol=3e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(37, 16, 2, 4, 2, 4, 3), (131, 64, 1, 8, 2, 16, 2), (19, 32, 1, 2, 2, 3, 1),
+                                   (21, 128, 1, 2, 1, 4, 4), (67, 48, 1, 4, 4, 8, 1)])
+def test_every_gradient_custom_graph(gpu, dtype, shape):
+    print(f"backward custom {shape} {dtype}", flush=True)
+    inputs, nb, blocks, pool = make_case(*shape, dtype=dtype)
+    og = ref.prepare_geometry(nb, blocks, pool)
+    hg = p3d.prepare_geometry(nb.to(gpu), blocks.to(gpu), pool)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    rs = [t.detach().clone().requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, hg, temperature=0.7)
+    e = ref.pack3d_reference(*rs, og, temperature=0.7)
+    up = torch.randn(e.shape, generator=torch.Generator().manual_seed(91)).to(dtype)
+    got = torch.autograd.grad(y, xs, up.to(gpu))
+    exp = torch.autograd.grad(e, rs, up)
+    _compare(got, exp, dtype, f"custom {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind,kv_heads", [("native_block_morton", 2), ("raster_block", 4)])
+def test_every_gradient_grid_rope_fused(gpu, dtype, kind, kv_heads):
+    """A complete-grid layout (brick forward) with the rotation fused: the
+    gradients of q, kl, kg are those of the unrotated projections."""
+    print(f"backward grid {kind} g{kv_heads} {dtype}", flush=True)
+    shape, d = (8, 8, 12), 48
+    n = math.prod(shape)
+    lay_h = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout=kind)
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout=kind)
+    inputs = random_core_inputs(1, 4, kv_heads, n, d, 64, dtype, seed=23)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    rs = [t.detach().clone().requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip_rope(*xs, lay_h.geometry, hip_axial(d, shape, lay_h.coords), temperature=0.8)
+    rot = [ref.axial_rope(t, lay_r.coords) if i in (0, 1, 3) else t for i, t in enumerate(rs)]
+    e = ref.pack3d_reference(*rot, lay_r.geometry, temperature=0.8)
+    up = torch.randn(e.shape, generator=torch.Generator().manual_seed(5)).to(dtype)
+    got = torch.autograd.grad(y, xs, up.to(gpu))
+    exp = torch.autograd.grad(e, rs, up)
+    _compare(got, exp, dtype, f"grid {kind}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_singleton_summary_has_no_query_or_key_gradient(gpu, dtype):
+    """One token, one summary: the local row is empty and attention to a single
+    summary is its value, so q, kl, vl, kg and the pooling parameters get
+    exactly zero gradient (tests/test_triton.py:262-271)."""
+    inputs, nb, blocks, pool = make_case(n=1, d=16, b=1, h=1, g=1, volume=1, pool=1, dtype=dtype)
+    hg = p3d.prepare_geometry(nb.to(gpu), blocks.to(gpu), pool)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, hg)
+    grads = torch.autograd.grad(y, xs, torch.randn_like(y))
+    for index in (0, 1, 2, 3, 5, 6):
+        assert torch.count_nonzero(grads[index]) == 0, (index, grads[index].abs().max().item())
+
+
+def test_mutated_saved_geometry_fails_backward(gpu):
+    inputs, nb, blocks, pool = make_case()
+    hg = p3d.prepare_geometry(nb.to(gpu), blocks.to(gpu), pool)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, hg)
+    hg.neighbors[1, 0] = 1
+    with pytest.raises(RuntimeError, match="changed"):
+        y.sum().backward()
+
+
+def test_repeated_backward_is_deterministic(gpu):
+    inputs, nb, blocks, pool = make_case(131, 64, 1, 8, 2, 16, 2)
+    hg = p3d.prepare_geometry(nb.to(gpu), blocks.to(gpu), pool)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, hg)
+    dy = torch.randn_like(y)
+    g1 = torch.autograd.grad(y, xs, dy, retain_graph=True)
+    g2 = torch.autograd.grad(y, xs, dy)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_layer_gradients_match_oracle(gpu):
+    """The whole layer in fp32 on an anisotropic grid: input and every
+    parameter gradient against the oracle layer under the same weights."""
+    print("layer backward", flush=True)
+    torch.manual_seed(0)
+    shape = (4, 16, 8)
+    oracle = ref.PACK3DAttention(192, heads=4, kv_heads=2, head_dim=48, block_volume=64)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=2, head_dim=48, block_volume=64)
+    layer.load_state_dict(oracle.state_dict())
+    layer = layer.to(gpu)
+    lay_h = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    x = torch.randn(1, math.prod(shape), 192, generator=torch.Generator().manual_seed(1))
+    xh = x.to(gpu).requires_grad_()
+    xr = x.clone().requires_grad_()
+    dy = torch.randn(x.shape, generator=torch.Generator().manual_seed(2))
+    layer(xh, lay_h).backward(dy.to(gpu))
+    oracle(xr, lay_r).backward(dy)
+    torch.testing.assert_close(xh.grad.cpu(), xr.grad, atol=3e-5, rtol=3e-5)
+    expected = dict(oracle.named_parameters())
+    for name, p in layer.named_parameters():
+        err = rel_l2(p.grad.cpu(), expected[name].grad)
+        print(f"  layer {name}: rel_l2={err:.3g}", flush=True)
+        assert err < 1e-4, (name, err)
+
+
+def test_full_size_c4_backward_sampled(gpu):
+    """c4: 32 x 128 x 64 (262,144 tokens), bf16 under autocast, forward and
+    backward through the layer.  dq_i depends only on row i's forward (and
+    every summary), so dq on sampled rows is checked exactly against the
+    oracle evaluated on those rows; every gradient must be finite."""
+    print("full size c4 backward", flush=True)
+    torch.manual_seed(0)
+    shape = (32, 128, 64)
+    n = math.prod(shape)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    for lin in (layer.to_q, layer.to_kv, layer.to_out):
+        torch.nn.init.xavier_uniform_(lin.weight)
+    layer = layer.to(gpu)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1)).to(gpu)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, lay)
+    core = [t.detach().requires_grad_() for t in (q, kl, vl, kg, vg)]
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = p3d.pack3d_hip_rope(*core, layer.pool_weight, layer.slot_bias, gate.detach(), layer.local_scale,
+                                layer.global_scale, lay.geometry, rope)
+    dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(2)).to(gpu, y.dtype)
+    grads = torch.autograd.grad(y, core + [layer.pool_weight, layer.slot_bias], dy)
+    for gr in grads:
+        assert torch.isfinite(gr).all()
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(3))[:256]
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    cpu = [t.detach().cpu().float() for t in (q, kl, vl, kg, vg)]
+    qr = cpu[0].requires_grad_()
+    rot = [ref.axial_rope(qr, lay_r.coords), ref.axial_rope(cpu[1], lay_r.coords), cpu[2],
+           ref.axial_rope(cpu[3], lay_r.coords), cpu[4]]
+    params = [t.detach().cpu().float() for t in (layer.pool_weight, layer.slot_bias)]
+    e = ref.pack3d_reference(*rot, *params, gate.detach().cpu().float(), layer.local_scale.detach().cpu(),
+                             layer.global_scale.detach().cpu(), lay_r.geometry, rows=rows, chunk=256)
+    (e * dy[:, :, rows.to(gpu)].cpu().float()).sum().backward()
+    exp = qr.grad[:, :, rows]
+    got = grads[0][:, :, rows.to(gpu)].float().cpu()
+    err = rel_l2(got, exp)
+    print(f"  c4 sampled dq: rel_l2={err:.3g}", flush=True)
+    assert err < TOL[torch.bfloat16]

@@ -180,6 +180,15 @@ int p3d_local_fwd_indexed(const p3d_attn_args* args, const int32_t* neighbors, i
 int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tokens,
                int32_t head_dim, int32_t dtype, const p3d_rope* rope, int32_t inverse, void* stream);
 
+/* ---- layer (attention.py:64) ------------------------------------------- */
+
+/* nn.LayerNorm over the last dimension of x [rows, dim] (contiguous, dtype):
+ * y = (x - mean) / sqrt(var + eps) * weight + bias, statistics in fp32,
+ * weight / bias [dim] of param_dtype.  dim must be a multiple of the 16-byte
+ * piece and at most 64 pieces. */
+int p3d_layer_norm(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
+                   int64_t rows, int32_t dim, int32_t dtype, float eps, void* stream);
+
 /* ---- backward (replaces kernels.py:313-356, autograd.py:19-28) --------- */
 
 /* Shared argument block of the backward passes.  q and kl are the ROTATED

@@ -84,6 +84,7 @@ SIGNATURES = {
     "p3d_struct_sizes": ([_P], c_int32),
     "p3d_rotate": ([View, View, c_int32, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(Rope), c_int32, _P],
                    c_int32),
+    "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
     "p3d_mix_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),
     "p3d_global_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),

@@ -2,9 +2,10 @@
 
 Same constructor, parameters (names, shapes, initialisation order) and
 forward as ``PACK3DAttention`` of amilworks/Pack3D (``src/pack3d/attention.py``),
-with ``backend="hip"``: LayerNorm, projections, the gate softmax, ``to_out``
-and the residual stay in PyTorch (hipBLASLt GEMMs); the rotation, pooling,
-local and global attention and their fusion run in ``libpack3d_hip.so``.
+with ``backend="hip"``: the projections, the gate softmax and ``to_out``
+(with the residual as the GEMM's C operand) stay in PyTorch (hipBLASLt
+GEMMs); LayerNorm (without autograd), the rotation, pooling, local and global
+attention and their fusion run in ``libpack3d_hip.so``.
 The projections are consumed as strided views, without copies.
 """
 from __future__ import annotations
@@ -14,9 +15,34 @@ import math
 import torch
 from torch import nn
 
+from . import _lib
 from .core import SUPPORTED_HEAD_DIMS, pack3d_hip_rope
 from .geometry import TokenLayout
 from .rope import axial_rope, balanced_pairs, packed_rope
+
+
+def layer_norm(norm: nn.LayerNorm, x):
+    """``norm(x)`` on the HIP LayerNorm kernel when no gradient is needed.
+
+    With autograd active (training, autocast) the differentiable torch op
+    runs instead; shapes the kernel does not take (a channel count that is
+    not a whole number of 16-byte pieces, or above 64 pieces) do too.
+    """
+    dim = x.shape[-1]
+    dtypes = _lib.DTYPES
+    ep = 16 // x.element_size()
+    usable = (x.is_cuda and x.dtype in dtypes and norm.weight is not None and norm.bias is not None
+              and norm.weight.dtype == norm.bias.dtype and norm.weight.dtype in dtypes
+              and dim % ep == 0 and dim // ep <= 64 and len(norm.normalized_shape) == 1)
+    if not usable or (torch.is_grad_enabled() and (x.requires_grad or norm.weight.requires_grad
+                                                   or norm.bias.requires_grad)):
+        return norm(x)
+    xc = x.contiguous()
+    y = torch.empty_like(xc)
+    _lib.call("p3d_layer_norm", xc.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(),
+              dtypes[norm.weight.dtype], y.data_ptr(), xc.numel() // dim, dim, dtypes[x.dtype], float(norm.eps),
+              _lib.stream_of(x.device))
+    return y
 
 
 class PACK3DAttention(nn.Module):
@@ -55,7 +81,7 @@ class PACK3DAttention(nn.Module):
     def core_inputs(self, x, layout: TokenLayout):
         """Unrotated q, kl, vl, kg, vg (views of the projections), gate, and the rotation."""
         b, n = x.shape[0], x.shape[1]
-        xn = self.norm(x)
+        xn = layer_norm(self.norm, x)
         q = self.to_q(xn).view(b, n, self.heads, self.head_dim).transpose(1, 2)
         kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
                           for t in self.to_kv(xn).view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
@@ -80,4 +106,6 @@ class PACK3DAttention(nn.Module):
         q, kl, vl, kg, vg, gate, rope = self.core_inputs(x, layout)
         out = pack3d_hip_rope(q, kl, vl, kg, vg, self.pool_weight, self.slot_bias, gate, self.local_scale,
                               self.global_scale, layout.geometry, rope, temperature=self.temperature)
-        return x + self.to_out(out.transpose(1, 2).reshape(b, n, -1))
+        # x + to_out(out) as one GEMM with the residual as its C operand (to_out has no bias).
+        o = out.transpose(1, 2).reshape(b * n, -1)
+        return torch.addmm(x.reshape(b * n, self.dim), o, self.to_out.weight.t()).view(b, n, self.dim)

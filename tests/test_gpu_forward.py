@@ -236,3 +236,23 @@ def test_core_loose_bound_takes_exact_path(gpu, grid):
         geom = p3d.prepare_geometry(lay_r.geometry.neighbors, lay_r.geometry.blocks, 1)
     got = p3d.pack3d_hip(*(t.to(gpu) for t in inputs), geom)
     _check(got, exp, torch.float32, "y")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim", [192, 64, 512])
+def test_layer_norm_kernel_matches_torch(gpu, dtype, dim):
+    """The layer's LayerNorm kernel against torch's (attention.py:64), parameters
+    in the storage type and in fp32."""
+    from pack3d_amd.attention import layer_norm
+    gen = torch.Generator().manual_seed(dim)
+    x = (torch.randn(3, 1000, dim, generator=gen) * 2 + 0.5).to(gpu, dtype)
+    for pdtype in (dtype, torch.float32):
+        norm = torch.nn.LayerNorm(dim).to(gpu, pdtype)
+        with torch.no_grad():
+            norm.weight.copy_(torch.randn(dim, generator=gen))
+            norm.bias.copy_(torch.randn(dim, generator=gen))
+            got = layer_norm(norm, x)
+            exp = torch.nn.functional.layer_norm(x.float(), (dim,), norm.weight.float(), norm.bias.float(),
+                                                 norm.eps)
+        tol = 1e-5 if dtype == torch.float32 else (2e-3 if dtype == torch.float16 else 1.6e-2)
+        torch.testing.assert_close(got.float(), exp.to(dtype).float(), atol=tol * 4, rtol=tol)

@@ -240,6 +240,15 @@ int p3d_mix_bwd(const p3d_bwd_args* args, void* stream);
 int p3d_local_bwd_indexed(const p3d_bwd_args* args, const int32_t* neighbors, int32_t width,
                           const int32_t* reverse, int32_t rwidth, void* stream);
 
+/* Local pathway backward for complete-grid layouts (build_layout and its
+ * repacks; the brick decomposition of p3d_attn_fwd_grid): dq_local, dk_local
+ * and dv_local as p3d_local_bwd_indexed, from halo planes in LDS on MFMA,
+ * without the neighbour tables.  grid (Z, Y, X), per-axis radius <= 2.
+ * Returns P3D_EUNSUPPORTED when a halo plane does not fit in LDS (fp32 with
+ * head_dim 128). */
+int p3d_local_bwd_grid(const p3d_bwd_args* args, const int32_t grid[3], const int32_t radius[3],
+                       const int32_t* raster_to_packed, void* stream);
+
 /* Summary pathway backward (kernels.py:184-237): dq_global and the split
  * partials dsk_part / dsv_part (sv_rows and skt are filled first). */
 int p3d_global_bwd(const p3d_bwd_args* args, void* stream);

@@ -87,6 +87,7 @@ SIGNATURES = {
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
     "p3d_mix_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),
+    "p3d_local_bwd_grid": ([ctypes.POINTER(BwdArgs), _P, _P, _P, _P], c_int32),
     "p3d_global_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_finish_bwd": ([ctypes.POINTER(BwdArgs), ctypes.POINTER(Rope), _P, _P, _P], c_int32),
     "p3d_pool_bwd": ([ctypes.POINTER(PoolArgs), _P, _P, c_int32, _P, _P, _P, _P, _P], c_int32),
@@ -133,6 +134,10 @@ def ptr(t):
 
 def i64x3(values):
     return (c_int64 * 3)(*[int(v) for v in values])
+
+
+def i32x3(values):
+    return (c_int32 * 3)(*[int(v) for v in values])
 
 
 def view(t: torch.Tensor) -> View:

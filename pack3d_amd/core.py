@@ -297,8 +297,14 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     keep += [qr, klr, gate_k, sl32, sg32, dy]
 
     _lib.call("p3d_mix_bwd", a, stream)
-    nb, rev = geometry.neighbors, geometry.reverse_neighbors
-    _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)
+    if grid_kernel_applies(geometry) and not (q.dtype == torch.float32 and d == 128):
+        # Brick-tiled on MFMA; fp32 planes of head_dim 128 do not fit in LDS.
+        shape, radius = geometry._grid
+        _lib.call("p3d_local_bwd_grid", a, _lib.i32x3(shape), _lib.i32x3(radius),
+                  _lib.ptr(geometry._raster_to_packed), stream)
+    else:
+        nb, rev = geometry.neighbors, geometry.reverse_neighbors
+        _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)
     _lib.call("p3d_global_bwd", a, stream)
     dq = empty(b, h, n, d)
     dkl = empty(b, g, n, d)

@@ -173,3 +173,26 @@ def test_full_size_c4_backward_sampled(gpu):
     err = rel_l2(got, exp)
     print(f"  c4 sampled dq: rel_l2={err:.3g}", flush=True)
     assert err < TOL[torch.bfloat16]
+
+
+from tests.test_gpu_forward import GRIDS  # noqa: E402
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,block,radius,kind,heads,kv_heads,d", GRIDS)
+def test_every_gradient_grid_shapes(gpu, dtype, shape, block, radius, kind, heads, kv_heads, d):
+    """Complete-grid layouts of every radius pattern and partial bricks (the
+    brick-tiled local backward), against the oracle's autograd."""
+    print(f"backward grid {shape} {block} {radius} {kind} h{heads} g{kv_heads} d{d} {dtype}", flush=True)
+    lay_h = p3d.build_layout(shape, block, radius=radius, pool_size=1, layout=kind)
+    lay_r = ref.build_layout(shape, block, radius=radius, pool_size=1, layout=kind)
+    n, vol = math.prod(shape), math.prod(block)
+    inputs = random_core_inputs(1, heads, kv_heads, n, d, vol, dtype, seed=n + 3 * d)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    rs = [t.detach().clone().requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, lay_h.geometry, temperature=0.9)
+    e = ref.pack3d_reference(*rs, lay_r.geometry, temperature=0.9)
+    up = torch.randn(e.shape, generator=torch.Generator().manual_seed(17)).to(dtype)
+    got = torch.autograd.grad(y, xs, up.to(gpu))
+    exp = torch.autograd.grad(e, rs, up)
+    _compare(got, exp, dtype, f"grid {shape}")

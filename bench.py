@@ -187,6 +187,50 @@ def traffic_probe():
     print("traffic probe done", flush=True)
 
 
+C4_SHAPE = (32, 128, 64)
+
+
+def bench_c4(steps, warmup):
+    """c4: layer forward + backward on 32 x 128 x 64
+    (262,144 tokens), batch 1, raster, bf16 autocast, upstream gradient N(0, 1).
+    A step is one forward and one backward to every parameter and the input."""
+    import pack3d_amd as p3d
+
+    dev = torch.device("cuda:0")
+    n = math.prod(C4_SHAPE)
+    torch.manual_seed(0)
+    layer = p3d.PACK3DAttention(DIM, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
+                                block_volume=math.prod(BLOCK))
+    for lin in (layer.to_q, layer.to_kv, layer.to_out):
+        torch.nn.init.xavier_uniform_(lin.weight)
+    layer = layer.to(dev)
+    layout = p3d.build_layout(C4_SHAPE, BLOCK, radius=RADIUS, pool_size=1, layout="raster_block", device=dev)
+    x = torch.randn(1, n, DIM, generator=torch.Generator().manual_seed(1)).to(dev).requires_grad_()
+    dy = torch.randn(1, n, DIM, generator=torch.Generator().manual_seed(2)).to(dev)
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = layer(x, layout)
+        y.backward(dy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = 1000.0 * (time.perf_counter() - t0) / steps
+    return {"metric": "ms per PACK3D layer fwd+bwd @c4 (32x128x64, 262,144 tokens) bf16 autocast",
+            "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "c4: PACK3D layer forward + backward, 32x128x64 volume, batch 1, raster, "
+                                   "bf16 autocast", "dim": DIM, "heads": HEADS, "kv_heads": KV_HEADS,
+                       "head_dim": HEAD_DIM, "radius": RADIUS, "block": list(BLOCK), "pool_size": 1,
+                       "tokens_per_s": round(n / (ms * 1e-3)), "parallelism": "single GPU"}}
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
@@ -196,6 +240,8 @@ def main():
     p.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     p.add_argument("--traffic-probe", action="store_true",
                    help="only run the launch sequence that the HBM traffic counters are collected over")
+    p.add_argument("--c4", action="store_true",
+                   help="time the c4 layer forward + backward instead (one JSON line of its own)")
     a = p.parse_args()
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
@@ -205,6 +251,9 @@ def main():
         sys.exit(2)
     if a.traffic_probe:
         traffic_probe()
+        return
+    if a.c4:
+        print(json.dumps(bench_c4(a.steps, a.warmup)), flush=True)
         return
 
     import pack3d_amd as p3d

@@ -360,8 +360,8 @@ __device__ __forceinline__ void build_rope_window(const AttnDev& a, int D, int o
 }
 
 // Workgroups are dispatched round-robin over the 8 XCDs.  Give each XCD a
-// contiguous run of bricks (raster brick order) so that the bricks an XCD
-// runs together are neighbours and share halo rows in its L2.
+// contiguous run of work items (heads of a brick, then bricks in raster
+// order) so that the items an XCD runs together share rows in its L2.
 __device__ __forceinline__ int xcd_brick(int id, int bricks) {
     const int q = bricks / 8, r = bricks % 8;
     const int xcd = id % 8, slot = id / 8;
@@ -472,9 +472,13 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     T* Vp = Kp + kPlaneKeys * C::KSTR;
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, qi = lane & 31;
-    const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.G);
+    // Heads run fastest: the workgroups of one brick's heads follow each other
+    // on one XCD, so the rows they share (every head's slice of a token's
+    // projection row lies in the same cache lines) are fetched from HBM once.
+    const int work = xcd_brick(blockIdx.x, gridDim.x);
+    const int bh = work % (a.B * a.H), brick = work / (a.B * a.H);
+    const int b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.G);
     const int64_t bg = (int64_t)b * a.G + kvh;
-    const int brick = xcd_brick(blockIdx.x, gridDim.x);
     const int Z0 = 4 * (brick / (a.bricks_y * a.bricks_x));
     const int Y0 = 8 * ((brick / a.bricks_x) % a.bricks_y);
     const int X0 = 8 * (brick % a.bricks_x);
@@ -745,8 +749,8 @@ extern "C" int p3d_attn_fwd_grid(const p3d_attn_args* args, void* stream) {
     d.rz = args->radius[0], d.ry = args->radius[1], d.rx = args->radius[2];
     d.bricks_y = (int)cdiv(d.Y, 8), d.bricks_x = (int)cdiv(d.X, 8);
     const int64_t bricks = cdiv(d.Z, 4) * d.bricks_y * d.bricks_x;
-    P3D_REQUIRE(bricks < (1LL << 31) && (int64_t)d.B * d.H < 65536, "launch grid too large");
-    dim3 grid((unsigned)bricks, (unsigned)(d.B * d.H));
+    P3D_REQUIRE(bricks * d.B * d.H < (1LL << 31), "launch grid too large");
+    dim3 grid((unsigned)(bricks * d.B * d.H));
     hipStream_t s = as_stream(stream);
     switch (args->head_dim) {
 #define CASE(DD) \

@@ -29,6 +29,10 @@ if ROOT not in sys.path:
 METRIC = "ms per PACK3D layer fwd @262,144 tokens bf16; % of MFMA/HBM roofline"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# v_exp_f32 issue rate of the whole chip, two waves per SIMD, measured by
+# `bench.py --probe-rates` (profiles/issue_rates.md): the transcendental
+# rate that bounds the softmax of the summary pathway.
+PEAK_EXP_PER_S = 11.81e12
 
 SHAPE = (64, 64, 64)
 DIM, HEADS, KV_HEADS, HEAD_DIM, BLOCK, RADIUS = 192, 4, 4, 48, (4, 4, 4), 2
@@ -231,6 +235,39 @@ def bench_c4(steps, warmup):
                        "tokens_per_s": round(n / (ms * 1e-3)), "parallelism": "single GPU"}}
 
 
+def probe_rates():
+    """Issue rates the summary pathway is bound by, with two waves per SIMD on
+    every CU, timed with HIP events: v_exp_f32 and v_fma_f32 per second, the
+    bf16 32x32x16 MFMA in TFLOP/s, and both rates when every wave issues 4
+    MFMAs and 16 exponentials per iteration, independent of each other."""
+    from pack3d_amd import _lib
+
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks, iters = 2 * cus, 4096
+    waves = blocks * 4
+    cycles = torch.zeros(waves, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for kind, name in ((0, "exp"), (1, "fma"), (2, "mfma"), (3, "mix")):
+        _lib.call("p3d_probe_issue_rates", kind, 64, blocks, cycles.data_ptr(), stream.cuda_stream)
+        ms = time_events(lambda: _lib.call("p3d_probe_issue_rates", kind, iters, blocks, cycles.data_ptr(),
+                                           stream.cuda_stream), 3, stream)
+        sec = ms * 1e-3
+        lanes = waves * 64 * iters * 16
+        mfma_flops = waves * iters * 4 * 32 * 32 * 16 * 2
+        if name == "exp":
+            res["exp_per_s"] = lanes / sec
+        elif name == "fma":
+            res["fma_per_s"] = lanes / sec
+        elif name == "mfma":
+            res["mfma_tflops"] = mfma_flops / sec / 1e12
+        else:
+            res["mix_mfma_tflops"] = mfma_flops / sec / 1e12
+            res["mix_exp_per_s"] = lanes / sec
+    return {k: float(f"{v:.4g}") for k, v in res.items()} | {"cus": cus, "waves_per_simd": 2}
+
+
 def main():
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("--gpus", type=int, default=1)
@@ -242,6 +279,8 @@ def main():
                    help="only run the launch sequence that the HBM traffic counters are collected over")
     p.add_argument("--c4", action="store_true",
                    help="time the c4 layer forward + backward instead (one JSON line of its own)")
+    p.add_argument("--probe-rates", action="store_true",
+                   help="measure the exp / fma / MFMA issue rates instead (one JSON line of its own)")
     a = p.parse_args()
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
@@ -254,6 +293,9 @@ def main():
         return
     if a.c4:
         print(json.dumps(bench_c4(a.steps, a.warmup)), flush=True)
+        return
+    if a.probe_rates:
+        print(json.dumps(probe_rates()), flush=True)
         return
 
     import pack3d_amd as p3d
@@ -292,6 +334,8 @@ def main():
     flops_summary = 4 * HEADS * n * m * HEAD_DIM
     flops_local = 4 * HEADS * edges * HEAD_DIM
     attn_tflops = (flops_summary + flops_local) / (ms_attn * 1e-3) / 1e12
+    exps = HEADS * n * m + HEADS * edges  # one exponential per (query, summary) and per valid edge
+    exp_rate = exps / (ms_attn * 1e-3)
     pool_bytes = 2 * KV_HEADS * n * HEAD_DIM * 2 + 2 * KV_HEADS * m * HEAD_DIM * 2
     pool_gbs = pool_bytes / (ms_pool * 1e-3) / 1e9
     cpu = None if a.no_cpu_baseline else cpu_baseline(SHAPE, a.cpu_threads)
@@ -310,6 +354,9 @@ def main():
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get("attn_bytes_per_launch"),
                      "algorithmic_flops": flops_summary + flops_local},
+        "roofline_exp": {"kernel": "k_attn_grid", "bound": "valu-transcendental", "achieved": float(f"{exp_rate:.4g}"),
+                         "peak": PEAK_EXP_PER_S, "unit": "exp/s", "frac": round(exp_rate / PEAK_EXP_PER_S, 4),
+                         "algorithmic_exps": exps},
         "roofline_pool": {"kernel": "k_pool_fwd", "bound": "hbm", "achieved": round(pool_gbs, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(pool_gbs / PEAK_HBM_GBS, 4),
                           "traffic": traffic.get("pool_bytes_per_launch"),

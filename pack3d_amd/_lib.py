@@ -82,6 +82,7 @@ SIGNATURES = {
     "p3d_local_fwd_indexed": ([ctypes.POINTER(AttnArgs), _P, c_int32, _P, _P], c_int32),
     "p3d_selftest_mfma": ([c_int32, _P, _P, _P, _P], c_int32),
     "p3d_struct_sizes": ([_P], c_int32),
+    "p3d_probe_issue_rates": ([c_int32, c_int64, c_int32, _P, _P], c_int32),
     "p3d_rotate": ([View, View, c_int32, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(Rope), c_int32, _P],
                    c_int32),
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),

@@ -29,10 +29,70 @@ __global__ void k_mfma_probe(const T* A, const T* B, float* Dout) {
     for (int r = 0; r < 16; ++r) Dout[acc_row(r, g) * 32 + i] = acc[r];
 }
 
+// Issue-rate probes (kind): 0 = v_exp_f32, 1 = v_fma_f32, 2 = 32x32x16 bf16
+// MFMA, 3 = per iteration 4 MFMAs and 16 exponentials, independent of each
+// other (the mix of the summary pathway).  Every wave writes the shader
+// clock cycles of its loop; 16 (or 4) independent chains keep the units fed.
+template <int KIND>
+__global__ __launch_bounds__(256) void k_rate_probe(int iters, long long* cycles) {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = (threadIdx.x + i) * 1e-6f - 1.f;
+    bf16x8 a, b;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        a[j] = (__bf16)(0.01f * j);
+        b[j] = (__bf16)(0.02f * j);
+    }
+    f32x16 c[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) c[k][r] = 0.f;
+    const long long t0 = clock64();
+    for (int it = 0; it < iters; ++it) {
+        if constexpr (KIND == 0 || KIND == 3) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[i] = __builtin_amdgcn_exp2f(x[i]) - 1.5f;
+        }
+        if constexpr (KIND == 1) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[i] = fmaf(x[i], 0.999f, -0.5f);
+        }
+        if constexpr (KIND == 2 || KIND == 3) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) c[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c[k], 0, 0, 0);
+        }
+    }
+    const long long t1 = clock64();
+    float keep = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) keep += x[i];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) keep += c[k][r];
+    if ((threadIdx.x & 63) == 0) cycles[blockIdx.x * 4 + (threadIdx.x >> 6)] = (t1 - t0) + (keep == 12345.f);
+}
+
 }  // namespace
 }  // namespace p3d
 
 using namespace p3d;
+
+extern "C" int p3d_probe_issue_rates(int32_t kind, int64_t iters, int32_t blocks, long long* cycles, void* stream) {
+    P3D_REQUIRE(cycles && kind >= 0 && kind <= 3 && iters >= 1 && iters < (1LL << 31) && blocks >= 1,
+                "bad probe arguments");
+    hipStream_t s = as_stream(stream);
+    const int n = (int)iters;
+    switch (kind) {
+        case 0: k_rate_probe<0><<<(unsigned)blocks, 256, 0, s>>>(n, cycles); break;
+        case 1: k_rate_probe<1><<<(unsigned)blocks, 256, 0, s>>>(n, cycles); break;
+        case 2: k_rate_probe<2><<<(unsigned)blocks, 256, 0, s>>>(n, cycles); break;
+        default: k_rate_probe<3><<<(unsigned)blocks, 256, 0, s>>>(n, cycles); break;
+    }
+    return check_launch("p3d_probe_issue_rates");
+}
 
 extern "C" int p3d_selftest_mfma(int32_t dtype, const void* a, const void* b, float* d, void* stream) {
     P3D_REQUIRE(a && b && d, "null argument");

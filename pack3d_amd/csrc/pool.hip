@@ -4,12 +4,12 @@
 // One wave pools one coarse summary of one (batch, kv head).  For each of its
 // fine blocks the wave issues every 16-byte load of the block's K and V rows
 // at once (lane l holds pieces l, l + 64, ... of the 64 x D/EP piece grid)
-// and writes the K rows to LDS with 16-byte stores.  Then one lane per slot
-// reads its K row (conflict-free 16-byte reads), rotates it, rounds it to the
-// storage type (the reference pools rotated keys stored in that type), writes
-// it back and forms the slot logit; the slot softmax is a wave reduction.  The
-// weighted sums are column reads of the K rows, then of the V rows staged in
-// the same buffer.  The coarse mean divides by the number of non-empty fine
+// and writes the K and V rows to two LDS row buffers with 16-byte stores.
+// Then one lane per slot reads its K row (conflict-free 16-byte reads),
+// rotates it, rounds it to the storage type (the reference pools rotated keys
+// stored in that type), writes it back and forms the slot logit; the slot
+// softmax is a wave reduction.  The weighted sums are column reads of the K
+// and V rows.  The coarse mean divides by the number of non-empty fine
 // blocks.
 #include <algorithm>
 
@@ -37,11 +37,11 @@ struct PoolDev {
     float* sk_norm_max;
 };
 
-// LDS plan of one wave: one buffer of 64 rows (row stride D + EP elements)
-// that holds the block's K rows and then its V rows, plus the 64 slot
-// weights.  For the column sums lane (h, u) owns column dword u of the slots
-// h, h + S, h + 2S, ...; the row stride is 4 dwords more than a row, so the
-// S lane groups read disjoint banks when S rows fit in 64 banks.
+// Row geometry of the K / V row buffers in LDS: 64 rows (one per slot) of
+// row stride D + EP elements.  For the column sums lane (h, u) owns column
+// dword u of the slots h, h + S, h + 2S, ...; the row stride is 4 dwords more
+// than a row, so the S lane groups read disjoint banks when S rows fit in 64
+// banks.
 template <typename T, int D>
 struct PoolCfg {
     static constexpr int EP = Piece<T>::N;        // elements per 16-byte piece
@@ -52,7 +52,6 @@ struct PoolCfg {
     static constexpr int LW = DW <= 8 ? 8 : (DW <= 16 ? 16 : (DW <= 32 ? 32 : 64));  // lanes per slot group
     static constexpr int S = 64 / LW;              // slot groups
     static constexpr int SJ = (DW + 63) / 64;      // column dwords per lane
-    static constexpr int WAVE_DW = 64 * RD + 64;   // rows + slot weights
 };
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -72,59 +71,26 @@ __device__ __forceinline__ void stage_rows(uint32_t* rows, const uint4 (&r)[C::P
     }
 }
 
-// sum_s w_s * row_s, column by column; every lane ends with the totals of its
-// column dwords (lane % LW, + 64, ...).  w is the slot weight held by lane s;
-// it is broadcast with readlane, so the loop issues only row reads to LDS.
-template <typename C, typename T>
-__device__ __forceinline__ void column_sums(const uint32_t* rows, float w, int lane, float (&out)[C::SJ][C::CPD]) {
-    const int h = lane / C::LW, u0 = lane % C::LW;
-    float part[C::SJ][C::CPD];
-#pragma unroll
-    for (int j = 0; j < C::SJ; ++j)
-#pragma unroll
-        for (int c = 0; c < C::CPD; ++c) part[j][c] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 64 / C::S; ++i) {
-        float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i * C::S));
-#pragma unroll
-        for (int hh = 1; hh < C::S; ++hh) {
-            const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), i * C::S + hh));
-            ws = h == hh ? o : ws;
-        }
-        const int s = i * C::S + h;
-#pragma unroll
-        for (int j = 0; j < C::SJ; ++j) {
-            const int u = u0 + 64 * j;
-            if (u < C::DW) {
-                const uint32_t raw = rows[s * C::RD + u];
-                const T* x = reinterpret_cast<const T*>(&raw);
-#pragma unroll
-                for (int c = 0; c < C::CPD; ++c) part[j][c] += ws * to_f32(x[c]);
-            }
-        }
-    }
-#pragma unroll
-    for (int o = C::LW; o < 64; o <<= 1)
-#pragma unroll
-        for (int j = 0; j < C::SJ; ++j)
-#pragma unroll
-            for (int c = 0; c < C::CPD; ++c) part[j][c] += __shfl_xor(part[j][c], o);
-#pragma unroll
-    for (int j = 0; j < C::SJ; ++j)
-#pragma unroll
-        for (int c = 0; c < C::CPD; ++c) out[j][c] += part[j][c];
+// Rotary metadata of pair j as staged in LDS: {base, stride along axis 0,
+// along axis 1, along axis 2}, where only the pair's own axis has a non-zero
+// stride, so the table index is base + sum_a stride_a * pos[a] with no
+// per-pair branch on the axis.
+__device__ __forceinline__ int4 pair_meta(const int32_t* pairs, int j) {
+    const int base = pairs[3 * j], stride = pairs[3 * j + 1], axis = pairs[3 * j + 2];
+    return int4{base, axis == 0 ? stride : 0, axis == 1 ? stride : 0, axis == 2 ? stride : 0};
+}
+
+__device__ __forceinline__ float2 pair_cs(const int4& p, const float2* tab, const int pos[3]) {
+    return tab[p.x + p.y * pos[0] + p.z * pos[1] + p.w * pos[2]];
 }
 
 // Rotate a run of EP channels starting at c0 with (cos, sin) from `tab`
-// (the rope table, in LDS or in global memory); meta[j] = {base, stride, axis}
-// of rotary pair j, staged in LDS.
+// (the rope table, in LDS or in global memory); meta as built by pair_meta.
 template <int EP>
 __device__ __forceinline__ void rotate_piece(const int4* meta, const float2* tab, const int pos[3], int c0, float* x) {
 #pragma unroll
     for (int e = 0; e < EP; e += 2) {
-        const int4 p = meta[(c0 + e) >> 1];
-        const int coord = p.z == 0 ? pos[0] : (p.z == 1 ? pos[1] : pos[2]);
-        const float2 cs = tab[p.x + p.y * coord];
+        const float2 cs = pair_cs(meta[(c0 + e) >> 1], tab, pos);
         rotate_pair(x[e], x[e + 1], cs.x, cs.y);
     }
 }
@@ -135,9 +101,7 @@ __device__ __forceinline__ void rotate_piece_inverse(const int4* meta, const flo
                                                      float* x) {
 #pragma unroll
     for (int e = 0; e < EP; e += 2) {
-        const int4 p = meta[(c0 + e) >> 1];
-        const int coord = p.z == 0 ? pos[0] : (p.z == 1 ? pos[1] : pos[2]);
-        const float2 cs = tab[p.x + p.y * coord];
+        const float2 cs = pair_cs(meta[(c0 + e) >> 1], tab, pos);
         rotate_pair(x[e], x[e + 1], cs.x, -cs.y);
     }
 }
@@ -157,13 +121,12 @@ __device__ __forceinline__ void column_sums_w(const uint32_t* rows, const float*
         const float ws = w[s];
 #pragma unroll
         for (int j = 0; j < C::SJ; ++j) {
-            const int u = u0 + 64 * j;
-            if (u < C::DW) {
-                const uint32_t raw = rows[s * C::RD + u];
-                const T* x = reinterpret_cast<const T*>(&raw);
+            // Lanes past the last column re-read it (no divergent branch);
+            // their sums are never stored.
+            const uint32_t raw = rows[s * C::RD + min(u0 + 64 * j, C::DW - 1)];
+            const T* x = reinterpret_cast<const T*>(&raw);
 #pragma unroll
-                for (int c = 0; c < C::CPD; ++c) part[j][c] += ws * to_f32(x[c]);
-            }
+            for (int c = 0; c < C::CPD; ++c) part[j][c] += ws * to_f32(x[c]);
         }
     }
 #pragma unroll
@@ -178,15 +141,65 @@ __device__ __forceinline__ void column_sums_w(const uint32_t* rows, const float*
         for (int c = 0; c < C::CPD; ++c) out[j][c] += part[j][c];
 }
 
+// Round the EP channels of a piece to T in place (x then holds the rounded
+// values) and return them packed as one 16-byte piece.  bf16 pairs take one
+// packed round-to-nearest-even conversion each.
+template <typename T, int EP>
+__device__ __forceinline__ uint4 round_piece(float (&x)[EP]) {
+    uint4 raw;
+    T* t = reinterpret_cast<T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < EP; ++e) {
+        t[e] = from_f32<T>(x[e]);
+        x[e] = to_f32(t[e]);
+    }
+    return raw;
+}
+
+template <>
+__device__ __forceinline__ uint4 round_piece<__bf16, 8>(float (&x)[8]) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        w[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x[2 * t], x[2 * t + 1]}, bf16x2));
+        x[2 * t] = __uint_as_float(w[t] << 16);
+        x[2 * t + 1] = __uint_as_float(w[t] & 0xffff0000u);
+    }
+    return uint4{w[0], w[1], w[2], w[3]};
+}
+
+template <>
+__device__ __forceinline__ uint4 round_piece<_Float16, 8>(float (&x)[8]) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    uint32_t w[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const f16x2 r = __builtin_convertvector((f32x2){x[2 * t], x[2 * t + 1]}, f16x2);
+        w[t] = __builtin_bit_cast(uint32_t, r);
+        x[2 * t] = (float)r.x;
+        x[2 * t + 1] = (float)r.y;
+    }
+    return uint4{w[0], w[1], w[2], w[3]};
+}
+
+// Store the mean-pooled summary of one (batch * kv head bg, summary m) from
+// the per-lane partial column sums (lane (h, u) holds slot group h of column
+// dword u; the groups are summed here).
 template <typename T, int D>
-__device__ __forceinline__ void write_summary(const PoolDev& a, int64_t item, int lane, int count,
-                                              const float (&acck)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD],
-                                              const float (&accv)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD]) {
+__device__ __forceinline__ void write_summary(const PoolDev& a, int bg, int m, int lane, int count,
+                                              float (&acck)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD],
+                                              float (&accv)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD]) {
     typedef PoolCfg<T, D> C;
-    const int g = (int)(item % a.G);
-    const int64_t bm = item / a.G;
-    const int m = (int)(bm % a.Mp), b = (int)(bm / a.Mp);
-    const int64_t bg = (int64_t)b * a.G + g;
+#pragma unroll
+    for (int o = C::LW; o < 64; o <<= 1)
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j)
+#pragma unroll
+            for (int c = 0; c < C::CPD; ++c) {
+                acck[j][c] += __shfl_xor(acck[j][c], o);
+                accv[j][c] += __shfl_xor(accv[j][c], o);
+            }
     // The coarse stage divides the group sum by the count (compression.py:42-43).
     T* sk = reinterpret_cast<T*>(a.sk) + ((int64_t)bg * a.Mp + m) * D;
     T* svt = reinterpret_cast<T*>(a.svt) + (((int64_t)bg * (a.Mp / 32) + m / 32) * D) * 32 + (m & 31);
@@ -210,7 +223,75 @@ __device__ __forceinline__ void write_summary(const PoolDev& a, int64_t item, in
     // like their bit patterns, so an integer max is an exact float max.
     const float norm = sqrtf(wave_sum(sq)) * (1.f + 1e-6f);
     if (lane == 0 && m < a.M)
-        atomicMax(reinterpret_cast<int*>(a.sk_norm_max) + bg * kNormSlots + (m % kNormSlots), __float_as_int(norm));
+        atomicMax(reinterpret_cast<int*>(a.sk_norm_max) + (int64_t)bg * kNormSlots + (m % kNormSlots),
+                  __float_as_int(norm));
+}
+
+// LDS plan of the forward: pair metadata [D/2] int4, per-piece "contiguous
+// table run" flags [PFN] int, weights [D], biases [64], the rope table when
+// it fits, then per wave one row buffer (64 x RD dwords: the K rows, then the
+// V rows) and the 64 slot weights.
+template <typename T, int D>
+struct PoolFwdCfg {
+    typedef PoolCfg<T, D> C;
+    static constexpr int PFN = (C::PPR + 3) & ~3;
+    static constexpr size_t FIXED = (size_t)(D / 2) * 16 + PFN * 4 + D * 4 + 64 * 4;
+    static constexpr int WAVE_DW = 64 * C::RD + 64;
+    // Small rows: the V pieces are loaded with the K pieces and held in
+    // registers until the V rows are staged; large rows load each tensor in
+    // chunks of CH pieces per lane right before staging it.
+    static constexpr bool KV_TOGETHER = C::PPR <= 8;
+    static constexpr int CH = KV_TOGETHER ? C::PPR : 4;
+};
+
+// Issue the loads of pieces [i0, i0 + CH) of the lane's share of a fine
+// block's rows of one tensor (lane l holds pieces i * 64 + l of the 64 x PPR
+// piece grid).  Empty slots read row 0; their slot weight is exactly 0, so
+// they add 0 * row 0 to the sums, as the reference's masked product does
+// (compression.py:38-39).
+template <typename T, int D, int CH>
+__device__ __forceinline__ void pool_load(const T* X, int64_t xsn, int idx, int i0, int lane, u32x4 (&r)[CH]) {
+    typedef PoolCfg<T, D> C;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int q = (i0 + i) * 64 + lane, s = q / C::PPR, p = q - s * C::PPR;
+        const int tok = max(__shfl(idx, s), 0);
+        r[i] = *reinterpret_cast<const u32x4*>(X + (int64_t)tok * xsn + p * C::EP);
+    }
+}
+
+// Write pieces [i0, i0 + CH) to the row buffer.
+template <typename T, int D, int CH>
+__device__ __forceinline__ void pool_stage(uint32_t* rows, int i0, int lane, const u32x4 (&r)[CH]) {
+    typedef PoolCfg<T, D> C;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+        const int q = (i0 + i) * 64 + lane, s = q / C::PPR, p = q - s * C::PPR;
+        *reinterpret_cast<u32x4*>(rows + s * C::RD + p * 4) = r[i];
+    }
+}
+
+// Column sums over the row buffer with the slot weights in LDS: lane (h, u)
+// adds slots h, h + S, ... of column dword u into out (per-lane partials; the
+// slot groups are summed when the summary is stored).  Lanes past the last
+// column re-read it (no divergent branch); their sums are never stored.
+template <typename T, int D>
+__device__ __forceinline__ void pool_column_sums(const uint32_t* rows, const float* lw, int lane,
+                                                 float (&out)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD]) {
+    typedef PoolCfg<T, D> C;
+    const int h = lane / C::LW, u0 = lane % C::LW;
+#pragma unroll 8
+    for (int i = 0; i < 64 / C::S; ++i) {
+        const int s = i * C::S + h;
+        const float ws = lw[s];
+#pragma unroll
+        for (int j = 0; j < C::SJ; ++j) {
+            const uint32_t raw = rows[s * C::RD + min(u0 + 64 * j, C::DW - 1)];
+            const T* x = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+            for (int c = 0; c < C::CPD; ++c) out[j][c] += ws * to_f32(x[c]);
+        }
+    }
 }
 
 // Persistent: wave w of block k takes items k * waves + w, + waves * grid, ...
@@ -222,20 +303,32 @@ __device__ __forceinline__ void write_summary(const PoolDev& a, int64_t item, in
 template <typename T, int D, bool TAB_LDS>
 __global__ __launch_bounds__(256) void k_pool_fwd(PoolDev a) {
     typedef PoolCfg<T, D> C;
-    constexpr int EP = C::EP, PPR = C::PPR, CPD = C::CPD;
+    typedef PoolFwdCfg<T, D> F;
+    constexpr int EP = C::EP, PPR = C::PPR, CPD = C::CPD, CH = F::CH;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int waves = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    // LDS: pair metadata [D/2] int4, weights [D], biases [64], the rope table
-    // (TAB_LDS), then one row buffer per wave.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     int4* meta = reinterpret_cast<int4*>(smem_raw);
-    float* lweight = reinterpret_cast<float*>(meta + D / 2);
+    int* prun = reinterpret_cast<int*>(meta + D / 2);
+    float* lweight = reinterpret_cast<float*>(prun + F::PFN);
     float* lbias = lweight + D;
     float2* ltab = reinterpret_cast<float2*>(lbias + 64);
     const int tab_dw = TAB_LDS ? ((a.table_entries * 2 + 3) & ~3) : 0;
-    uint32_t* rows = reinterpret_cast<uint32_t*>(ltab) + tab_dw + wave * C::WAVE_DW;
-    for (int j = threadIdx.x; j < D / 2; j += blockDim.x)
-        meta[j] = int4{a.rope.pairs[3 * j], a.rope.pairs[3 * j + 1], a.rope.pairs[3 * j + 2], 0};
+    uint32_t* rows = reinterpret_cast<uint32_t*>(ltab) + tab_dw + wave * F::WAVE_DW;
+    float* lw = reinterpret_cast<float*>(rows + 64 * C::RD);
+    for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(a.rope.pairs, j);
+    // Piece p is a table run when its pairs read consecutive entries with one
+    // stride vector: entry(j0 + t) = entry(j0) + t for every position.
+    for (int p = threadIdx.x; p < PPR; p += blockDim.x) {
+        const int j0 = p * EP / 2;
+        const int4 m0 = pair_meta(a.rope.pairs, j0);
+        int run = 1;
+        for (int t = 1; t < EP / 2; ++t) {
+            const int4 mt = pair_meta(a.rope.pairs, j0 + t);
+            run &= mt.x == m0.x + t && mt.y == m0.y && mt.z == m0.z && mt.w == m0.w;
+        }
+        prun[p] = run;
+    }
     for (int c = threadIdx.x; c < D; c += blockDim.x) lweight[c] = a.weight[c];
     for (int c = threadIdx.x; c < 64; c += blockDim.x) lbias[c] = c < a.V ? a.bias[c] : 0.f;
     const float2* tab = a.rope.table;
@@ -245,81 +338,116 @@ __global__ __launch_bounds__(256) void k_pool_fwd(PoolDev a) {
     }
     __syncthreads();
 
-    const int64_t total = (int64_t)a.B * a.G * a.Mp;
-    const int64_t stride = (int64_t)gridDim.x * waves;
-    for (int64_t item = (int64_t)blockIdx.x * waves + wave; item < total; item += stride) {
+    // Item indices fit in 32 bits (checked on the host), so the wave-uniform
+    // item arithmetic is 32-bit scalar code.
+    const unsigned total = (unsigned)a.B * a.G * a.Mp;
+    const unsigned stride = gridDim.x * waves;
+    // Block-table row of an item's first fine block (-1 past the end or for a
+    // padding summary).  The next item's row is fetched right after this
+    // item's first K / V loads (so waiting for those leaves it in flight) and
+    // arrives while this item is reduced: the table read is off the item's
+    // critical path.
+    auto first_row = [&](unsigned it) -> int {
+        if (it >= total) return -1;
+        const unsigned mm = (it / a.G) % a.Mp;
+        return (mm < (unsigned)a.M && lane < a.V) ? a.blocks[(int64_t)mm * a.P * a.V + lane] : -1;
+    };
+    unsigned item = blockIdx.x * waves + wave;
+    int idx_first = first_row(item);
+    for (; item < total; item += stride) {
+        int idx_next = -1;
+        bool fetched = false;
         const int g = (int)(item % a.G);
-        const int64_t bm = item / a.G;
+        const unsigned bm = item / a.G;
         const int m = (int)(bm % a.Mp), b = (int)(bm / a.Mp);
+        const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
+        const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
         float acck[C::SJ][CPD], accv[C::SJ][CPD];
 #pragma unroll
         for (int j = 0; j < C::SJ; ++j)
 #pragma unroll
             for (int c = 0; c < CPD; ++c) acck[j][c] = accv[j][c] = 0.f;
         int count = 0;
-        const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
-        const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
         const int f_end = m < a.M ? min(a.F, (m + 1) * a.P) : 0;
         for (int f = m * a.P; f < f_end; ++f) {
-            const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
+            const int idx = f == m * a.P ? idx_first : (lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1);
             if (__ballot(idx >= 0) == 0) continue;  // empty fine block: no mass, no count
             ++count;
-            // Every load of the block is in flight before any is used; empty
-            // slots read row 0 and are zeroed afterwards (straight-line code).
             int pos[3];
             rope_position32(a.rope, max(idx, 0), pos);
-            uint4 kr[PPR], vr[PPR];
-            int tok[PPR];
-#pragma unroll
-            for (int i = 0; i < PPR; ++i) tok[i] = __shfl(idx, (i * 64 + lane) / PPR);
-#pragma unroll
-            for (int i = 0; i < PPR; ++i) {
-                const int q = i * 64 + lane, p = q - (q / PPR) * PPR;
-                const int t = max(tok[i], 0);
-                kr[i] = *reinterpret_cast<const uint4*>(K + (int64_t)t * a.ksn + p * EP);
-                vr[i] = *reinterpret_cast<const uint4*>(Vv + (int64_t)t * a.vsn + p * EP);
+            u32x4 kr[CH], vr[CH];
+            if constexpr (F::KV_TOGETHER) {
+                // Every load of the block is in flight before any is used.
+                pool_load<T, D, CH>(K, a.ksn, idx, 0, lane, kr);
+                pool_load<T, D, CH>(Vv, a.vsn, idx, 0, lane, vr);
+                if (!fetched) idx_next = first_row(item + stride);
+                fetched = true;
+                pool_stage<T, D, CH>(rows, 0, lane, kr);
+            } else {
+                if (!fetched) idx_next = first_row(item + stride);
+                fetched = true;
+#pragma unroll 1
+                for (int i0 = 0; i0 < PPR; i0 += CH) {
+                    pool_load<T, D, CH>(K, a.ksn, idx, i0, lane, kr);
+                    pool_stage<T, D, CH>(rows, i0, lane, kr);
+                }
             }
-#pragma unroll
-            for (int i = 0; i < PPR; ++i) {
-                if (tok[i] < 0) kr[i] = vr[i] = uint4{0u, 0u, 0u, 0u};
-            }
-            stage_rows<C>(rows, kr, lane);
             wave_lds_sync();
             // One lane per slot: rotate the slot's K row in place, round it to
             // the storage type, and form its logit (compression.py:31-35):
-            // (k . w) / tau + bias_s.  Rotary pair metadata is wave-uniform here.
+            // (k . w) / tau + bias_s.
             float logit = -INFINITY;
             if (idx >= 0) {
                 float dot = 0.f;
-#pragma unroll 1  // one piece at a time keeps the table reads from occupying registers
+#pragma unroll 1
                 for (int p = 0; p < PPR; ++p) {
-                    uint4 raw = *reinterpret_cast<const uint4*>(rows + lane * C::RD + p * 4);
-                    T* kt = reinterpret_cast<T*>(&raw);
+                    uint32_t* rp = rows + lane * C::RD + p * 4;
+                    const u32x4 raw = *reinterpret_cast<const u32x4*>(rp);
+                    const T* kt = reinterpret_cast<const T*>(&raw);
                     float kx[EP];
 #pragma unroll
                     for (int e = 0; e < EP; ++e) kx[e] = to_f32(kt[e]);
-                    rotate_piece<EP>(meta, tab, pos, p * EP, kx);
+                    const int j0 = p * EP / 2;
+                    const int4 m0 = meta[j0];
+                    const int e0 = m0.x + __mul24(m0.y, pos[0]) + __mul24(m0.z, pos[1]) + __mul24(m0.w, pos[2]);
+                    float2 cs[EP / 2];
+                    if (__builtin_amdgcn_readfirstlane(prun[p])) {
 #pragma unroll
-                    for (int e = 0; e < EP; ++e) {
-                        kt[e] = from_f32<T>(kx[e]);
-                        dot += to_f32(kt[e]) * lweight[p * EP + e];
+                        for (int t = 0; t < EP / 2; ++t) cs[t] = tab[e0 + t];
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < EP / 2; ++t) cs[t] = pair_cs(meta[j0 + t], tab, pos);
                     }
-                    *reinterpret_cast<uint4*>(rows + lane * C::RD + p * 4) = raw;
+#pragma unroll
+                    for (int t = 0; t < EP / 2; ++t) rotate_pair(kx[2 * t], kx[2 * t + 1], cs[t].x, cs[t].y);
+                    *reinterpret_cast<uint4*>(rp) = round_piece<T, EP>(kx);
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) dot += kx[e] * lweight[p * EP + e];
                 }
                 logit = dot * a.inv_tau + lbias[lane];
             }
             const float mx = wave_max(logit);
             const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
-            const float w = ex / wave_sum(ex);
-            wave_lds_sync();  // rotated rows are read across lanes below
-            column_sums<C, T>(rows, w, lane, acck);
+            lw[lane] = ex / wave_sum(ex);
+            wave_lds_sync();  // rotated rows and slot weights are read across lanes below
+            pool_column_sums<T, D>(rows, lw, lane, acck);
+            wave_lds_sync();  // the V rows overwrite the K rows
+            if constexpr (F::KV_TOGETHER) {
+                pool_stage<T, D, CH>(rows, 0, lane, vr);
+            } else {
+#pragma unroll 1
+                for (int i0 = 0; i0 < PPR; i0 += CH) {
+                    pool_load<T, D, CH>(Vv, a.vsn, idx, i0, lane, vr);
+                    pool_stage<T, D, CH>(rows, i0, lane, vr);
+                }
+            }
             wave_lds_sync();
-            stage_rows<C>(rows, vr, lane);
-            wave_lds_sync();
-            column_sums<C, T>(rows, w, lane, accv);
+            pool_column_sums<T, D>(rows, lw, lane, accv);
             wave_lds_sync();  // the next fine block overwrites the rows
         }
-        write_summary<T, D>(a, item, lane, count, acck, accv);
+        if (!fetched) idx_next = first_row(item + stride);
+        write_summary<T, D>(a, b * a.G + g, m, lane, count, acck, accv);
+        idx_first = idx_next;
     }
 }
 
@@ -349,7 +477,7 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
     constexpr int WAVE_DW = 2 * 64 * C::RD + 2 * D + 64;  // K rows, V rows, g_k, g_v, slot weights
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int waves = blockDim.x >> 6;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     int4* meta = reinterpret_cast<int4*>(smem_raw);
     float* lweight = reinterpret_cast<float*>(meta + D / 2);
     float* lbias = lweight + D;
@@ -361,7 +489,7 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
     float* gv = gk + D;
     float* lw = gv + D;
     for (int j = threadIdx.x; j < D / 2; j += blockDim.x)
-        meta[j] = int4{a.rope.pairs[3 * j], a.rope.pairs[3 * j + 1], a.rope.pairs[3 * j + 2], 0};
+        meta[j] = pair_meta(a.rope.pairs, j);
     for (int c = threadIdx.x; c < D; c += blockDim.x) lweight[c] = a.weight[c];
     for (int c = threadIdx.x; c < 64; c += blockDim.x) lbias[c] = c < a.V ? a.bias[c] : 0.f;
     const float2* tab = a.rope.table;
@@ -371,12 +499,12 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
     }
     __syncthreads();
 
-    const int64_t total = (int64_t)a.B * a.G * a.Mp;
-    const int64_t stride = (int64_t)gridDim.x * waves;
-    const int64_t slice = (int64_t)a.B * a.G * a.Mp * D;  // one split of the partials
-    for (int64_t item = (int64_t)blockIdx.x * waves + wave; item < total; item += stride) {
+    const unsigned total = (unsigned)a.B * a.G * a.Mp;
+    const unsigned stride = gridDim.x * waves;
+    const int64_t slice = (int64_t)total * D;  // one split of the partials
+    for (unsigned item = blockIdx.x * waves + wave; item < total; item += stride) {
         const int g = (int)(item % a.G);
-        const int64_t bm = item / a.G;
+        const unsigned bm = item / a.G;
         const int m = (int)(bm % a.Mp), b = (int)(bm / a.Mp);
         const int64_t bg = (int64_t)b * a.G + g;
         const int f0 = m * a.P, f_end = m < a.M ? min(a.F, (m + 1) * a.P) : 0;
@@ -490,7 +618,7 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
             wave_lds_sync();  // the next fine block overwrites the rows
         }
         // Partials of this item: dw (column dwords of group 0) and db (one per slot).
-        float* dwp = bd.dw_part + item * D;
+        float* dwp = bd.dw_part + (int64_t)item * D;
 #pragma unroll
         for (int j = 0; j < C::SJ; ++j) {
             const int u = lane + 64 * j;
@@ -498,7 +626,7 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
 #pragma unroll
                 for (int c = 0; c < CPD; ++c) dwp[u * CPD + c] = dwacc[j][c];
         }
-        if (lane < a.V) bd.db_part[item * a.V + lane] = dbacc;
+        if (lane < a.V) bd.db_part[(int64_t)item * a.V + lane] = dbacc;
     }
 }
 
@@ -550,14 +678,15 @@ inline int pool_waves(size_t fixed, size_t per_wave) {
 }
 
 template <typename T, int D>
-void launch_pool_t(const PoolDev& d, int64_t items, hipStream_t s) {
-    // Four waves (four kv heads of a summary) per block; a persistent grid of
-    // as many blocks as stay resident, each striding over the items.
+void launch_pool_t(const PoolDev& d, hipStream_t s) {
+    // Up to four waves (the kv heads of a summary) per block; a persistent
+    // grid of as many blocks as stay resident, each striding over the items.
     const bool tab_lds = d.table_entries * 8 <= kTableLdsBytes;
     const size_t tab_bytes = tab_lds ? (size_t)((d.table_entries * 2 + 3) & ~3) * 4 : 0;
-    const size_t fixed = (size_t)(D / 2) * 16 + (size_t)D * 4 + 64 * 4;
-    const int waves = pool_waves(fixed + tab_bytes, (size_t)PoolCfg<T, D>::WAVE_DW * 4);
-    const size_t smem = fixed + tab_bytes + (size_t)PoolCfg<T, D>::WAVE_DW * 4 * waves;
+    const size_t fixed = PoolFwdCfg<T, D>::FIXED + tab_bytes;
+    const size_t per_wave = (size_t)PoolFwdCfg<T, D>::WAVE_DW * 4;
+    const int waves = pool_waves(fixed, per_wave);
+    const size_t smem = fixed + per_wave * waves;
     int dev = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -565,6 +694,7 @@ void launch_pool_t(const PoolDev& d, int64_t items, hipStream_t s) {
         (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_fwd<T, D, true>, 64 * waves, smem);
     else
         (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_fwd<T, D, false>, 64 * waves, smem);
+    const int64_t items = (int64_t)d.B * d.G * d.Mp;
     const int64_t resident = (int64_t)std::max(1, cus) * std::max(1, per_cu);
     const int64_t needed = cdiv(items, waves);
     // Equal shares: the fewest rounds that cover every item, spread evenly.
@@ -577,11 +707,11 @@ void launch_pool_t(const PoolDev& d, int64_t items, hipStream_t s) {
 }
 
 template <int D>
-void launch_pool(const PoolDev& d, int dtype, int64_t items, hipStream_t s) {
+void launch_pool(const PoolDev& d, int dtype, hipStream_t s) {
     switch (dtype) {
-        case P3D_F32: launch_pool_t<float, D>(d, items, s); break;
-        case P3D_F16: launch_pool_t<_Float16, D>(d, items, s); break;
-        default: launch_pool_t<__bf16, D>(d, items, s); break;
+        case P3D_F32: launch_pool_t<float, D>(d, s); break;
+        case P3D_F16: launch_pool_t<_Float16, D>(d, s); break;
+        default: launch_pool_t<__bf16, D>(d, s); break;
     }
 }
 
@@ -601,13 +731,15 @@ int fill_pool(const p3d_pool_args* args, PoolDev& d) {
     P3D_REQUIRE(a.dtype >= P3D_F32 && a.dtype <= P3D_BF16, "unknown dtype");
     P3D_REQUIRE(a.head_dim == 16 || a.head_dim == 32 || a.head_dim == 48 || a.head_dim == 64 || a.head_dim == 128,
                 "head_dim must be 16, 32, 48, 64 or 128");
+    P3D_REQUIRE(a.batch >= 1 && a.kv_heads >= 1 && a.tokens >= 1 && a.fine_blocks >= 1, "empty pooling problem");
     P3D_REQUIRE(a.slots >= 1 && a.slots <= 64 && a.pool_size >= 1 && a.pool_size <= 32, "bad pooling shape");
     P3D_REQUIRE(a.summaries == (a.fine_blocks + a.pool_size - 1) / a.pool_size, "summaries != ceil(F/P)");
     P3D_REQUIRE(view_ok(a.kg, es) && view_ok(a.vg, es), "kg/vg rows must be 16-byte aligned");
     P3D_REQUIRE(a.sk && a.svt && a.sk_norm_max && a.blocks && a.weight && a.bias && a.rope.table && a.rope.pairs,
                 "null pointer argument");
     P3D_REQUIRE(a.rope.packed || a.rope.coords, "rope needs coords unless packed");
-    P3D_REQUIRE(a.rope.table_entries >= 1, "rope table_entries must be positive");
+    P3D_REQUIRE(a.rope.table_entries >= 1 && a.rope.table_entries < (1 << 23),
+                "rope table_entries must be in [1, 2^23)");
     P3D_REQUIRE(a.temperature > 0.f, "temperature must be positive");
     P3D_REQUIRE(a.key_scale > 0.f, "key_scale must be positive");
     d = PoolDev{};
@@ -619,6 +751,7 @@ int fill_pool(const p3d_pool_args* args, PoolDev& d) {
     d.P = a.pool_size;
     d.M = a.summaries;
     d.Mp = (int)cdiv(a.summaries, 32) * 32;
+    P3D_REQUIRE((int64_t)a.batch * a.kv_heads * d.Mp < ((int64_t)1 << 31), "batch * kv_heads * summaries too large");
     d.inv_tau = 1.f / a.temperature;
     d.key_scale = a.key_scale;
     d.kg = (const char*)a.kg.data;
@@ -680,13 +813,12 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     hipStream_t s = as_stream(stream);
     const int bgn = a.batch * a.kv_heads * kNormSlots;
     k_zero_f32<<<(unsigned)cdiv(bgn, 256), 256, 0, s>>>(a.sk_norm_max, bgn);
-    const int64_t items = (int64_t)d.B * d.G * d.Mp;
     switch (a.head_dim) {
-        case 16: launch_pool<16>(d, a.dtype, items, s); break;
-        case 32: launch_pool<32>(d, a.dtype, items, s); break;
-        case 48: launch_pool<48>(d, a.dtype, items, s); break;
-        case 64: launch_pool<64>(d, a.dtype, items, s); break;
-        default: launch_pool<128>(d, a.dtype, items, s); break;
+        case 16: launch_pool<16>(d, a.dtype, s); break;
+        case 32: launch_pool<32>(d, a.dtype, s); break;
+        case 48: launch_pool<48>(d, a.dtype, s); break;
+        case 64: launch_pool<64>(d, a.dtype, s); break;
+        default: launch_pool<128>(d, a.dtype, s); break;
     }
     return check_launch("p3d_pool_fwd");
 }

@@ -58,9 +58,12 @@ __device__ __forceinline__ void rope_position32(const RopeDev& r, int n, int pos
         pos[1] = 0;
         pos[2] = 0;
     } else {
-        pos[0] = (int)r.coords[3 * (int64_t)n + 0];
-        pos[1] = (int)r.coords[3 * (int64_t)n + 1];
-        pos[2] = (int)r.coords[3 * (int64_t)n + 2];
+        // Coordinates are non-negative and below 2^31: read the low words of
+        // the int64 entries only (no dead high halves held by a load).
+        const int32_t* c = reinterpret_cast<const int32_t*>(r.coords) + 6 * (int64_t)n;
+        pos[0] = c[0];
+        pos[1] = c[2];
+        pos[2] = c[4];
     }
 }
 

@@ -123,13 +123,46 @@ __device__ __forceinline__ constexpr int kperm(int rho) {
 // Value held by lane l ^ 32.
 __device__ __forceinline__ float swap_half(float x) { return __shfl_xor(x, 32); }
 
+// x of the lane that the DPP control CTRL selects (a permutation within each
+// 16-lane row: every source lane exists, so `old` is never taken).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// x of lane l ^ 16 and of lane l ^ 32, through the gfx950 row swaps (no LDS).
+// permlane16_swap(a, b) exchanges the odd 16-lane rows of a with the even
+// rows of b; with a = b = x, an even-row lane finds its partner's value in the
+// second result and an odd-row lane in the first.  permlane32_swap does the
+// same for the two 32-lane halves.
+__device__ __forceinline__ float lane_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((__lane_id() & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((__lane_id() & 32) ? r[0] : r[1]);
+}
+
+// All-reduce over the 64 lanes without LDS: partners l ^ 1, l ^ 2 (quad_perm),
+// l ^ 7 within 8 (row_half_mirror), l ^ 15 within 16 (row_mirror), l ^ 16 and
+// l ^ 32.  Each step combines two disjoint groups of equal size, and the
+// operations are commutative, so every lane ends with the same bits.
 __device__ __forceinline__ float wave_max(float x) {
-    for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-    return x;
+    x = fmaxf(x, dpp_move<0xB1>(x));
+    x = fmaxf(x, dpp_move<0x4E>(x));
+    x = fmaxf(x, dpp_move<0x141>(x));
+    x = fmaxf(x, dpp_move<0x140>(x));
+    x = fmaxf(x, lane_xor16(x));
+    return fmaxf(x, lane_xor32(x));
 }
 __device__ __forceinline__ float wave_sum(float x) {
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
-    return x;
+    x += dpp_move<0xB1>(x);
+    x += dpp_move<0x4E>(x);
+    x += dpp_move<0x141>(x);
+    x += dpp_move<0x140>(x);
+    x += lane_xor16(x);
+    return x + lane_xor32(x);
 }
 __device__ __forceinline__ int wave_max_i(int x) {
     for (int o = 32; o >= 1; o >>= 1) x = max(x, __shfl_xor(x, o));

@@ -81,7 +81,8 @@ __device__ __forceinline__ int4 pair_meta(const int32_t* pairs, int j) {
 }
 
 __device__ __forceinline__ float2 pair_cs(const int4& p, const float2* tab, const int pos[3]) {
-    return tab[p.x + p.y * pos[0] + p.z * pos[1] + p.w * pos[2]];
+    // Table indices are below 2^23 (checked on the host): 24-bit products.
+    return tab[p.x + __mul24(p.y, pos[0]) + __mul24(p.z, pos[1]) + __mul24(p.w, pos[2])];
 }
 
 // Rotate a run of EP channels starting at c0 with (cos, sin) from `tab`
@@ -183,40 +184,135 @@ __device__ __forceinline__ uint4 round_piece<_Float16, 8>(float (&x)[8]) {
     return uint4{w[0], w[1], w[2], w[3]};
 }
 
-// Store the mean-pooled summary of one (batch * kv head bg, summary m) from
-// the per-lane partial column sums (lane (h, u) holds slot group h of column
-// dword u; the groups are summed here).
+// ------------------------------------------------------------------ forward
+//
+// One wave pools one (batch, kv head, summary) item at a time.  The K and V
+// rows of a fine block are loaded with 16 bytes per lane and consecutive
+// lanes on consecutive pieces of a row, so one load instruction covers whole
+// row spans, and are written to the wave's LDS buffer as rows.  The loads of
+// the wave's next fine block are issued into the same registers right after
+// that, before any arithmetic: the HBM latency of one step hides behind the
+// arithmetic of the step before it.  Each lane then takes its own slot's
+// rows (lane = slot): rotate the key, round it to the storage type, form the
+// slot logit, and take the slot softmax as a wave reduction.
+//
+// The weighted sums over the 64 slots, sum_s a_s k_s and sum_s a_s v_s, are
+// a matrix-vector product.  For 2-byte types the lanes write their rounded
+// K row and their V row as columns of an LDS matrix X^T [2D channels][64
+// slots], and the MFMA computes W X with W = [hi(a); lo(a)], the weights
+// split into two storage-type parts (hi = round(a), lo = round(a - hi)):
+// each product of two storage-type values is exact in fp32 and the sum
+// carries a with 16 significant bits.  fp32 rows are summed across lanes by
+// a reduce-scatter butterfly instead.
+
 template <typename T, int D>
-__device__ __forceinline__ void write_summary(const PoolDev& a, int bg, int m, int lane, int count,
-                                              float (&acck)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD],
-                                              float (&accv)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD]) {
-    typedef PoolCfg<T, D> C;
+struct PoolRowCfg {
+    static constexpr bool MF = sizeof(T) == 2;       // MFMA slot sums
+    static constexpr int EP = Piece<T>::N;          // elements per 16-byte piece
+    static constexpr int PPR = D / EP;               // pieces per row
+    static constexpr int PFN = (PPR + 3) & ~3;       // run flags, padded to 16 bytes
+    static constexpr int RB = D * (int)sizeof(T);    // row bytes
+    // X^T row stride: 64 slots plus 16 bytes, so the 16-byte operand reads
+    // of 16 consecutive channel rows start in distinct bank groups.
+    static constexpr int XS = 64 * (int)sizeof(T) + 16;
+    static constexpr int XT_BYTES = 2 * D * XS;      // the K rows / V rows are staged inside it
+    // MFMA path: X^T, then the weight rows hi, lo and a zero row (64 slots each).
+    static constexpr int WAVE_BYTES = MF ? XT_BYTES + 3 * 64 * 2 : 2 * 64 * RB;
+    static constexpr int MAX_WAVES = (159 * 1024) / WAVE_BYTES < 8 ? (159 * 1024) / WAVE_BYTES : 8;
+    static constexpr int VOFF = MF ? D * XS : 64 * RB;  // where the V rows are staged
+    static constexpr int NT = 2 * D / 32;            // 32-channel MFMA tiles of [k; v]
+    static constexpr int NCH = D / 16;               // 16-channel chunks of the butterfly
+    static constexpr int PPC = 16 / EP;              // pieces per chunk
+    static constexpr int NACC = MF ? NT : NCH;       // per-lane partial sums
+    static constexpr size_t FIXED = (size_t)(D / 2) * 16 + PFN * 4 + D * 4 + 64 * 4;
+};
+
+// One halving step of the butterfly between lanes l and l ^ 32 (rows of 32
+// lanes swapped): the lower half ends with a summed over the pair, the upper
+// half with b summed over the pair.
+__device__ __forceinline__ float halve32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The same between lanes l and l ^ 16 (odd and even 16-lane rows swapped).
+__device__ __forceinline__ float halve16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The same within a row through a DPP lane permutation CTRL that pairs lanes
+// across one lane bit; `upper` is that bit of this lane.
+template <int CTRL>
+__device__ __forceinline__ float halve_dpp(float a, float b, bool upper) {
+    const float keep = upper ? b : a, send = upper ? a : b;
+    return keep + dpp_move<CTRL>(send);
+}
+
+// Sums k[0..15] and v[0..15] over the 64 lanes of the wave.  Lane l ends
+// with the full sum of tensor (l bit 5: 0 = k, 1 = v) at channel
+// 8 b4 + 4 b3 + 2 b2 + b1 (bits of l); lanes l and l ^ 1 hold the same value.
+// The pairings are l ^ 32, l ^ 16, l ^ 8 (row_ror:8), l ^ 7 (row_half_mirror,
+// splitting on bit 2), l ^ 2 and l ^ 1 (quad_perm); their XOR span is the
+// whole wave, so every value is a sum over all 64 lanes.
+__device__ __forceinline__ float butterfly_sum(const float (&k)[16], const float (&v)[16], int lane) {
+    float u[16];
 #pragma unroll
-    for (int o = C::LW; o < 64; o <<= 1)
+    for (int j = 0; j < 16; ++j) u[j] = halve32(k[j], v[j]);
+    float w[8];
 #pragma unroll
-        for (int j = 0; j < C::SJ; ++j)
+    for (int j = 0; j < 8; ++j) w[j] = halve16(u[j], u[8 + j]);
+    float x[4];
 #pragma unroll
-            for (int c = 0; c < C::CPD; ++c) {
-                acck[j][c] += __shfl_xor(acck[j][c], o);
-                accv[j][c] += __shfl_xor(accv[j][c], o);
-            }
-    // The coarse stage divides the group sum by the count (compression.py:42-43).
+    for (int j = 0; j < 4; ++j) x[j] = halve_dpp<0x128>(w[j], w[4 + j], lane & 8);
+    float y[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) y[j] = halve_dpp<0x141>(x[j], x[2 + j], lane & 4);
+    const float z = halve_dpp<0x4E>(y[0], y[1], lane & 2);
+    return z + dpp_move<0xB1>(z);
+}
+
+template <typename T, int EP>
+__device__ __forceinline__ void unpack_piece(const u32x4& raw, float (&x)[EP]) {
+    const T* t = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < EP; ++e) x[e] = to_f32(t[e]);
+}
+
+// Store the summary of (batch * kv head bg, summary m) from the lane's sums
+// acc (over the fine blocks of the summary).  MFMA layout: lanes 0..31 hold
+// channel 32 t + l of [k; v] in acc[t].  Butterfly layout: lane l holds
+// channel 16 k + 8 b4 + 4 b3 + 2 b2 + b1 of tensor b5 in acc[k] (even lanes
+// store).  The coarse stage divides the group sum by the count of non-empty
+// fine blocks (compression.py:42-43); keys are stored times key_scale.
+template <typename T, int D>
+__device__ __forceinline__ void store_summary(const PoolDev& a, int bg, int m, int lane, int count,
+                                              const float (&acc)[PoolRowCfg<T, D>::NACC]) {
+    typedef PoolRowCfg<T, D> C;
     T* sk = reinterpret_cast<T*>(a.sk) + ((int64_t)bg * a.Mp + m) * D;
     T* svt = reinterpret_cast<T*>(a.svt) + (((int64_t)bg * (a.Mp / 32) + m / 32) * D) * 32 + (m & 31);
     float sq = 0.f;
 #pragma unroll
-    for (int j = 0; j < C::SJ; ++j) {
-        const int u = lane + 64 * j;
-        if (lane < C::LW && u < C::DW) {
-            uint32_t word;
-            T* x = reinterpret_cast<T*>(&word);
-#pragma unroll
-            for (int c = 0; c < C::CPD; ++c) {
-                x[c] = from_f32<T>(count ? acck[j][c] / (float)count * a.key_scale : 0.f);
-                sq += to_f32(x[c]) * to_f32(x[c]);
-                svt[(u * C::CPD + c) * 32] = from_f32<T>(count ? accv[j][c] / (float)count : 0.f);
-            }
-            *reinterpret_cast<uint32_t*>(sk + u * C::CPD) = word;
+    for (int k = 0; k < C::NACC; ++k) {
+        int c;
+        bool is_v, writer;
+        if constexpr (C::MF) {
+            const int cc = 32 * k + lane;
+            is_v = cc >= D;
+            c = is_v ? cc - D : cc;
+            writer = lane < 32;
+        } else {
+            c = 16 * k + 8 * ((lane >> 4) & 1) + 4 * ((lane >> 3) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 1) & 1);
+            is_v = lane & 32;
+            writer = !(lane & 1);
+        }
+        const float mean = count ? acc[k] / (float)count : 0.f;
+        if (writer && !is_v) {
+            const T x = from_f32<T>(mean * a.key_scale);
+            sk[c] = x;
+            sq += to_f32(x) * to_f32(x);
+        } else if (writer) {
+            svt[c * 32] = from_f32<T>(mean);
         }
     }
     // Norm of the stored (rounded) summary key; non-negative floats order
@@ -227,95 +323,66 @@ __device__ __forceinline__ void write_summary(const PoolDev& a, int bg, int m, i
                   __float_as_int(norm));
 }
 
-// LDS plan of the forward: pair metadata [D/2] int4, per-piece "contiguous
-// table run" flags [PFN] int, weights [D], biases [64], the rope table when
-// it fits, then per wave one row buffer (64 x RD dwords: the K rows, then the
-// V rows) and the 64 slot weights.
-template <typename T, int D>
-struct PoolFwdCfg {
-    typedef PoolCfg<T, D> C;
-    static constexpr int PFN = (C::PPR + 3) & ~3;
-    static constexpr size_t FIXED = (size_t)(D / 2) * 16 + PFN * 4 + D * 4 + 64 * 4;
-    static constexpr int WAVE_DW = 64 * C::RD + 64;
-    // Small rows: the V pieces are loaded with the K pieces and held in
-    // registers until the V rows are staged; large rows load each tensor in
-    // chunks of CH pieces per lane right before staging it.
-    static constexpr bool KV_TOGETHER = C::PPR <= 8;
-    static constexpr int CH = KV_TOGETHER ? C::PPR : 4;
-};
-
-// Issue the loads of pieces [i0, i0 + CH) of the lane's share of a fine
-// block's rows of one tensor (lane l holds pieces i * 64 + l of the 64 x PPR
-// piece grid).  Empty slots read row 0; their slot weight is exactly 0, so
+// Load the lane's pieces of the K and V rows of item i's step with slot
+// tokens idx: lane l holds pieces l, l + 64, ... of the 64 x PPR grid of
+// (slot, piece).  Empty slots read row 0; their slot weight is exactly 0, so
 // they add 0 * row 0 to the sums, as the reference's masked product does
 // (compression.py:38-39).
-template <typename T, int D, int CH>
-__device__ __forceinline__ void pool_load(const T* X, int64_t xsn, int idx, int i0, int lane, u32x4 (&r)[CH]) {
-    typedef PoolCfg<T, D> C;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-        const int q = (i0 + i) * 64 + lane, s = q / C::PPR, p = q - s * C::PPR;
-        const int tok = max(__shfl(idx, s), 0);
-        r[i] = *reinterpret_cast<const u32x4*>(X + (int64_t)tok * xsn + p * C::EP);
-    }
-}
-
-// Write pieces [i0, i0 + CH) to the row buffer.
-template <typename T, int D, int CH>
-__device__ __forceinline__ void pool_stage(uint32_t* rows, int i0, int lane, const u32x4 (&r)[CH]) {
-    typedef PoolCfg<T, D> C;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-        const int q = (i0 + i) * 64 + lane, s = q / C::PPR, p = q - s * C::PPR;
-        *reinterpret_cast<u32x4*>(rows + s * C::RD + p * 4) = r[i];
-    }
-}
-
-// Column sums over the row buffer with the slot weights in LDS: lane (h, u)
-// adds slots h, h + S, ... of column dword u into out (per-lane partials; the
-// slot groups are summed when the summary is stored).  Lanes past the last
-// column re-read it (no divergent branch); their sums are never stored.
 template <typename T, int D>
-__device__ __forceinline__ void pool_column_sums(const uint32_t* rows, const float* lw, int lane,
-                                                 float (&out)[PoolCfg<T, D>::SJ][PoolCfg<T, D>::CPD]) {
-    typedef PoolCfg<T, D> C;
-    const int h = lane / C::LW, u0 = lane % C::LW;
-#pragma unroll 8
-    for (int i = 0; i < 64 / C::S; ++i) {
-        const int s = i * C::S + h;
-        const float ws = lw[s];
+__device__ __forceinline__ void pool_fetch(const PoolDev& a, unsigned i, int idx, int lane,
+                                           u32x4 (&pk)[PoolRowCfg<T, D>::PPR], u32x4 (&pv)[PoolRowCfg<T, D>::PPR]) {
+    constexpr int PPR = PoolRowCfg<T, D>::PPR, EP = PoolRowCfg<T, D>::EP;
+    const int g = (int)(i % a.G), b = (int)(i / a.G / a.Mp);
+    const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
+    const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
 #pragma unroll
-        for (int j = 0; j < C::SJ; ++j) {
-            const uint32_t raw = rows[s * C::RD + min(u0 + 64 * j, C::DW - 1)];
-            const T* x = reinterpret_cast<const T*>(&raw);
-#pragma unroll
-            for (int c = 0; c < C::CPD; ++c) out[j][c] += ws * to_f32(x[c]);
-        }
+    for (int r = 0; r < PPR; ++r) {
+        const int q = r * 64 + lane, s = q / PPR, p = q - s * PPR;
+        const int64_t tok = max(__shfl(idx, s), 0);
+        pk[r] = *reinterpret_cast<const u32x4*>(K + tok * a.ksn + p * EP);
+        pv[r] = *reinterpret_cast<const u32x4*>(Vv + tok * a.vsn + p * EP);
     }
 }
+
+// Write the 16-bit halves of the packed row `row` (channels 2j, 2j + 1 in
+// word j) as column `lane` of rows c0, c0 + 1, ... of X^T.
+template <int PPR, int XS>
+__device__ __forceinline__ void write_column(unsigned char* xt, int c0, int lane, const u32x4 (&row)[PPR]) {
+#pragma unroll
+    for (int p = 0; p < PPR; ++p)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const unsigned word = row[p][w];
+            unsigned char* col = xt + (c0 + 8 * p + 2 * w) * XS + lane * 2;
+            *reinterpret_cast<unsigned short*>(col) = (unsigned short)word;
+            *reinterpret_cast<unsigned short*>(col + XS) = (unsigned short)(word >> 16);
+        }
+}
+
 
 // Persistent: wave w of block k takes items k * waves + w, + waves * grid, ...
 // Items run kv head fastest, so the waves of a block read the neighbouring
 // head slices of the same token rows together and each row's kg / vg span is
-// fetched from HBM once and in one piece.  With TAB_LDS the block first
-// copies the rope table into LDS, so the per-slot (cos, sin) gathers of the
-// rotation are LDS reads.
+// fetched from HBM once.  A step is one fine block of an item (a padding
+// summary has one step with no block); the block-table row of the step after
+// next and the coordinates of the next step's tokens are loaded with the next
+// step's rows.
 template <typename T, int D, bool TAB_LDS>
-__global__ __launch_bounds__(256) void k_pool_fwd(PoolDev a) {
-    typedef PoolCfg<T, D> C;
-    typedef PoolFwdCfg<T, D> F;
-    constexpr int EP = C::EP, PPR = C::PPR, CPD = C::CPD, CH = F::CH;
+__global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd(PoolDev a) {
+    typedef PoolRowCfg<T, D> C;
+    constexpr int EP = C::EP, PPR = C::PPR, RB = C::RB, NCH = C::NCH, PPC = C::PPC, XS = C::XS;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     int4* meta = reinterpret_cast<int4*>(smem_raw);
     int* prun = reinterpret_cast<int*>(meta + D / 2);
-    float* lweight = reinterpret_cast<float*>(prun + F::PFN);
+    float* lweight = reinterpret_cast<float*>(prun + C::PFN);
     float* lbias = lweight + D;
     float2* ltab = reinterpret_cast<float2*>(lbias + 64);
     const int tab_dw = TAB_LDS ? ((a.table_entries * 2 + 3) & ~3) : 0;
-    uint32_t* rows = reinterpret_cast<uint32_t*>(ltab) + tab_dw + wave * F::WAVE_DW;
-    float* lw = reinterpret_cast<float*>(rows + 64 * C::RD);
+    unsigned char* rows = reinterpret_cast<unsigned char*>(reinterpret_cast<uint32_t*>(ltab) + tab_dw) +
+                          (size_t)wave * C::WAVE_BYTES;
+    T* wrows = reinterpret_cast<T*>(rows + C::XT_BYTES);  // MFMA path: weight rows hi, lo, 0
     for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(a.rope.pairs, j);
     // Piece p is a table run when its pairs read consecutive entries with one
     // stride vector: entry(j0 + t) = entry(j0) + t for every position.
@@ -342,113 +409,186 @@ __global__ __launch_bounds__(256) void k_pool_fwd(PoolDev a) {
     // item arithmetic is 32-bit scalar code.
     const unsigned total = (unsigned)a.B * a.G * a.Mp;
     const unsigned stride = gridDim.x * waves;
-    // Block-table row of an item's first fine block (-1 past the end or for a
-    // padding summary).  The next item's row is fetched right after this
-    // item's first K / V loads (so waiting for those leaves it in flight) and
-    // arrives while this item is reduced: the table read is off the item's
-    // critical path.
-    auto first_row = [&](unsigned it) -> int {
-        if (it >= total) return -1;
-        const unsigned mm = (it / a.G) % a.Mp;
-        return (mm < (unsigned)a.M && lane < a.V) ? a.blocks[(int64_t)mm * a.P * a.V + lane] : -1;
+    unsigned it = blockIdx.x * waves + wave;
+    if (it >= total) return;
+
+    auto steps_of = [&](unsigned i) __attribute__((always_inline)) -> int {
+        const int m = (int)((i / a.G) % a.Mp);
+        return m < a.M ? min(a.F, (m + 1) * a.P) - m * a.P : 1;
     };
-    unsigned item = blockIdx.x * waves + wave;
-    int idx_first = first_row(item);
-    for (; item < total; item += stride) {
-        int idx_next = -1;
-        bool fetched = false;
-        const int g = (int)(item % a.G);
-        const unsigned bm = item / a.G;
-        const int m = (int)(bm % a.Mp), b = (int)(bm / a.Mp);
-        const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
-        const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
-        float acck[C::SJ][CPD], accv[C::SJ][CPD];
+    // The lane's slot token of step (i, fl), or -1 (empty slot, padding summary).
+    auto row_of = [&](unsigned i, int fl) __attribute__((always_inline)) -> int {
+        const int m = (int)((i / a.G) % a.Mp);
+        return (m < a.M && lane < a.V) ? a.blocks[(int64_t)(m * a.P + fl) * a.V + lane] : -1;
+    };
+    // Pair metadata of each piece's first pair and the table-run flags, as
+    // wave-uniform values (scalar registers) for the whole loop.
+    int4 pm[PPR];
+    unsigned runs = 0;
 #pragma unroll
-        for (int j = 0; j < C::SJ; ++j)
+    for (int p = 0; p < PPR; ++p) {
+        const int4 m0 = meta[p * EP / 2];
+        pm[p] = int4{__builtin_amdgcn_readfirstlane(m0.x), __builtin_amdgcn_readfirstlane(m0.y),
+                     __builtin_amdgcn_readfirstlane(m0.z), __builtin_amdgcn_readfirstlane(m0.w)};
+        runs |= (unsigned)(__builtin_amdgcn_readfirstlane(prun[p]) != 0) << p;
+    }
+    u32x4 pk[PPR], pv[PPR];
+    // MFMA path: lane l supplies weight row min(l % 32, 2) of the A operand.
+    const T* wsrc = wrows + 64 * min(lane & 31, 2);
+    if constexpr (C::MF) wrows[128 + lane] = from_f32<T>(0.f);
+
+    int fl = 0, ns = steps_of(it);
+    int idx = row_of(it, 0);
+    int pos[3];
+    rope_position32(a.rope, max(idx, 0), pos);
+    pool_fetch<T, D>(a, it, idx, lane, pk, pv);
+    unsigned it1 = ns > 1 ? it : it + stride;
+    int fl1 = ns > 1 ? 1 : 0;
+    int idx1 = it1 < total ? row_of(it1, fl1) : -1;
+    float acc[C::NACC];
 #pragma unroll
-            for (int c = 0; c < CPD; ++c) acck[j][c] = accv[j][c] = 0.f;
-        int count = 0;
-        const int f_end = m < a.M ? min(a.F, (m + 1) * a.P) : 0;
-        for (int f = m * a.P; f < f_end; ++f) {
-            const int idx = f == m * a.P ? idx_first : (lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1);
-            if (__ballot(idx >= 0) == 0) continue;  // empty fine block: no mass, no count
+    for (int k = 0; k < C::NACC; ++k) acc[k] = 0.f;
+    int count = 0;
+    // The summary of a finished item is stored in the next step, after that
+    // step's rows are staged and before the loads of the step after it are
+    // issued, so the wait for those loads never waits on the stores.
+    bool pending = false;
+    int pend_bg = 0, pend_m = 0, pend_count = 0;
+    float pend[C::NACC];
+    for (;;) {
+        // Stage this step's pieces as rows (slot s at s * RB).
+#pragma unroll
+        for (int r = 0; r < PPR; ++r) {
+            const int q = r * 64 + lane;
+            *reinterpret_cast<u32x4*>(rows + q * 16) = pk[r];
+            *reinterpret_cast<u32x4*>(rows + C::VOFF + q * 16) = pv[r];
+        }
+        wave_lds_sync();
+        if (pending) {
+            store_summary<T, D>(a, pend_bg, pend_m, lane, pend_count, pend);
+            pending = false;
+        }
+        // The lane's own K and V rows.
+        u32x4 kr[PPR], vr[PPR];
+#pragma unroll
+        for (int p = 0; p < PPR; ++p) {
+            kr[p] = *reinterpret_cast<const u32x4*>(rows + lane * RB + p * 16);
+            vr[p] = *reinterpret_cast<const u32x4*>(rows + C::VOFF + lane * RB + p * 16);
+        }
+        wave_lds_sync();  // every row is read before X^T overwrites the rows
+        // Next step's rows and coordinates, and the block-table row after it.
+        const bool more = it1 < total;
+        int ns1 = 1, pos1[3] = {0, 0, 0}, idx2 = -1;
+        unsigned it2 = total;
+        int fl2 = 0;
+        if (more) {
+            ns1 = steps_of(it1);
+            pool_fetch<T, D>(a, it1, idx1, lane, pk, pv);
+            rope_position32(a.rope, max(idx1, 0), pos1);
+            it2 = fl1 + 1 < ns1 ? it1 : it1 + stride;
+            fl2 = fl1 + 1 < ns1 ? fl1 + 1 : 0;
+            if (it2 < total) idx2 = row_of(it2, fl2);
+        }
+
+        if (__ballot(idx >= 0) != 0) {  // empty fine block: no mass, no count
             ++count;
-            int pos[3];
-            rope_position32(a.rope, max(idx, 0), pos);
-            u32x4 kr[CH], vr[CH];
-            if constexpr (F::KV_TOGETHER) {
-                // Every load of the block is in flight before any is used.
-                pool_load<T, D, CH>(K, a.ksn, idx, 0, lane, kr);
-                pool_load<T, D, CH>(Vv, a.vsn, idx, 0, lane, vr);
-                if (!fetched) idx_next = first_row(item + stride);
-                fetched = true;
-                pool_stage<T, D, CH>(rows, 0, lane, kr);
-            } else {
-                if (!fetched) idx_next = first_row(item + stride);
-                fetched = true;
-#pragma unroll 1
-                for (int i0 = 0; i0 < PPR; i0 += CH) {
-                    pool_load<T, D, CH>(K, a.ksn, idx, i0, lane, kr);
-                    pool_stage<T, D, CH>(rows, i0, lane, kr);
+            if constexpr (C::MF) write_column<PPR, XS>(rows, D, lane, vr);
+            // Rotate the slot's key, round it to the storage type, and form its
+            // logit (compression.py:31-35): (k . w) / tau + bias_s.
+            float dot = 0.f;
+#pragma unroll
+            for (int p = 0; p < PPR; ++p) {
+                float kx[EP];
+                unpack_piece<T, EP>(kr[p], kx);
+                const int e0 = pm[p].x + __mul24(pm[p].y, pos[0]) + __mul24(pm[p].z, pos[1]) +
+                               __mul24(pm[p].w, pos[2]);
+                float2 cs[EP / 2];
+                if (runs >> p & 1) {
+#pragma unroll
+                    for (int t = 0; t < EP / 2; ++t) cs[t] = tab[e0 + t];
+                } else {
+#pragma unroll
+                    for (int t = 0; t < EP / 2; ++t) cs[t] = pair_cs(meta[p * EP / 2 + t], tab, pos);
                 }
+#pragma unroll
+                for (int t = 0; t < EP / 2; ++t) rotate_pair(kx[2 * t], kx[2 * t + 1], cs[t].x, cs[t].y);
+                kr[p] = __builtin_bit_cast(u32x4, round_piece<T, EP>(kx));
+#pragma unroll
+                for (int e = 0; e < EP; ++e) dot += kx[e] * lweight[p * EP + e];
             }
-            wave_lds_sync();
-            // One lane per slot: rotate the slot's K row in place, round it to
-            // the storage type, and form its logit (compression.py:31-35):
-            // (k . w) / tau + bias_s.
-            float logit = -INFINITY;
-            if (idx >= 0) {
-                float dot = 0.f;
-#pragma unroll 1
-                for (int p = 0; p < PPR; ++p) {
-                    uint32_t* rp = rows + lane * C::RD + p * 4;
-                    const u32x4 raw = *reinterpret_cast<const u32x4*>(rp);
-                    const T* kt = reinterpret_cast<const T*>(&raw);
-                    float kx[EP];
-#pragma unroll
-                    for (int e = 0; e < EP; ++e) kx[e] = to_f32(kt[e]);
-                    const int j0 = p * EP / 2;
-                    const int4 m0 = meta[j0];
-                    const int e0 = m0.x + __mul24(m0.y, pos[0]) + __mul24(m0.z, pos[1]) + __mul24(m0.w, pos[2]);
-                    float2 cs[EP / 2];
-                    if (__builtin_amdgcn_readfirstlane(prun[p])) {
-#pragma unroll
-                        for (int t = 0; t < EP / 2; ++t) cs[t] = tab[e0 + t];
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < EP / 2; ++t) cs[t] = pair_cs(meta[j0 + t], tab, pos);
-                    }
-#pragma unroll
-                    for (int t = 0; t < EP / 2; ++t) rotate_pair(kx[2 * t], kx[2 * t + 1], cs[t].x, cs[t].y);
-                    *reinterpret_cast<uint4*>(rp) = round_piece<T, EP>(kx);
-#pragma unroll
-                    for (int e = 0; e < EP; ++e) dot += kx[e] * lweight[p * EP + e];
-                }
-                logit = dot * a.inv_tau + lbias[lane];
-            }
+            const float logit = idx >= 0 ? dot * a.inv_tau + lbias[lane] : -INFINITY;
             const float mx = wave_max(logit);
             const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
-            lw[lane] = ex / wave_sum(ex);
-            wave_lds_sync();  // rotated rows and slot weights are read across lanes below
-            pool_column_sums<T, D>(rows, lw, lane, acck);
-            wave_lds_sync();  // the V rows overwrite the K rows
-            if constexpr (F::KV_TOGETHER) {
-                pool_stage<T, D, CH>(rows, 0, lane, vr);
+            const float wgt = ex / wave_sum(ex);
+            if constexpr (C::MF) {
+                typedef typename Mma<T>::Frag Frag;
+                write_column<PPR, XS>(rows, 0, lane, kr);
+                const T hi = from_f32<T>(wgt);
+                wrows[lane] = hi;
+                wrows[64 + lane] = from_f32<T>(wgt - to_f32(hi));
+                wave_lds_sync();
+                // D[w][c] = sum_s W[w][s] X^T[c][s] for the weight rows w = 0
+                // (hi), 1 (lo), over 16 slots per instruction: lane l holds
+                // slots 8 (l / 32) + j of channel l % 32 (B) and, for l % 32 <
+                // 2, of weight row l % 32 (A); rows 0 and 1 of D are
+                // registers 0 and 1 of lanes 0..31.
+                const int g = lane >> 5, n = lane & 31;
+                f32x16 d[C::NT];
+#pragma unroll
+                for (int t = 0; t < C::NT; ++t)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) d[t][r] = 0.f;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const Frag wa = __builtin_bit_cast(Frag, *reinterpret_cast<const u32x4*>(wsrc + 16 * ks + 8 * g));
+#pragma unroll
+                    for (int t = 0; t < C::NT; ++t) {
+                        const Frag xb = __builtin_bit_cast(
+                            Frag, *reinterpret_cast<const u32x4*>(rows + (32 * t + n) * XS + (16 * ks + 8 * g) * 2));
+                        d[t] = Mma<T>::mfma(wa, xb, d[t]);
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < C::NT; ++t) acc[t] += d[t][0] + d[t][1];
             } else {
-#pragma unroll 1
-                for (int i0 = 0; i0 < PPR; i0 += CH) {
-                    pool_load<T, D, CH>(Vv, a.vsn, idx, i0, lane, vr);
-                    pool_stage<T, D, CH>(rows, i0, lane, vr);
+#pragma unroll
+                for (int k = 0; k < NCH; ++k) {
+                    float kv[16], vv[16];
+#pragma unroll
+                    for (int t = 0; t < PPC; ++t) {
+                        float xk[EP], xv[EP];
+                        unpack_piece<T, EP>(kr[k * PPC + t], xk);
+                        unpack_piece<T, EP>(vr[k * PPC + t], xv);
+#pragma unroll
+                        for (int e = 0; e < EP; ++e) {
+                            kv[t * EP + e] = wgt * xk[e];
+                            vv[t * EP + e] = wgt * xv[e];
+                        }
+                    }
+                    acc[k] += butterfly_sum(kv, vv, lane);
                 }
             }
-            wave_lds_sync();
-            pool_column_sums<T, D>(rows, lw, lane, accv);
-            wave_lds_sync();  // the next fine block overwrites the rows
         }
-        if (!fetched) idx_next = first_row(item + stride);
-        write_summary<T, D>(a, b * a.G + g, m, lane, count, acck, accv);
-        idx_first = idx_next;
+        if (fl + 1 == ns) {
+            const unsigned bm = it / a.G;
+            pending = true;
+            pend_bg = (int)(bm / a.Mp) * a.G + (int)(it % a.G);
+            pend_m = (int)(bm % a.Mp);
+            pend_count = count;
+#pragma unroll
+            for (int k = 0; k < C::NACC; ++k) {
+                pend[k] = acc[k];
+                acc[k] = 0.f;
+            }
+            count = 0;
+        }
+        if (!more) break;
+        wave_lds_sync();  // the next step's staging overwrites the rows
+        it = it1, fl = fl1, ns = ns1, idx = idx1;
+        pos[0] = pos1[0], pos[1] = pos1[1], pos[2] = pos1[2];
+        it1 = it2, fl1 = fl2, idx1 = idx2;
     }
+    if (pending) store_summary<T, D>(a, pend_bg, pend_m, lane, pend_count, pend);
 }
 
 // Pooling backward (the VJP of compression.py:28-44; kernels.py:240-270 of
@@ -679,14 +819,15 @@ inline int pool_waves(size_t fixed, size_t per_wave) {
 
 template <typename T, int D>
 void launch_pool_t(const PoolDev& d, hipStream_t s) {
-    // Up to four waves (the kv heads of a summary) per block; a persistent
-    // grid of as many blocks as stay resident, each striding over the items.
+    // As many waves per block as the LDS holds row buffers for (at most 12);
+    // a persistent grid of as many blocks as stay resident, each striding
+    // over the items.
+    typedef PoolRowCfg<T, D> C;
     const bool tab_lds = d.table_entries * 8 <= kTableLdsBytes;
     const size_t tab_bytes = tab_lds ? (size_t)((d.table_entries * 2 + 3) & ~3) * 4 : 0;
-    const size_t fixed = PoolFwdCfg<T, D>::FIXED + tab_bytes;
-    const size_t per_wave = (size_t)PoolFwdCfg<T, D>::WAVE_DW * 4;
-    const int waves = pool_waves(fixed, per_wave);
-    const size_t smem = fixed + per_wave * waves;
+    const size_t fixed = C::FIXED + tab_bytes;
+    const int waves = (int)std::min<size_t>(C::MAX_WAVES, (160 * 1024 - fixed) / C::WAVE_BYTES);
+    const size_t smem = fixed + (size_t)C::WAVE_BYTES * waves;
     int dev = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);

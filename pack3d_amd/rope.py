@@ -56,16 +56,28 @@ def _cached(key, make):
 
 
 def _tables(pairs, extents, head_dim, device, base=10000.0):
-    """(table, pair descriptors) for per-axis pair counts and axis extents."""
+    """(table, pair descriptors) for per-axis pair counts and axis extents.
+
+    Entry (axis, coordinate, pair j) sits at descriptor base_j + stride *
+    coordinate.  The stride is the axis' pair count rounded up to an odd
+    number (pad entries hold the identity (1, 0)): lanes that read the same
+    pair at consecutive coordinates, as a fine block of a raster row does,
+    then hit distinct LDS banks.
+    """
     parts, desc, offset = [], [], 0
     for axis, (count, extent) in enumerate(zip(pairs, extents)):
         if count == 0:
             continue
+        stride = count | 1
         freq = base ** (-torch.arange(count, dtype=torch.float32) / count)
         angle = torch.arange(extent, dtype=torch.float32)[:, None] * freq
-        parts.append(torch.stack((angle.cos(), angle.sin()), -1).reshape(-1, 2))
-        desc.extend([offset + j, count, axis] for j in range(count))
-        offset += extent * count
+        cs = torch.stack((angle.cos(), angle.sin()), -1)
+        if stride > count:
+            pad = torch.tensor([1.0, 0.0]).expand(extent, stride - count, 2)
+            cs = torch.cat((cs, pad), 1)
+        parts.append(cs.reshape(-1, 2))
+        desc.extend([offset + j, stride, axis] for j in range(count))
+        offset += extent * stride
     assert len(desc) == head_dim // 2
     table = torch.cat(parts).contiguous().to(device)
     return table, torch.tensor(desc, dtype=torch.int32).to(device)

@@ -103,6 +103,29 @@ def kernel_times_in_layer(layer, x, layout, steps, stream):
     return sum(spans[0::2]) / steps, sum(spans[1::2]) / steps
 
 
+def summary_pathway_ms(plan, steps, stream):
+    """Mean duration (ms) of the summary pathway alone on the plan's inputs.
+
+    The rows kernel runs the same summary pass (rotated queries against all
+    summaries on MFMA, fixed Cauchy-Schwarz reference point) and the same
+    epilogue as the fused grid kernel, for every query row, with the local
+    term read from a zero fp32 buffer instead of computed: its duration is
+    the summary pathway's cost plus that extra read (4 B x H x N x d).
+    """
+    from pack3d_amd import _lib
+    from pack3d_amd.core import ctypes_copy
+
+    a = plan.attn_args
+    rows = _lib.AttnArgs()
+    ctypes_copy(rows, a)
+    o_local = torch.zeros(a.batch * a.heads * a.tokens * a.head_dim, dtype=torch.float32, device=plan.device)
+    rows.o_local_in = o_local.data_ptr()
+    rows.lse_local = None
+    run = lambda: _lib.call("p3d_attn_fwd_rows", rows, stream.cuda_stream)
+    run()
+    return time_events(run, max(5, steps), stream)
+
+
 def cpu_baseline(shape, threads, repeats=3):
     """The oracle (a restatement of the reference CPU path) on the whole c2 layer.
 
@@ -328,6 +351,7 @@ def main():
                            layer.global_scale, layout.geometry, layer.temperature, rope, rope)
         plan.run()
         ms_core = time_events(plan.run, max(5, a.steps), stream)
+        ms_summary = summary_pathway_ms(plan, a.steps, stream)
 
     m = layout.geometry.num_summaries
     edges = valid_edges(SHAPE, RADIUS)
@@ -349,7 +373,8 @@ def main():
                    "block": list(BLOCK), "pool_size": 1, "summaries": m, "valid_edges": edges,
                    "tokens_per_s": round(n / (ms_layer * 1e-3)), "ms_layer": round(ms_layer, 4),
                    "ms_core": round(ms_core, 4), "ms_pool_kernel": round(ms_pool, 4),
-                   "ms_attn_kernel": round(ms_attn, 4), "parallelism": "single GPU"},
+                   "ms_attn_kernel": round(ms_attn, 4), "ms_summary_pathway": round(ms_summary, 4),
+                   "parallelism": "single GPU"},
         "roofline": {"kernel": "k_attn_grid (fused local+global forward)", "bound": "mfma",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get("attn_bytes_per_launch"),
@@ -357,6 +382,11 @@ def main():
         "roofline_exp": {"kernel": "k_attn_grid", "bound": "valu-transcendental", "achieved": float(f"{exp_rate:.4g}"),
                          "peak": PEAK_EXP_PER_S, "unit": "exp/s", "frac": round(exp_rate / PEAK_EXP_PER_S, 4),
                          "algorithmic_exps": exps},
+        "roofline_summary": {"kernel": "k_attn_rows (summary pathway + epilogue, local term from a zero buffer)",
+                             "bound": "mfma", "achieved": round(flops_summary / (ms_summary * 1e-3) / 1e12, 2),
+                             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(flops_summary / (ms_summary * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                             "algorithmic_flops": flops_summary},
         "roofline_pool": {"kernel": "k_pool_fwd", "bound": "hbm", "achieved": round(pool_gbs, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(pool_gbs / PEAK_HBM_GBS, 4),
                           "traffic": traffic.get("pool_bytes_per_launch"),

@@ -6,7 +6,8 @@
 //
 // Eight lanes share a row; lane j of the group holds the 16-byte pieces j,
 // j + 8, ... of the row, so a wave covers 8 rows and every load and store is
-// a full 16 bytes.
+// a full 16 bytes.  The affine weight and bias are staged in LDS as fp32 once
+// per block; the row sums reduce over the 8 lanes through DPP.
 #include "common.hpp"
 
 namespace p3d {
@@ -14,11 +15,25 @@ namespace {
 
 constexpr int kLanesPerRow = 8;
 constexpr int kMaxPiecesPerLane = 8;
+constexpr int kMaxDim = 512;
+
+// Sum over the 8-lane group: lanes l ^ 1, l ^ 2 (quad_perm), then l ^ 7
+// within 8 (row_half_mirror).
+__device__ __forceinline__ float group8_sum(float x) {
+    x += dpp_move<0xB1>(x);
+    x += dpp_move<0x4E>(x);
+    return x + dpp_move<0x141>(x);
+}
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, const void* b, int param_dtype,
                                                     T* y, int64_t rows, int dim, float eps) {
     constexpr int EP = Piece<T>::N;
+    __shared__ __align__(16) float lw[kMaxDim], lb[kMaxDim];
+    for (int c = threadIdx.x; c < dim; c += blockDim.x) {
+        lw[c] = load_any(w, c, param_dtype);
+        lb[c] = load_any(b, c, param_dtype);
+    }
     const int lane = threadIdx.x & 63;
     const int sub = lane % kLanesPerRow;
     const int pieces = dim / EP;
@@ -36,9 +51,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, c
             for (int e = 0; e < EP; ++e) sum += v[i][e];
         }
     }
-#pragma unroll
-    for (int o = 1; o < kLanesPerRow; o <<= 1) sum += __shfl_xor(sum, o);
-    const float mean = sum / (float)dim;
+    const float mean = group8_sum(sum) / (float)dim;
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxPiecesPerLane; ++i) {
@@ -50,9 +63,8 @@ __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, c
                 sq += c * c;
             }
     }
-#pragma unroll
-    for (int o = 1; o < kLanesPerRow; o <<= 1) sq += __shfl_xor(sq, o);
-    const float rstd = 1.f / sqrtf(sq / (float)dim + eps);
+    const float rstd = 1.f / sqrtf(group8_sum(sq) / (float)dim + eps);
+    __syncthreads();
     if (!live) return;
 #pragma unroll
     for (int i = 0; i < kMaxPiecesPerLane; ++i) {
@@ -63,9 +75,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, c
 #pragma unroll
             for (int e = 0; e < EP; ++e) {
                 const int c = p * EP + e;
-                const float wc = load_any(reinterpret_cast<const char*>(w), c, param_dtype);
-                const float bc = load_any(reinterpret_cast<const char*>(b), c, param_dtype);
-                o[e] = from_f32<T>((v[i][e] - mean) * rstd * wc + bc);
+                o[e] = from_f32<T>((v[i][e] - mean) * rstd * lw[c] + lb[c]);
             }
             *reinterpret_cast<uint4*>(y + row * dim + p * EP) = raw;
         }
@@ -83,8 +93,8 @@ extern "C" int p3d_layer_norm(const void* x, const void* weight, const void* bia
     P3D_REQUIRE(dtype >= P3D_F32 && dtype <= P3D_BF16 && param_dtype >= P3D_F32 && param_dtype <= P3D_BF16,
                 "unknown dtype");
     const int ep = 16 / dtype_size(dtype);
-    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kLanesPerRow * kMaxPiecesPerLane,
-                "dim must be a multiple of the 16-byte piece, at most 64 pieces");
+    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kLanesPerRow * kMaxPiecesPerLane && dim <= kMaxDim,
+                "dim must be a multiple of the 16-byte piece, at most 64 pieces and 512 channels");
     P3D_REQUIRE(rows >= 1, "need at least one row");
     P3D_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0, "x and y must be 16-byte aligned");
     const int64_t threads = rows * kLanesPerRow;

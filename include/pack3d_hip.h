@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 3
+#define P3D_ABI_VERSION 4
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -189,6 +189,38 @@ int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tok
 int p3d_layer_norm(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
                    int64_t rows, int32_t dim, int32_t dtype, float eps, void* stream);
 
+/* Fused input projections of the layer (attention.py:64-67,85): LayerNorm
+ * of x [rows, dim], then q = xn Wq^T [rows, q_out], kv = xn Wkv^T
+ * [rows, kv_out] (the chunks kl | vl | kg | vg of to_kv) and, for each of
+ * the `heads` gate pairs, gate[row, h] = softmax(xn Wg^T + b_g)[2h + 1]
+ * [rows, heads], where Wg is [2 heads, dim].  x, the weights and the outputs
+ * have dtype (fp16 or bf16); the LayerNorm parameters and the gate bias have
+ * their own dtypes.  Rounding points are those of the torch ops it replaces:
+ * the normalised tokens, the linear outputs (the gate's after its bias) and
+ * the gate probability are rounded to dtype.  Replaces nn.LayerNorm, the
+ * to_q / to_kv / gate nn.Linear calls and the gate softmax of the layer's
+ * no-grad forward.  dim in {64, 96, 128, 192, 256, 384, 512}; q_out and
+ * kv_out multiples of 16; x, the weights, q and kv 16-byte aligned, all
+ * contiguous. */
+typedef struct p3d_project_args {
+    const void* x;
+    const void* ln_weight;
+    const void* ln_bias;
+    const void* wq;
+    const void* wkv;
+    const void* wg;
+    const void* gate_bias;
+    void* q;
+    void* kv;
+    void* gate;
+    int64_t rows;
+    int32_t dim, q_out, kv_out, heads;
+    int32_t dtype, ln_dtype, gate_bias_dtype;
+    float eps;
+} p3d_project_args;
+
+int p3d_project(const p3d_project_args* args, void* stream);
+
 /* ---- backward (replaces kernels.py:313-356, autograd.py:19-28) --------- */
 
 /* Shared argument block of the backward passes.  q and kl are the ROTATED
@@ -281,8 +313,8 @@ int p3d_selftest_mfma(int32_t dtype, const void* a, const void* b, float* d, voi
  * rates the summary pathway is bound by. */
 int p3d_probe_issue_rates(int32_t kind, int64_t iters, int32_t blocks, long long* cycles, void* stream);
 
-/* sizeof of p3d_view, p3d_rope, p3d_pool_args, p3d_attn_args, p3d_bwd_args
- * into out[5], so a binding can check its struct mirrors. */
+/* sizeof of p3d_view, p3d_rope, p3d_pool_args, p3d_attn_args, p3d_bwd_args,
+ * p3d_project_args into out[6], so a binding can check its struct mirrors. */
 int p3d_struct_sizes(int64_t* out);
 
 #ifdef __cplusplus

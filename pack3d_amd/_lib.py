@@ -22,7 +22,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 3  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 4  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -65,6 +65,14 @@ class BwdArgs(ctypes.Structure):
                 ("dk_local", c_void_p), ("dv_local", c_void_p), ("dsk_part", c_void_p), ("dsv_part", c_void_p)]
 
 
+class ProjectArgs(ctypes.Structure):
+    _fields_ = [("x", c_void_p), ("ln_weight", c_void_p), ("ln_bias", c_void_p), ("wq", c_void_p),
+                ("wkv", c_void_p), ("wg", c_void_p), ("gate_bias", c_void_p), ("q", c_void_p), ("kv", c_void_p),
+                ("gate", c_void_p), ("rows", c_int64), ("dim", c_int32), ("q_out", c_int32), ("kv_out", c_int32),
+                ("heads", c_int32), ("dtype", c_int32), ("ln_dtype", c_int32), ("gate_bias_dtype", c_int32),
+                ("eps", c_float)]
+
+
 _P = c_void_p
 SIGNATURES = {
     "p3d_last_error": ([], ctypes.c_char_p),
@@ -86,6 +94,7 @@ SIGNATURES = {
     "p3d_rotate": ([View, View, c_int32, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(Rope), c_int32, _P],
                    c_int32),
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
+    "p3d_project": ([ctypes.POINTER(ProjectArgs), _P], c_int32),
     "p3d_mix_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),
     "p3d_local_bwd_grid": ([ctypes.POINTER(BwdArgs), _P, _P, _P, _P], c_int32),

@@ -2,11 +2,14 @@
 
 Same constructor, parameters (names, shapes, initialisation order) and
 forward as ``PACK3DAttention`` of amilworks/Pack3D (``src/pack3d/attention.py``),
-with ``backend="hip"``: the projections, the gate softmax and ``to_out``
-(with the residual as the GEMM's C operand) stay in PyTorch (hipBLASLt
-GEMMs); LayerNorm (without autograd), the rotation, pooling, local and global
-attention and their fusion run in ``libpack3d_hip.so``.
-The projections are consumed as strided views, without copies.
+with ``backend="hip"``.  In the no-grad forward (fp16 / bf16) LayerNorm,
+to_q, to_kv, the gate map and its softmax run as one kernel
+(``p3d_project``); with autograd active, or for fp32 models, they are the
+torch ops (LayerNorm on the HIP kernel when no gradient is needed).  The
+rotation, pooling, local and global attention and their fusion run in
+``libpack3d_hip.so``; ``to_out`` with the residual as its C operand stays a
+hipBLASLt GEMM.  The projections are consumed as strided views, without
+copies.
 """
 from __future__ import annotations
 
@@ -45,6 +48,42 @@ def layer_norm(norm: nn.LayerNorm, x):
     return y
 
 
+PROJECT_DIMS = (64, 96, 128, 192, 256, 384, 512)
+
+
+def fused_projections(layer, x):
+    """(q [B,N,H*d], kv [B,N,4*G*d], gate [B,N,H]) of the no-grad forward from
+    one kernel (``p3d_project``): LayerNorm, to_q, to_kv, the gate map and its
+    pair softmax.  None when it does not apply (autograd active, fp32 or mixed
+    dtypes, a model width the kernel does not take); the caller then runs the
+    separate ops, which compute the same values."""
+    norm, lin = layer.norm, (layer.to_q, layer.to_kv, layer.gate)
+    dt = x.dtype
+    params = [norm.weight, norm.bias, *(m.weight for m in lin), layer.gate.bias]
+    if any(p is None for p in params):
+        return None
+    if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in params)):
+        return None
+    if (not x.is_cuda or dt not in (torch.float16, torch.bfloat16) or layer.dim not in PROJECT_DIMS
+            or tuple(norm.normalized_shape) != (layer.dim,) or any(m.weight.dtype != dt for m in lin)
+            or any(not m.weight.is_contiguous() for m in lin) or norm.weight.dtype != norm.bias.dtype
+            or norm.weight.dtype not in _lib.DTYPES or layer.gate.bias.dtype not in _lib.DTYPES):
+        return None
+    b, n = x.shape[0], x.shape[1]
+    h, g, d = layer.heads, layer.kv_heads, layer.head_dim
+    xc = x.contiguous()
+    q = torch.empty(b, n, h * d, dtype=dt, device=x.device)
+    kv = torch.empty(b, n, 4 * g * d, dtype=dt, device=x.device)
+    gate = torch.empty(b, n, h, dtype=dt, device=x.device)
+    args = _lib.ProjectArgs(xc.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(),
+                            layer.to_q.weight.data_ptr(), layer.to_kv.weight.data_ptr(), layer.gate.weight.data_ptr(),
+                            layer.gate.bias.data_ptr(), q.data_ptr(), kv.data_ptr(), gate.data_ptr(), b * n, layer.dim,
+                            h * d, 4 * g * d, h, _lib.DTYPES[dt], _lib.DTYPES[norm.weight.dtype],
+                            _lib.DTYPES[layer.gate.bias.dtype], float(norm.eps))
+    _lib.call("p3d_project", args, _lib.stream_of(x.device))
+    return q, kv, gate
+
+
 class PACK3DAttention(nn.Module):
     """Local residual plus gated compressed attention and an outer residual (attention.py:10-21)."""
 
@@ -81,11 +120,17 @@ class PACK3DAttention(nn.Module):
     def core_inputs(self, x, layout: TokenLayout):
         """Unrotated q, kl, vl, kg, vg (views of the projections), gate, and the rotation."""
         b, n = x.shape[0], x.shape[1]
-        xn = layer_norm(self.norm, x)
-        q = self.to_q(xn).view(b, n, self.heads, self.head_dim).transpose(1, 2)
+        fused = fused_projections(self, x)
+        if fused is not None:
+            qp, kvp, gp = fused
+            gate = gp.transpose(1, 2)
+        else:
+            xn = layer_norm(self.norm, x)
+            qp, kvp = self.to_q(xn), self.to_kv(xn)
+            gate = self.gate(xn).view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
+        q = qp.view(b, n, self.heads, self.head_dim).transpose(1, 2)
         kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
-                          for t in self.to_kv(xn).view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
-        gate = self.gate(xn).view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
+                          for t in kvp.view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
         if self.position_encoding == "packed":
             rope = packed_rope(self.head_dim, n, x.device)
         else:

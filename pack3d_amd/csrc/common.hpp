@@ -123,6 +123,15 @@ __device__ __forceinline__ constexpr int kperm(int rho) {
 // Value held by lane l ^ 32.
 __device__ __forceinline__ float swap_half(float x) { return __shfl_xor(x, 32); }
 
+// Orders this wave's LDS writes before its later LDS reads of other lanes'
+// data (and the compiler's view of them): a wavefront-scope fence pair
+// around a wave barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // x of the lane that the DPP control CTRL selects (a permutation within each
 // 16-lane row: every source lane exists, so `old` is never taken).
 template <int CTRL>

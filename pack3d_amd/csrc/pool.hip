@@ -54,12 +54,6 @@ struct PoolCfg {
     static constexpr int SJ = (DW + 63) / 64;      // column dwords per lane
 };
 
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Store a tensor's pieces (lane l holds pieces l, l + 64, ... of the 64 x PPR
 // grid) as rows of the LDS buffer.
 template <typename C>

@@ -113,5 +113,6 @@ extern "C" int p3d_struct_sizes(int64_t* out) {
     out[2] = sizeof(p3d_pool_args);
     out[3] = sizeof(p3d_attn_args);
     out[4] = sizeof(p3d_bwd_args);
+    out[5] = sizeof(p3d_project_args);
     return P3D_OK;
 }

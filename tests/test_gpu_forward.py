@@ -256,3 +256,48 @@ def test_layer_norm_kernel_matches_torch(gpu, dtype, dim):
                                                  norm.eps)
         tol = 1e-5 if dtype == torch.float32 else (2e-3 if dtype == torch.float16 else 1.6e-2)
         torch.testing.assert_close(got.float(), exp.to(dtype).float(), atol=tol * 4, rtol=tol)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim,heads,kv_heads,d", [(192, 4, 4, 48), (64, 2, 1, 32), (128, 4, 2, 16), (256, 2, 2, 64)])
+def test_fused_projections_match_torch(gpu, dtype, dim, heads, kv_heads, d):
+    """p3d_project against the separate torch ops it replaces (LayerNorm, the
+    three linear maps, the gate softmax), with random LayerNorm affine and
+    gate bias; rows not a multiple of the 128-token tile."""
+    from pack3d_amd.attention import fused_projections
+    print(f"fused projections {dim} h{heads} g{kv_heads} d{d} {dtype}", flush=True)
+    torch.manual_seed(dim + d)
+    layer = p3d.PACK3DAttention(dim, heads=heads, kv_heads=kv_heads, head_dim=d, block_volume=64)
+    with torch.no_grad():
+        layer.norm.weight.uniform_(0.5, 1.5)
+        layer.norm.bias.normal_(0.0, 0.1)
+        layer.gate.bias.normal_(0.0, 0.5)
+    layer = layer.to(gpu, dtype)
+    n = 1000
+    x = (torch.randn(2, n, dim) * 2.0 + 0.3).to(gpu, dtype)
+    with torch.no_grad():
+        got = fused_projections(layer, x)
+        assert got is not None
+        xn = layer.norm(x)
+        exp = (layer.to_q(xn), layer.to_kv(xn), layer.gate(xn).view(2, n, heads, 2).softmax(-1)[..., 1])
+    tol = {torch.bfloat16: 2 ** -6, torch.float16: 2 ** -9}[dtype]
+    for name, g_, e_ in zip(("q", "kv", "gate"), got, exp):
+        assert g_.shape == e_.shape, name
+        g32, e32 = g_.float(), e_.float()
+        # one rounding step of the output, relative to its magnitude (the
+        # contraction order differs from hipBLASLt's)
+        bound = tol * (e32.abs() + 1.0)
+        assert ((g32 - e32).abs() <= bound).all(), (name, float((g32 - e32).abs().max()))
+        assert float((g32 - e32).abs().mean()) < tol * 0.1, name
+
+
+@pytest.mark.gpu
+def test_fused_projections_not_used_with_grad(gpu):
+    from pack3d_amd.attention import fused_projections
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64).to(gpu, torch.bfloat16)
+    x = torch.randn(1, 64, 192, device=gpu, dtype=torch.bfloat16)
+    assert fused_projections(layer, x) is None  # parameters require grad and autograd is on
+    with torch.no_grad():
+        assert fused_projections(layer, x) is not None
+        assert fused_projections(layer.float(), x.float()) is None

@@ -29,10 +29,11 @@ def test_library_exports_every_declared_symbol():
 
 def test_struct_mirrors_match_c_sizes():
     from pack3d_amd import _lib
-    out = (ctypes.c_int64 * 5)()
+    out = (ctypes.c_int64 * 6)()
     assert _lib.lib().p3d_struct_sizes(out) == 0
     assert list(out) == [ctypes.sizeof(_lib.View), ctypes.sizeof(_lib.Rope), ctypes.sizeof(_lib.PoolArgs),
-                         ctypes.sizeof(_lib.AttnArgs), ctypes.sizeof(_lib.BwdArgs)]
+                         ctypes.sizeof(_lib.AttnArgs), ctypes.sizeof(_lib.BwdArgs),
+                         ctypes.sizeof(_lib.ProjectArgs)]
     header = open(os.path.join(ROOT, "include", "pack3d_hip.h")).read()
     version = int(re.search(r"#define P3D_ABI_VERSION (\d+)", header).group(1))
     assert _lib.lib().p3d_abi_version() == version == _lib.ABI_VERSION

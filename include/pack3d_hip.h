@@ -221,6 +221,16 @@ typedef struct p3d_project_args {
 
 int p3d_project(const p3d_project_args* args, void* stream);
 
+/* Output projection with the residual (attention.py:89): out = x + y Wo^T for
+ * y [rows, k] (the core's output, heads concatenated), Wo [dim, k] and x,
+ * out [rows, dim], all of dtype (fp16 or bf16), contiguous and 16-byte
+ * aligned; fp32 accumulation and one rounding of x + y Wo^T, as
+ * torch.addmm(x, y, Wo^T).  Replaces the layer's to_out nn.Linear and
+ * residual add in the no-grad forward.  k in {64, 96, 128, 192, 256, 384,
+ * 512}; dim a multiple of 32, at most 512. */
+int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int32_t k,
+                     int32_t dim, int32_t dtype, void* stream);
+
 /* ---- backward (replaces kernels.py:313-356, autograd.py:19-28) --------- */
 
 /* Shared argument block of the backward passes.  q and kl are the ROTATED

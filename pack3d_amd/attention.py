@@ -7,9 +7,10 @@ to_q, to_kv, the gate map and its softmax run as one kernel
 (``p3d_project``); with autograd active, or for fp32 models, they are the
 torch ops (LayerNorm on the HIP kernel when no gradient is needed).  The
 rotation, pooling, local and global attention and their fusion run in
-``libpack3d_hip.so``; ``to_out`` with the residual as its C operand stays a
-hipBLASLt GEMM.  The projections are consumed as strided views, without
-copies.
+``libpack3d_hip.so``, and so does ``x + to_out(y)`` in the no-grad fp16 /
+bf16 forward (``p3d_out_residual``; otherwise one hipBLASLt GEMM with the
+residual as its C operand).  The projections are consumed as strided views,
+without copies.
 """
 from __future__ import annotations
 
@@ -84,6 +85,26 @@ def fused_projections(layer, x):
     return q, kv, gate
 
 
+def fused_out_residual(layer, x, y):
+    """x + to_out(y) of the no-grad forward from one kernel (``p3d_out_residual``)
+    for y [B*N, H*d]; None when it does not apply (autograd active, fp32 or
+    mixed dtypes, widths the kernel does not take)."""
+    w = layer.to_out.weight
+    if torch.is_grad_enabled() and (x.requires_grad or y.requires_grad or w.requires_grad):
+        return None
+    dt = x.dtype
+    k = layer.heads * layer.head_dim
+    if (not x.is_cuda or dt not in (torch.float16, torch.bfloat16) or w.dtype != dt or y.dtype != dt
+            or k not in PROJECT_DIMS or layer.dim % 32 or layer.dim > 512 or not w.is_contiguous()
+            or not y.is_contiguous()):
+        return None
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    _lib.call("p3d_out_residual", y.data_ptr(), w.data_ptr(), xc.data_ptr(), out.data_ptr(), y.shape[0], k,
+              layer.dim, _lib.DTYPES[dt], _lib.stream_of(x.device))
+    return out
+
+
 class PACK3DAttention(nn.Module):
     """Local residual plus gated compressed attention and an outer residual (attention.py:10-21)."""
 
@@ -151,6 +172,10 @@ class PACK3DAttention(nn.Module):
         q, kl, vl, kg, vg, gate, rope = self.core_inputs(x, layout)
         out = pack3d_hip_rope(q, kl, vl, kg, vg, self.pool_weight, self.slot_bias, gate, self.local_scale,
                               self.global_scale, layout.geometry, rope, temperature=self.temperature)
-        # x + to_out(out) as one GEMM with the residual as its C operand (to_out has no bias).
+        # x + to_out(out): one kernel in the no-grad forward, else one GEMM with the
+        # residual as its C operand (to_out has no bias).
         o = out.transpose(1, 2).reshape(b * n, -1)
+        fused = fused_out_residual(self, x, o)
+        if fused is not None:
+            return fused.view(b, n, self.dim)
         return torch.addmm(x.reshape(b * n, self.dim), o, self.to_out.weight.t()).view(b, n, self.dim)

@@ -77,6 +77,25 @@ def grid_kernel_applies(geometry):
     return grid is not None and all(r <= 2 for r in grid[1])
 
 
+def param_f32(t):
+    """Contiguous fp32 copy of a small parameter vector (pooling weight, slot
+    bias, branch scales) for the kernels.  The copy is kept on the tensor and
+    reused while its storage and version counter are unchanged, so an
+    inference loop does not launch a conversion per call."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t.detach()
+    key = (t.data_ptr(), t._version, t.device)
+    hit = getattr(t, "_p3d_f32", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    v = t.detach().float().contiguous()
+    try:
+        t._p3d_f32 = (key, v)
+    except (AttributeError, RuntimeError):
+        pass
+    return v
+
+
 class ForwardPlan:
     """Buffers and ctypes argument blocks of one forward; ``run()`` launches it.
 
@@ -99,8 +118,8 @@ class ForwardPlan:
         self.svt = torch.empty(b, g, mp // 32, d, 32, dtype=q.dtype, device=dev)
         self.sk_norm_max = torch.empty(b * g * 64, dtype=torch.float32, device=dev)
         self._keep = [q, kl, vl, kg, vg, geometry, rope, pool_rope]
-        w32 = weight.detach().float().contiguous()
-        b32 = bias.detach().float().contiguous()
+        w32 = param_f32(weight)
+        b32 = param_f32(bias)
         # The attention kernels score against summaries stored pre-multiplied
         # by log2(e)/sqrt(d), so a score is already in the exp2 domain.
         self.key_scale = math.log2(math.e) / math.sqrt(d)
@@ -109,7 +128,7 @@ class ForwardPlan:
                                        w32.data_ptr(), b32.data_ptr(), pool_rope.struct(),
                                        self.sk.data_ptr(), self.svt.data_ptr(), self.sk_norm_max.data_ptr())
         self.y = torch.empty(b, n, h, d, dtype=q.dtype, device=dev).transpose(1, 2)
-        sl32, sg32 = sl.detach().float().contiguous(), sg.detach().float().contiguous()
+        sl32, sg32 = param_f32(sl), param_f32(sg)
         if gate.dtype not in _lib.DTYPES:
             gate = gate.float()
         self._keep += [w32, b32, sl32, sg32, gate]
@@ -265,7 +284,7 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
         for src, dst, heads in ((q, qr, h), (kl, klr, g)):
             _lib.call("p3d_rotate", _lib.view(src), _lib.view(dst), b, heads, n, d, dt, rope.struct(), 0, stream)
     gate_k = gate if gate.dtype in _lib.DTYPES else gate.float()
-    sl32, sg32 = sl.detach().float().contiguous(), sg.detach().float().contiguous()
+    sl32, sg32 = param_f32(sl), param_f32(sg)
     parts = _mix_parts(b * h * n)
     splits = _splits(n, m, b * g)
 
@@ -310,8 +329,8 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     dkl = empty(b, g, n, d)
     _lib.call("p3d_finish_bwd", a, rope.struct(), dq.data_ptr(), dkl.data_ptr(), stream)
 
-    w32 = weight.detach().float().contiguous()
-    b32 = bias.detach().float().contiguous()
+    w32 = param_f32(weight)
+    b32 = param_f32(bias)
     pool_args = _lib.PoolArgs(b, g, n, d, dt, f, slots, geometry.pool_size, m, float(temperature), float(key_scale),
                               _lib.view(kg), _lib.view(vg), geometry.blocks.data_ptr(), w32.data_ptr(),
                               b32.data_ptr(), pool_rope.struct(), sk.data_ptr(), svt.data_ptr(),

@@ -1,7 +1,8 @@
-// Fused input projections of the PACK3D layer (attention.py:64-67,85 of
-// amilworks/Pack3D): LayerNorm, the to_q, to_kv and gate linear maps of the
-// normalised tokens as one MFMA GEMM with contraction length dim, and the
-// gate's two-way softmax (softmax(-1)[..., 1]), in one pass over the tokens.
+// Fused projections of the PACK3D layer (attention.py:64-67,85,89 of
+// amilworks/Pack3D).  k_project: LayerNorm, the to_q, to_kv and gate linear
+// maps of the normalised tokens as one MFMA GEMM with contraction length
+// dim, and the gate's two-way softmax (softmax(-1)[..., 1]), in one pass
+// over the tokens.  k_out_residual: x + to_out(y).
 //
 // A wave owns 32 tokens.  Lane l holds token l % 32 and, for every 16-channel
 // k-step, channels 8 (l / 32) .. +8 of it: the B operand of the 32x32x16
@@ -196,6 +197,97 @@ __global__ __launch_bounds__(64 * kProjWaves) __attribute__((amdgpu_waves_per_eu
     }
 }
 
+// Output projection with the residual (attention.py:89): out = x + y Wo^T
+// for y [rows, K] (the core's output, heads concatenated), Wo [dim, K] and
+// x, out [rows, dim]: the same tiling as k_project without the LayerNorm (y
+// is the B operand as loaded), 32 outputs per block.  The block's fp32
+// accumulators go through the wave's tile, and the store phase adds the
+// residual piece and rounds once, as a GEMM with the residual as its C
+// operand does.
+template <typename T, int KS>
+__global__ __launch_bounds__(64 * kProjWaves) __attribute__((amdgpu_waves_per_eu(KS <= 12 ? 4 : 2)))
+void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const T* __restrict__ x, T* __restrict__ out,
+                    int64_t rows, int dim) {
+    typedef Mma<T> M;
+    typedef typename M::Frag Frag;
+    constexpr int K = 16 * KS;
+    constexpr int WS = K + 8;
+    constexpr int PIECES = 32 * K / 8;
+    constexpr int PPT = (PIECES + 64 * kProjWaves - 1) / (64 * kProjWaves);
+    constexpr int OS = 32 + 4;                      // fp32 output tile row stride
+    __shared__ __align__(16) T wbuf[2][32 * WS];
+    __shared__ __align__(16) float otile[kProjWaves][32 * OS];
+    const int nblocks = dim / 32;
+    u32x4 wreg[PPT];
+    auto fetch = [&](int ob) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (K / 8), c = (pc % (K / 8)) * 8;
+            wreg[i] = pc < PIECES ? *reinterpret_cast<const u32x4*>(wo + (int64_t)(32 * ob + r) * K + c)
+                                  : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (K / 8), c = (pc % (K / 8)) * 8;
+            if (pc < PIECES) *reinterpret_cast<u32x4*>(&wbuf[buf][r * WS + c]) = wreg[i];
+        }
+    };
+    fetch(0);
+    stage(0);
+    if (nblocks > 1) fetch(1);
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
+    const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + (threadIdx.x >> 6)) * 32, tok = tok0 + t;
+    const bool live = tok < rows;
+    float* tile = otile[threadIdx.x >> 6];
+    const T* yr = y + (live ? tok : 0) * K + 8 * g;
+    Frag yf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) yf[ks] = __builtin_bit_cast(Frag, *reinterpret_cast<const u32x4*>(yr + 16 * ks));
+
+    for (int ob = 0; ob < nblocks; ++ob) {
+        const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
+        f32x16 d;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) d[r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) d = M::mfma(*reinterpret_cast<const Frag*>(wb + 16 * ks), yf[ks], d);
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd)
+            *reinterpret_cast<f32x4*>(tile + t * OS + acc_row(4 * qd, g)) =
+                f32x4{d[4 * qd], d[4 * qd + 1], d[4 * qd + 2], d[4 * qd + 3]};
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int tt = 16 * i + (lane >> 2), pp = lane & 3, o0 = 32 * ob + 8 * pp;
+            const int64_t tk = tok0 + tt;
+            if (tk < rows) {
+                const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp);
+                const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp + 4);
+                const u32x4 res = *reinterpret_cast<const u32x4*>(x + tk * dim + o0);
+                const T* rv = reinterpret_cast<const T*>(&res);
+                u32x4 o;
+                T* ov = reinterpret_cast<T*>(&o);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ov[e] = from_f32<T>(lo[e] + to_f32(rv[e]));
+                    ov[4 + e] = from_f32<T>(hi[e] + to_f32(rv[4 + e]));
+                }
+                *reinterpret_cast<u32x4*>(out + tk * dim + o0) = o;
+            }
+        }
+        wave_lds_sync();
+        if (ob + 1 < nblocks) {
+            stage((ob + 1) & 1);
+            if (ob + 2 < nblocks) fetch(ob + 2);
+        }
+        __syncthreads();
+    }
+}
+
 template <typename T>
 int launch_project(const ProjDev& d, hipStream_t s) {
     const unsigned blocks = (unsigned)cdiv(cdiv(d.rows, 32), kProjWaves);
@@ -211,10 +303,40 @@ int launch_project(const ProjDev& d, hipStream_t s) {
     return check_launch("p3d_project");
 }
 
+template <typename T>
+int launch_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int k, int dim,
+                        hipStream_t s) {
+    const unsigned blocks = (unsigned)cdiv(cdiv(rows, 32), kProjWaves);
+    switch (k) {
+#define CASE(KK)                                                                                               \
+    case KK:                                                                                                   \
+        k_out_residual<T, KK / 16><<<blocks, 64 * kProjWaves, 0, s>>>((const T*)y, (const T*)wo, (const T*)x, \
+                                                                      (T*)out, rows, dim);                     \
+        break;
+        CASE(64) CASE(96) CASE(128) CASE(192) CASE(256) CASE(384) CASE(512)
+#undef CASE
+        default: return fail(P3D_EUNSUPPORTED, "heads * head_dim must be one of 64, 96, 128, 192, 256, 384, 512");
+    }
+    return check_launch("p3d_out_residual");
+}
+
 }  // namespace
 }  // namespace p3d
 
 using namespace p3d;
+
+extern "C" int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int32_t k,
+                                int32_t dim, int32_t dtype, void* stream) {
+    P3D_REQUIRE(y && wo && x && out, "null pointer argument");
+    P3D_REQUIRE(dtype == P3D_F16 || dtype == P3D_BF16, "dtype must be fp16 or bf16");
+    P3D_REQUIRE(rows >= 1, "need at least one row");
+    P3D_REQUIRE(dim >= 32 && dim % 32 == 0 && dim <= kProjMaxDim, "dim must be a multiple of 32, at most 512");
+    P3D_REQUIRE(aligned16(y) && aligned16(wo) && aligned16(x) && aligned16(out), "pointers must be 16-byte aligned");
+    P3D_REQUIRE(cdiv(rows, 32 * kProjWaves) < (1LL << 31), "too many rows");
+    hipStream_t s = as_stream(stream);
+    return dtype == P3D_F16 ? launch_out_residual<_Float16>(y, wo, x, out, rows, k, dim, s)
+                            : launch_out_residual<__bf16>(y, wo, x, out, rows, k, dim, s);
+}
 
 extern "C" int p3d_project(const p3d_project_args* args, void* stream) {
     P3D_REQUIRE(args, "null args");

@@ -301,3 +301,25 @@ def test_fused_projections_not_used_with_grad(gpu):
     with torch.no_grad():
         assert fused_projections(layer, x) is not None
         assert fused_projections(layer.float(), x.float()) is None
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim,heads,d", [(192, 4, 48), (64, 2, 32), (256, 4, 16)])
+def test_fused_out_residual_matches_addmm(gpu, dtype, dim, heads, d):
+    """p3d_out_residual against torch.addmm(x, y, Wo^T) (one rounding of the
+    fp32 sum); rows not a multiple of the 256-token tile."""
+    from pack3d_amd.attention import fused_out_residual
+    print(f"fused out residual {dim} h{heads} d{d} {dtype}", flush=True)
+    torch.manual_seed(dim + heads)
+    layer = p3d.PACK3DAttention(dim, heads=heads, kv_heads=1, head_dim=d, block_volume=64).to(gpu, dtype)
+    n = 777
+    x = torch.randn(n, dim, device=gpu).to(dtype)
+    y = torch.randn(n, heads * d, device=gpu).to(dtype)
+    with torch.no_grad():
+        got = fused_out_residual(layer, x, y)
+        exp = torch.addmm(x, y, layer.to_out.weight.t())
+    assert got is not None and got.shape == exp.shape
+    tol = {torch.bfloat16: 2 ** -7, torch.float16: 2 ** -10}[dtype]
+    g32, e32 = got.float(), exp.float()
+    assert ((g32 - e32).abs() <= tol * (e32.abs() + 1.0)).all(), float((g32 - e32).abs().max())

@@ -126,3 +126,18 @@ def test_core_requires_hip_device_no_fallback():
     inputs[0] = inputs[0][..., :40]
     with pytest.raises(ValueError):
         pack3d_hip(*inputs, geom)
+
+
+def test_param_f32_cache_follows_updates():
+    import torch
+    from pack3d_amd.core import param_f32
+    p = torch.nn.Parameter(torch.arange(6, dtype=torch.bfloat16))
+    a = param_f32(p)
+    assert a.dtype == torch.float32 and torch.equal(a, p.detach().float())
+    assert param_f32(p) is a  # unchanged parameter: the cached copy
+    with torch.no_grad():
+        p.add_(1)
+    b = param_f32(p)
+    assert b is not a and torch.equal(b, p.detach().float())  # in-place update: a fresh copy
+    q = torch.arange(4, dtype=torch.float32)
+    assert param_f32(q).data_ptr() == q.data_ptr()  # fp32 contiguous: no copy

@@ -454,10 +454,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
                 const f32x16 dp = score_tile<C>(vf, df[nb]);
                 float ds[16];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const bool live = first + kperm<C::E, C::KS>(acc_row(r, g)) < a.M;
-                    // One summary: P = 1 and dS = 0 exactly (kernels.py:198-199).
-                    ds[r] = (live && a.M > 1) ? __builtin_amdgcn_exp2f(s[r] - lse2[nb]) * (dp[r] - delta[nb]) : 0.f;
+                for (int r = 0; r < 16; ++r) ds[r] = __builtin_amdgcn_exp2f(s[r] - lse2[nb]) * (dp[r] - delta[nb]);
+                if (first + 32 > a.M) {  // the last tile: summaries past M contribute nothing
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        if (first + kperm<C::E, C::KS>(acc_row(r, g)) >= a.M) ds[r] = 0.f;
                 }
 #pragma unroll
                 for (int ks = 0; ks < C::KSTEPS; ++ks) {
@@ -472,6 +473,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
         __syncthreads();
         buf ^= 1;
     }
+    // One summary: P = 1 and dS = 0 exactly (kernels.py:198-199), so dQ_G = 0.
+    const float out_scale = a.M > 1 ? kLn2 : 0.f;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         if (!qok[nb]) continue;
@@ -481,15 +484,17 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int c = 32 * mb + acc_row(r, g);
-                if (c < D) dq[c] = acc[nb][mb][r] * kLn2;
+                if (c < D) dq[c] = acc[nb][mb][r] * out_scale;
             }
     }
 }
 
 // Query stages of SK rows (64, or 32 when two stages of 64 would not fit in
 // LDS) for the global dK/dV pass: q and dO_G rows (row stride KSTR), q and
-// dO_G transposed (row stride SK + EP, zero padding rows), and lse_G (log2
-// units; +inf past the last query) and Delta_G.
+// dO_G transposed (row stride SK + EP, zero padding rows), and -lse_G (log2
+// units; -inf past the last query) and -Delta_G.  Each thread moves PI
+// 16-byte pieces; their offsets inside a stage are computed once (qoff), so a
+// stage load is one 64-bit add per piece on top of the stage's scalar base.
 template <typename C, int SK>
 struct KvStage {
     typedef typename C::T_ T;
@@ -501,26 +506,53 @@ struct KvStage {
     static constexpr int ROWS = 2 * SK * C::KSTR;                 // q rows, dO rows
     static constexpr int TRANS = 2 * 32 * C::MB * TGS;            // q^T, dO^T
     static constexpr int SIZE = ROWS + TRANS + 2 * SK * (int)(sizeof(float) / sizeof(T));  // + lse, delta
+    // 16-bit types: the transposed copies' 8-column groups are swizzled by row.
+    static constexpr int MASK = sizeof(T) == 2 ? SK / 8 - 1 : 0;
     uint4 q[PI], d[PI];
-    float lse, delta;
+    int64_t qoff[PI];
+    float nlse, ndelta;
 
-    __device__ __forceinline__ void load(const BwdDev& a, int b, int h, int64_t base) {
-        const int64_t bh = (int64_t)b * a.H + h;
+    // Row of piece i inside the stage (SK for a piece past the stage) and its column.
+    static __device__ __forceinline__ int piece_row(int i) {
+        const int p = threadIdx.x + i * 64 * kWaves;
+        return p < PIECES ? p / PPR : SK;
+    }
+    static __device__ __forceinline__ int piece_col(int i) {
+        const int p = threadIdx.x + i * 64 * kWaves;
+        return (p - (p / PPR) * PPR) * EP;
+    }
+
+    __device__ __forceinline__ void init(int64_t qsn) {
 #pragma unroll
-        for (int i = 0; i < PI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
-            const int r = p / PPR, c = (p - r * PPR) * EP;
-            const int64_t row = base + r;
-            q[i] = d[i] = uint4{0, 0, 0, 0};
-            if (p < PIECES && row < a.N) {
-                q[i] = *reinterpret_cast<const uint4*>(tp<T>(a.q) + b * a.qsb + h * a.qsh + row * a.qsn + c);
-                d[i] = *reinterpret_cast<const uint4*>(tp<T>(a.dog) + (bh * a.N + row) * C::D + c);
+        for (int i = 0; i < PI; ++i) qoff[i] = piece_row(i) * qsn + piece_col(i);
+    }
+
+    // qs, ds: first q and dO_G row of the stage; ls, dl: its lse_G and Delta_G;
+    // rows: queries of the stage that exist (1..SK).  Rows past them are zero.
+    __device__ __forceinline__ void load(const T* qs, const T* ds, const float* ls, const float* dl, int rows) {
+        if (rows == SK) {
+#pragma unroll
+            for (int i = 0; i < PI; ++i) {
+                if (PIECES % (64 * kWaves) == 0 || i + 1 < PI || piece_row(i) < SK) {
+                    q[i] = *reinterpret_cast<const uint4*>(qs + qoff[i]);
+                    d[i] = *reinterpret_cast<const uint4*>(ds + piece_row(i) * C::D + piece_col(i));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < PI; ++i) {
+                const int r = piece_row(i);
+                q[i] = d[i] = uint4{0, 0, 0, 0};
+                if (r < rows) {
+                    q[i] = *reinterpret_cast<const uint4*>(qs + qoff[i]);
+                    d[i] = *reinterpret_cast<const uint4*>(ds + r * C::D + piece_col(i));
+                }
             }
         }
         if (threadIdx.x < SK) {
-            const int64_t row = base + threadIdx.x;
-            lse = row < a.N ? a.lse_g[bh * a.N + row] * kLog2e : INFINITY;
-            delta = row < a.N ? a.dg[bh * a.N + row] : 0.f;
+            const bool live = (int)threadIdx.x < rows;
+            nlse = live ? -ls[threadIdx.x] * kLog2e : -INFINITY;
+            ndelta = live ? -dl[threadIdx.x] : 0.f;
         }
     }
 
@@ -529,24 +561,24 @@ struct KvStage {
         T* dt = qt + 32 * C::MB * TGS;
 #pragma unroll
         for (int i = 0; i < PI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
-            if (p < PIECES) {
-                const int r = p / PPR, c = (p - r * PPR) * EP;
+            const int r = piece_row(i), c = piece_col(i);
+            if (r < SK) {
                 *reinterpret_cast<uint4*>(stage + r * C::KSTR + c) = q[i];
                 *reinterpret_cast<uint4*>(stage + SK * C::KSTR + r * C::KSTR + c) = d[i];
                 const T* qv = reinterpret_cast<const T*>(&q[i]);
                 const T* dv = reinterpret_cast<const T*>(&d[i]);
+                const int col = swz_col<MASK>(c, r);  // rows c .. c + EP - 1 share one group swizzle
 #pragma unroll
                 for (int e = 0; e < EP; ++e) {
-                    qt[(c + e) * TGS + r] = qv[e];
-                    dt[(c + e) * TGS + r] = dv[e];
+                    qt[(c + e) * TGS + col] = qv[e];
+                    dt[(c + e) * TGS + col] = dv[e];
                 }
             }
         }
         if (threadIdx.x < SK) {
             float* f = reinterpret_cast<float*>(stage + ROWS + TRANS);
-            f[threadIdx.x] = lse;
-            f[SK + threadIdx.x] = delta;
+            f[threadIdx.x] = nlse;
+            f[SK + threadIdx.x] = ndelta;
         }
     }
 };
@@ -581,49 +613,78 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acck[mb][r] = accv[mb][r] = 0.f;
 
-    const int64_t per = cdiv(cdiv((int64_t)a.N, SK), a.splits) * SK;  // queries per split
-    const int64_t q0 = split * per, q1 = min((int64_t)a.N, q0 + per);
+    // Queries per split, this split's range [q0, q1) and its stage count: block-
+    // uniform values, kept in scalar registers (the divisions run on the VALU).
+    const int per = __builtin_amdgcn_readfirstlane((int)cdiv(cdiv((int64_t)a.N, SK), a.splits) * SK);
+    const int q0 = split * per, q1 = min(a.N, q0 + per);
+    const int stages = __builtin_amdgcn_readfirstlane(q1 > q0 ? (q1 - q0 + SK - 1) / SK : 0);
     zero_padding_rows<C>(lds + S::ROWS, S::TGS, SK);
     zero_padding_rows<C>(lds + S::ROWS + 32 * C::MB * S::TGS, S::TGS, SK);
     zero_padding_rows<C>(lds + S::SIZE + S::ROWS, S::TGS, SK);
     zero_padding_rows<C>(lds + S::SIZE + S::ROWS + 32 * C::MB * S::TGS, S::TGS, SK);
-    const int64_t stages = q1 > q0 ? cdiv(q1 - q0, SK) : 0;
-    const int64_t total = stages * rep;
+    const int total = stages * rep;
     if (total > 0) {
+        // Stage (h, qb): query head h of the group, queries [qb, qb + SK).  The
+        // stage pointers advance by additions: SK rows within a head, one head
+        // (back to q0) when a head's range ends.
+        const int h0 = kvh * rep;
+        const int64_t bh0 = (int64_t)b * a.H + h0;
+        const T* q_head = tp<T>(a.q) + b * a.qsb + h0 * a.qsh + q0 * a.qsn;
+        const T* do_head = tp<T>(a.dog) + (bh0 * a.N + q0) * D;
+        const float* ls_head = a.lse_g + bh0 * a.N + q0;
+        const float* dl_head = a.dg + bh0 * a.N + q0;
+        const int64_t q_step = SK * a.qsn;
+        const T* qs = q_head;
+        const T* ds = do_head;
+        const float* ls = ls_head;
+        const float* dl = dl_head;
+        int nq = q0;
         S regs;
-        regs.load(a, b, kvh * rep, q0);
+        regs.init(a.qsn);
+        regs.load(qs, ds, ls, dl, min(SK, a.N - nq));
         regs.store(lds);
         __syncthreads();
         int buf = 0;
-        for (int64_t it = 0; it < total; ++it) {
-            const int64_t nx = it + 1;
-            if (nx < total) regs.load(a, b, kvh * rep + (int)(nx / stages), q0 + (nx % stages) * SK);
+        for (int it = 0; it < total; ++it) {
+            const bool more = it + 1 < total;
+            nq += SK;
+            if (nq >= q1) {
+                nq = q0;
+                q_head += a.qsh;
+                do_head += (int64_t)a.N * D;
+                ls_head += a.N;
+                dl_head += a.N;
+                qs = q_head, ds = do_head, ls = ls_head, dl = dl_head;
+            } else {
+                qs += q_step, ds += SK * D, ls += SK, dl += SK;
+            }
+            if (more) regs.load(qs, ds, ls, dl, min(SK, a.N - nq));
             const T* cur = lds + buf * S::SIZE;
-            const float* lse = reinterpret_cast<const float*>(cur + S::ROWS + S::TRANS);
-            const float* dlt = lse + SK;
+            const float* nlse = reinterpret_cast<const float*>(cur + S::ROWS + S::TRANS);
+            const float* ndlt = nlse + SK;
 #pragma unroll
             for (int tt = 0; tt < SK / 32; ++tt) {
                 typename C::Frag qa[C::NT], da[C::NT], qt[C::MB * C::KSTEPS], dt[C::MB * C::KSTEPS];
                 load_kfrags<C>(cur + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, qa);
                 load_kfrags<C>(cur + SK * C::KSTR + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, da);
-                load_vfrags<C, true>(cur + S::ROWS, S::TGS, 32 * tt, lane, qt);
-                load_vfrags<C, true>(cur + S::ROWS + 32 * C::MB * S::TGS, S::TGS, 32 * tt, lane, dt);
+                load_vfrags<C, true, S::MASK>(cur + S::ROWS, S::TGS, 32 * tt, lane, qt);
+                load_vfrags<C, true, S::MASK>(cur + S::ROWS + 32 * C::MB * S::TGS, S::TGS, 32 * tt, lane, dt);
                 // Register r of lane group g holds query kperm(acc_row(r, g)) of the tile.
-                f32x16 init;
-                float dl[16];
+                // The score accumulator starts at -lse (log2 units) and the dP one at -Delta.
+                f32x16 init, dinit;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int qq = 32 * tt + kperm<C::E, C::KS>(acc_row(r, g));
-                    init[r] = -lse[qq];
-                    dl[r] = dlt[qq];
+                    init[r] = nlse[qq];
+                    dinit[r] = ndlt[qq];
                 }
                 const f32x16 s = score_tile<C>(qa, kf, init);
-                const f32x16 dp = score_tile<C>(da, vf);
+                const f32x16 dpd = score_tile<C>(da, vf, dinit);  // dP - Delta
                 float p[16], ds[16];
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     p[r] = __builtin_amdgcn_exp2f(s[r]);
-                    ds[r] = a.M > 1 ? p[r] * (dp[r] - dl[r]) : 0.f;  // kernels.py:230-233
+                    ds[r] = p[r] * dpd[r];
                 }
 #pragma unroll
                 for (int ks = 0; ks < C::KSTEPS; ++ks) {
@@ -636,13 +697,14 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
                     }
                 }
             }
-            if (nx < total) regs.store(lds + (buf ^ 1) * S::SIZE);
+            if (more) regs.store(lds + (buf ^ 1) * S::SIZE);
             __syncthreads();
             buf ^= 1;
         }
     }
     if (!kok) return;
-    const float inv_sqrt_d = 1.f / sqrtf((float)D);
+    // One summary: dS = 0 exactly (kernels.py:230-233), so dK = 0.
+    const float inv_sqrt_d = a.M > 1 ? 1.f / sqrtf((float)D) : 0.f;
     float* dk = a.dsk_part + (((int64_t)split * a.B * a.G + bg) * a.Mp + key) * D;
     float* dv = a.dsv_part + (((int64_t)split * a.B * a.G + bg) * a.Mp + key) * D;
 #pragma unroll

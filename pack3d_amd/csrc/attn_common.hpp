@@ -143,9 +143,20 @@ __device__ __forceinline__ void init_v_padding(typename C::T_* V, int vstride, i
     }
 }
 
+// Column of element (row, col) in a transposed buffer whose 8-column groups
+// are XOR-swizzled by row: group ^= (row / 8) & MASK (MASK = 0: no swizzle).
+// Rows 8 apart start in different bank ranges, so a 16-bit store of 6 channels x
+// 11 consecutive columns per wave spreads over the banks, while a 16-byte read
+// of 8 consecutive rows at one logical group stays conflict-free.
+template <int MASK>
+__device__ __forceinline__ int swz_col(int row, int col) {
+    return MASK ? col ^ (((row >> 3) & MASK) << 3) : col;
+}
+
 // Value fragments of block mb / k-step ks for a tile whose key 0 sits at
-// column `col` of a transposed V buffer with 32 * MB rows.
-template <typename C, bool ALIGNED16>
+// column `col` of a transposed V buffer with 32 * MB rows (8-column groups
+// swizzled by swz_col<MASK>).
+template <typename C, bool ALIGNED16, int MASK = 0>
 __device__ __forceinline__ void load_vfrags(const typename C::T_* Vs, int vstride, int col, int lane,
                                             typename C::Frag* vf) {
     typedef typename C::T_ T;
@@ -154,7 +165,8 @@ __device__ __forceinline__ void load_vfrags(const typename C::T_* Vs, int vstrid
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
         for (int ks = 0; ks < C::KSTEPS; ++ks) {
-            const T* p = Vs + (32 * mb + qi) * vstride + col + ks * C::KS + C::E * g;
+            const int row = 32 * mb + qi;
+            const T* p = Vs + row * vstride + swz_col<MASK>(row, col + ks * C::KS + C::E * g);
             vf[mb * C::KSTEPS + ks] = ALIGNED16 ? frag_load16<T>(p) : frag_load8<T>(p);
         }
 }

@@ -493,8 +493,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
 // LDS) for the global dK/dV pass: q and dO_G rows (row stride KSTR), q and
 // dO_G transposed (row stride SK + EP, zero padding rows), and -lse_G (log2
 // units; -inf past the last query) and -Delta_G.  Each thread moves PI
-// 16-byte pieces; their offsets inside a stage are computed once (qoff), so a
-// stage load is one 64-bit add per piece on top of the stage's scalar base.
+// 16-byte pieces.
 template <typename C, int SK>
 struct KvStage {
     typedef typename C::T_ T;
@@ -509,8 +508,10 @@ struct KvStage {
     // 16-bit types: the transposed copies' 8-column groups are swizzled by row.
     static constexpr int MASK = sizeof(T) == 2 ? SK / 8 - 1 : 0;
     uint4 q[PI], d[PI];
-    int64_t qoff[PI];
-    float nlse, ndelta;
+    unsigned qb[PI], db[PI], lb;
+    int qsn;
+    float lse_raw = 0.f, delta_raw = 0.f;
+    int lo = 0, hi = 0;
 
     // Row of piece i inside the stage (SK for a piece past the stage) and its column.
     static __device__ __forceinline__ int piece_row(int i) {
@@ -522,38 +523,44 @@ struct KvStage {
         return (p - (p / PPR) * PPR) * EP;
     }
 
-    __device__ __forceinline__ void init(int64_t qsn) {
+    // Byte offsets of the lane's pieces and of its lse / Delta entry inside a
+    // stage, fixed for the kernel (32-bit: the host checks that SK rows of q
+    // span less than 2^31 bytes).  Rows past max_row (only when the whole
+    // query range is shorter than a stage) repeat row max_row.
+    __device__ __forceinline__ void init(int64_t qsn_, int max_row) {
+        qsn = (int)qsn_;
 #pragma unroll
-        for (int i = 0; i < PI; ++i) qoff[i] = piece_row(i) * qsn + piece_col(i);
+        for (int i = 0; i < PI; ++i) {
+            const int r = min(piece_row(i), max_row);
+            qb[i] = (unsigned)((r * (int)qsn + piece_col(i)) * (int)sizeof(T));
+            db[i] = (unsigned)((r * C::D + piece_col(i)) * (int)sizeof(T));
+        }
+        lb = (unsigned)min((int)threadIdx.x, max_row) * 4u;
     }
 
-    // qs, ds: first q and dO_G row of the stage; ls, dl: its lse_G and Delta_G;
-    // rows: queries of the stage that exist (1..SK).  Rows past them are zero.
-    __device__ __forceinline__ void load(const T* qs, const T* ds, const float* ls, const float* dl, int rows) {
-        if (rows == SK) {
+    // Stage rows start at q (dO_G rows at dO, lse_G and Delta_G at ls, dl);
+    // rows [lo, hi) of the stage are queries of this pass, the others repeat
+    // queries and get lse = +inf in store(), so P = 0 and dS = 0 there.  The
+    // loads use only scalar bases and the loop-invariant offsets: address
+    // temporaries could be overwritten by the stage's MFMAs while the loads
+    // are in flight, and arithmetic on the loaded values here would wait for
+    // them, either of which stalls the compute behind this prefetch.
+    __device__ __forceinline__ void load(const T* qs, const T* ds, const float* ls, const float* dl, int lo_,
+                                         int hi_) {
+        const uint32_t qbytes = (uint32_t)(((SK - 1) * qsn + C::D) * (int)sizeof(T));
+        const __amdgpu_buffer_rsrc_t rq = buffer_rsrc(qs, qbytes);
+        const __amdgpu_buffer_rsrc_t rd = buffer_rsrc(ds, SK * C::D * (uint32_t)sizeof(T));
 #pragma unroll
-            for (int i = 0; i < PI; ++i) {
-                if (PIECES % (64 * kWaves) == 0 || i + 1 < PI || piece_row(i) < SK) {
-                    q[i] = *reinterpret_cast<const uint4*>(qs + qoff[i]);
-                    d[i] = *reinterpret_cast<const uint4*>(ds + piece_row(i) * C::D + piece_col(i));
-                }
+        for (int i = 0; i < PI; ++i)
+            if (PIECES % (64 * kWaves) == 0 || i + 1 < PI || piece_row(i) < SK) {
+                q[i] = buffer_load16(rq, qb[i]);
+                d[i] = buffer_load16(rd, db[i]);
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < PI; ++i) {
-                const int r = piece_row(i);
-                q[i] = d[i] = uint4{0, 0, 0, 0};
-                if (r < rows) {
-                    q[i] = *reinterpret_cast<const uint4*>(qs + qoff[i]);
-                    d[i] = *reinterpret_cast<const uint4*>(ds + r * C::D + piece_col(i));
-                }
-            }
-        }
         if (threadIdx.x < SK) {
-            const bool live = (int)threadIdx.x < rows;
-            nlse = live ? -ls[threadIdx.x] * kLog2e : -INFINITY;
-            ndelta = live ? -dl[threadIdx.x] : 0.f;
+            lse_raw = buffer_load_f32(buffer_rsrc(ls, SK * 4), lb);
+            delta_raw = buffer_load_f32(buffer_rsrc(dl, SK * 4), lb);
         }
+        lo = lo_, hi = hi_;
     }
 
     __device__ __forceinline__ void store(T* stage) const {
@@ -577,8 +584,9 @@ struct KvStage {
         }
         if (threadIdx.x < SK) {
             float* f = reinterpret_cast<float*>(stage + ROWS + TRANS);
-            f[threadIdx.x] = nlse;
-            f[SK + threadIdx.x] = ndelta;
+            const bool live = (int)threadIdx.x >= lo && (int)threadIdx.x < hi;
+            f[threadIdx.x] = live ? -lse_raw * kLog2e : -INFINITY;
+            f[SK + threadIdx.x] = live ? -delta_raw : 0.f;
         }
     }
 };
@@ -607,6 +615,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
     typename C::Frag kf[C::NT], vf[C::NT];
     load_row_frags<C>(tp<T>(a.sk) + (bg * a.Mp + (kok ? key : 0)) * D, kok, g, kf);
     load_row_frags<C>(tp<T>(a.sv_rows) + (bg * a.Mp + (kok ? key : 0)) * D, kok, g, vf);
+#pragma unroll
+    for (int t = 0; t < C::NT; ++t) settle(kf[t]), settle(vf[t]);
     f32x16 acck[C::MB], accv[C::MB];
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
@@ -624,24 +634,26 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
     zero_padding_rows<C>(lds + S::SIZE + S::ROWS + 32 * C::MB * S::TGS, S::TGS, SK);
     const int total = stages * rep;
     if (total > 0) {
-        // Stage (h, qb): query head h of the group, queries [qb, qb + SK).  The
-        // stage pointers advance by additions: SK rows within a head, one head
-        // (back to q0) when a head's range ends.
+        // Stage (h, qb): query head h of the group, queries [qb, min(qb + SK, q1)).
+        // Its rows start at bp = min(qb, N - SK) (0 when N < SK), so every
+        // stage reads SK existing rows at the same offsets; rows below qb - bp
+        // belong to the stage before it and are masked.
         const int h0 = kvh * rep;
         const int64_t bh0 = (int64_t)b * a.H + h0;
-        const T* q_head = tp<T>(a.q) + b * a.qsb + h0 * a.qsh + q0 * a.qsn;
-        const T* do_head = tp<T>(a.dog) + (bh0 * a.N + q0) * D;
-        const float* ls_head = a.lse_g + bh0 * a.N + q0;
-        const float* dl_head = a.dg + bh0 * a.N + q0;
-        const int64_t q_step = SK * a.qsn;
-        const T* qs = q_head;
-        const T* ds = do_head;
-        const float* ls = ls_head;
-        const float* dl = dl_head;
+        const T* q_head = tp<T>(a.q) + b * a.qsb + h0 * a.qsh;
+        const T* do_head = tp<T>(a.dog) + bh0 * a.N * D;
+        const float* ls_head = a.lse_g + bh0 * a.N;
+        const float* dl_head = a.dg + bh0 * a.N;
+        const int last = a.N >= SK ? a.N - SK : 0;
+        auto load_stage = [&](S& regs, int qb) __attribute__((always_inline)) {
+            const int bp = min(qb, last);
+            regs.load(q_head + (int64_t)bp * a.qsn, do_head + (int64_t)bp * D, ls_head + bp, dl_head + bp, qb - bp,
+                      min(SK, min(q1, a.N) - bp));
+        };
         int nq = q0;
         S regs;
-        regs.init(a.qsn);
-        regs.load(qs, ds, ls, dl, min(SK, a.N - nq));
+        regs.init(a.qsn, min(SK, a.N) - 1);
+        load_stage(regs, nq);
         regs.store(lds);
         __syncthreads();
         int buf = 0;
@@ -654,11 +666,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
                 do_head += (int64_t)a.N * D;
                 ls_head += a.N;
                 dl_head += a.N;
-                qs = q_head, ds = do_head, ls = ls_head, dl = dl_head;
-            } else {
-                qs += q_step, ds += SK * D, ls += SK, dl += SK;
             }
-            if (more) regs.load(qs, ds, ls, dl, min(SK, a.N - nq));
+            if (more) load_stage(regs, nq);
             const T* cur = lds + buf * S::SIZE;
             const float* nlse = reinterpret_cast<const float*>(cur + S::ROWS + S::TRANS);
             const float* ndlt = nlse + SK;
@@ -758,6 +767,8 @@ int fill_bwd(const p3d_bwd_args& x, BwdDev& d) {
     P3D_REQUIRE(x.summaries >= 1, "need at least one summary");
     P3D_REQUIRE(view_ok(x.q, es) && view_ok(x.kl, es) && view_ok(x.vl, es) && view_ok(x.dy, es),
                 "q/k/v/dy rows must be 16-byte aligned");
+    // The summary dK/dV stages address 64 query rows with 32-bit byte offsets.
+    P3D_REQUIRE(x.q.sn >= 0 && x.q.sn < (int64_t)1 << 23, "q token stride must be below 2^23 elements");
     d = BwdDev{};
     d.B = x.batch, d.H = x.heads, d.G = x.kv_heads, d.N = x.tokens, d.M = x.summaries;
     d.Mp = (int)cdiv(x.summaries, 32) * 32;

@@ -119,6 +119,41 @@ __device__ __forceinline__ constexpr int kperm(int rho) {
     return (r / E) * KS + E * g + (r % E);
 }
 
+// Completes the loads of x at this point (an empty asm that reads it).  A
+// value loaded before a loop and first used inside it would otherwise get its
+// wait inside the loop, where the in-order load counter also makes that wait
+// cover the loop's own prefetches on every iteration.
+template <typename X>
+__device__ __forceinline__ void settle(const X& x) {
+    asm volatile("" ::"v"(x));
+}
+
+// Raw buffer resource over [base, base + bytes) of global memory, for buffer
+// loads with a scalar base and 32-bit per-lane byte offsets (offsets past
+// `bytes` read zero).  base must be wave-uniform; it is moved to scalar
+// registers here.  The loads need no per-lane address arithmetic, so no
+// address temporaries stay live while they are in flight.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t v = reinterpret_cast<uint64_t>(base);
+    // readfirstlane returns a signed int: each half goes through uint32_t so
+    // that widening it does not sign-extend the low word into the high one.
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    const uint64_t u = ((uint64_t)hi << 32) | (uint64_t)lo;
+    // Word 3: 32-bit data format (the raw-buffer setting of gfx9 parts).
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const v4u x = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+    return uint4{x[0], x[1], x[2], x[3]};
+}
+
+__device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
+}
+
 // --------------------------------------------------------------- wave
 // Value held by lane l ^ 32.
 __device__ __forceinline__ float swap_half(float x) { return __shfl_xor(x, 32); }

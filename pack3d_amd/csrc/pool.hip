@@ -74,9 +74,15 @@ __device__ __forceinline__ int4 pair_meta(const int32_t* pairs, int j) {
     return int4{base, axis == 0 ? stride : 0, axis == 1 ? stride : 0, axis == 2 ? stride : 0};
 }
 
+// Product of two non-negative values below 2^24, as one 24-bit multiply
+// (v_mul_u32_u24; HIP's __mul24 is an out-of-line library call here).
+__device__ __forceinline__ int mul_u24(int x, int y) {
+    return (int)(((unsigned)x & 0xffffffu) * ((unsigned)y & 0xffffffu));
+}
+
 __device__ __forceinline__ float2 pair_cs(const int4& p, const float2* tab, const int pos[3]) {
     // Table indices are below 2^23 (checked on the host): 24-bit products.
-    return tab[p.x + __mul24(p.y, pos[0]) + __mul24(p.z, pos[1]) + __mul24(p.w, pos[2])];
+    return tab[p.x + mul_u24(p.y, pos[0]) + mul_u24(p.z, pos[1]) + mul_u24(p.w, pos[2])];
 }
 
 // Rotate a run of EP channels starting at c0 with (cos, sin) from `tab`
@@ -494,8 +500,8 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
             for (int p = 0; p < PPR; ++p) {
                 float kx[EP];
                 unpack_piece<T, EP>(kr[p], kx);
-                const int e0 = pm[p].x + __mul24(pm[p].y, pos[0]) + __mul24(pm[p].z, pos[1]) +
-                               __mul24(pm[p].w, pos[2]);
+                const int e0 = pm[p].x + mul_u24(pm[p].y, pos[0]) + mul_u24(pm[p].z, pos[1]) +
+                               mul_u24(pm[p].w, pos[2]);
                 float2 cs[EP / 2];
                 if (runs >> p & 1) {
 #pragma unroll

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 4
+#define P3D_ABI_VERSION 5
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -230,6 +230,20 @@ int p3d_project(const p3d_project_args* args, void* stream);
  * 512}; dim a multiple of 32, at most 512. */
 int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int32_t k,
                      int32_t dim, int32_t dtype, void* stream);
+
+/* Weight gradient of a linear map y = x W^T (the W part of the backward of
+ * the layer's to_q, to_kv, gate and to_out nn.Linear maps, attention.py:64-67,
+ * 85,89; torch computes it as dy^T x): dw[o][i] = sum over rows n of
+ * dy[n][o] x[n][i] with fp32 accumulation, written as fp32 [out_features,
+ * in_features].  dy [rows, out_features] and x [rows, in_features] are
+ * fp16 or bf16 with row strides ldy, ldx (elements, multiples of 8, 16-byte
+ * aligned rows).  The rows are split into `splits` ranges whose fp32
+ * partials go to workspace [splits, out_features, in_features] and are then
+ * summed in order (deterministic).  out_features a positive multiple of 8;
+ * in_features a multiple of 32, at most 256. */
+int p3d_weight_grad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float* dw, float* workspace,
+                    int64_t rows, int32_t out_features, int32_t in_features, int32_t splits, int32_t dtype,
+                    void* stream);
 
 /* ---- backward (replaces kernels.py:313-356, autograd.py:19-28) --------- */
 

@@ -4,13 +4,15 @@ Same constructor, parameters (names, shapes, initialisation order) and
 forward as ``PACK3DAttention`` of amilworks/Pack3D (``src/pack3d/attention.py``),
 with ``backend="hip"``.  In the no-grad forward (fp16 / bf16) LayerNorm,
 to_q, to_kv, the gate map and its softmax run as one kernel
-(``p3d_project``); with autograd active, or for fp32 models, they are the
-torch ops (LayerNorm on the HIP kernel when no gradient is needed).  The
+(``p3d_project``); with autograd active in fp16 / bf16 the linear maps are
+``linear.InputProjections`` / ``linear.OutputResidual`` (torch GEMMs forward,
+weight gradients from ``p3d_weight_grad``); for fp32 models they are the
+torch modules (LayerNorm on the HIP kernel when no gradient is needed).  The
 rotation, pooling, local and global attention and their fusion run in
 ``libpack3d_hip.so``, and so does ``x + to_out(y)`` in the no-grad fp16 /
-bf16 forward (``p3d_out_residual``; otherwise one hipBLASLt GEMM with the
-residual as its C operand).  The projections are consumed as strided views,
-without copies.
+bf16 forward (``p3d_out_residual``; otherwise one GEMM with the residual as
+its C operand).  The projections are consumed as strided views, without
+copies.
 """
 from __future__ import annotations
 
@@ -21,6 +23,7 @@ from torch import nn
 
 from . import _lib
 from .core import SUPPORTED_HEAD_DIMS, pack3d_hip_rope
+from .linear import InputProjections, OutputResidual, compute_dtype
 from .geometry import TokenLayout
 from .rope import axial_rope, balanced_pairs, packed_rope
 
@@ -147,8 +150,12 @@ class PACK3DAttention(nn.Module):
             gate = gp.transpose(1, 2)
         else:
             xn = layer_norm(self.norm, x)
-            qp, kvp = self.to_q(xn), self.to_kv(xn)
-            gate = self.gate(xn).view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
+            if self._hip_linear(x):
+                qp, kvp, gl = InputProjections.apply(xn, self.to_q.weight, self.to_kv.weight, self.gate.weight,
+                                                     self.gate.bias, compute_dtype(x))
+            else:
+                qp, kvp, gl = self.to_q(xn), self.to_kv(xn), self.gate(xn)
+            gate = gl.view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
         q = qp.view(b, n, self.heads, self.head_dim).transpose(1, 2)
         kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
                           for t in kvp.view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
@@ -173,9 +180,26 @@ class PACK3DAttention(nn.Module):
         out = pack3d_hip_rope(q, kl, vl, kg, vg, self.pool_weight, self.slot_bias, gate, self.local_scale,
                               self.global_scale, layout.geometry, rope, temperature=self.temperature)
         # x + to_out(out): one kernel in the no-grad forward, else one GEMM with the
-        # residual as its C operand (to_out has no bias).
+        # residual as its C operand (to_out has no bias), with a HIP weight gradient
+        # in 16-bit training.
         o = out.transpose(1, 2).reshape(b * n, -1)
         fused = fused_out_residual(self, x, o)
         if fused is not None:
             return fused.view(b, n, self.dim)
+        if self._hip_linear(x):
+            return OutputResidual.apply(x.reshape(b * n, self.dim), o, self.to_out.weight,
+                                        compute_dtype(x)).view(b, n, self.dim)
         return torch.addmm(x.reshape(b * n, self.dim), o, self.to_out.weight.t()).view(b, n, self.dim)
+
+    def _hip_linear(self, x):
+        """Whether the linear maps run as InputProjections / OutputResidual
+        (weight gradients from p3d_weight_grad): autograd active, a CUDA input
+        and a 16-bit compute type, the gate with a bias, and no hooks or
+        parametrisations on the linear modules that the functions would skip."""
+        mods = (self.to_q, self.to_kv, self.gate, self.to_out)
+        params = [m.weight for m in mods] + [self.gate.bias]
+        return (torch.is_grad_enabled() and x.is_cuda and compute_dtype(x) is not None
+                and (x.requires_grad or any(p.requires_grad for p in params))
+                and self.gate.bias is not None and self.to_q.bias is None and self.to_kv.bias is None
+                and self.to_out.bias is None
+                and all(type(m) is nn.Linear and not m._forward_hooks and not m._forward_pre_hooks for m in mods))

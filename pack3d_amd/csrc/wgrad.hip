@@ -1,0 +1,196 @@
+// Weight gradients of the PACK3D layer's linear maps (to_q, to_kv, gate and
+// to_out of attention.py:64-67,85,89 of amilworks/Pack3D): for y = x W^T,
+// dW[o][i] = sum over tokens n of dy[n][o] x[n][i], accumulated in fp32.
+// The contraction runs over all tokens (262,144 at 64^3) while W is small
+// (at most a few hundred rows), so the tokens are split across workgroups
+// and each writes an fp32 partial; a second kernel sums the partials in a
+// fixed order (deterministic).
+//
+// A workgroup owns 128 output rows (4 waves x 32) and a token range, taken
+// 32 tokens per stage.  A stage of dy [32 tokens x 128 rows] and of x [32
+// tokens x I] is loaded with 16-byte row pieces (the next stage in flight
+// while the current one is multiplied) and stored row-major in LDS.  The
+// MFMA operands need 8 consecutive tokens of one column per lane; they come
+// out of the row-major tiles through ds_read_b64_tr_b16, two 8-byte
+// transposed reads per fragment, so nothing is transposed on the way in.
+// Each wave then multiplies its 32 x 16-token A fragment with the I / 32
+// shared x fragments: D = dy^T x, 32 rows by I columns per wave.
+#include "common.hpp"
+
+namespace p3d {
+namespace {
+
+constexpr int kWgWaves = 4;
+constexpr int kWgRows = 32 * kWgWaves;  // output rows per workgroup
+constexpr int kWgTok = 32;              // tokens per stage
+
+// Row stride (elements of a 16-bit type) of an LDS tile w elements wide: the
+// stride in dwords is 16 mod 32, so the four consecutive rows that a 16-lane
+// block reads through one transposed load start in four distinct 16-bank
+// ranges; rows stay 16-byte aligned.
+constexpr int tile_stride(int w) { return w + 2 * ((16 - (w / 2) % 32 + 32) % 32); }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef short v8s __attribute__((ext_vector_type(8)));
+
+// MFMA operand fragment (32x32x16 layout: lane L holds index L % 32 of the
+// M or N dimension and contraction indices 8 (L / 32) .. + 8) from a
+// row-major LDS tile whose rows are the contraction index (tokens): rows
+// k0 + 8 (L / 32) + t, column c0 + L % 32.  ds_read_b64_tr_b16 hands lane
+// B + 4a + e of each 16-lane block element e of the 8-byte windows addressed
+// by lanes B + a + 4j (j = 0..3) as its values j, so lane L addresses row
+// k0 + 8 (L / 32) + (L % 16) / 4 (four rows further for the second read) at
+// column c0 + 16 ((L / 16) % 2) + 4 (L % 4).
+template <typename T>
+__device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* tile, int stride, int k0, int c0, int lane) {
+    const int row = k0 + 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int col = c0 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    typedef __attribute__((address_space(3))) v4s* lds_v4s;
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(tile + row * stride + col));
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(tile + (row + 4) * stride + col));
+    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(typename Mma<T>::Frag, v);
+}
+
+// Partial dW of token range [blockIdx.y * per, + per) for output rows
+// [blockIdx.x * 128, + 128), written to part[blockIdx.y][o][i].
+template <typename T, int IT>
+__global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(const T* dy, int64_t ldy, const T* x, int64_t ldx,
+                                                        float* part, int64_t rows, int O, int64_t per) {
+    typedef Mma<T> M;
+    constexpr int I = 32 * IT;
+    constexpr int SA = tile_stride(kWgRows), SB = tile_stride(I);
+    constexpr int STAGE = kWgTok * (SA + SB);             // elements
+    constexpr int PA = kWgTok * (kWgRows / 8) / (64 * kWgWaves);            // dy pieces per thread
+    constexpr int BP = kWgTok * (I / 8);                                     // x pieces per stage
+    constexpr int PB = (BP + 64 * kWgWaves - 1) / (64 * kWgWaves);           // x pieces per thread
+    static_assert(PA * 64 * kWgWaves == kWgTok * (kWgRows / 8), "dy stage pieces must divide evenly");
+    __shared__ __align__(16) T lds[2 * STAGE];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
+    const int ob = blockIdx.x * kWgRows;
+    const int64_t n0 = (int64_t)blockIdx.y * per, n1 = min(rows, n0 + per);
+    const bool active = ob + 32 * wave < O;  // wave-uniform
+
+    u32x4 ra[PA], rb[PB];
+    auto fetch = [&](int64_t t0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PA; ++i) {
+            const int p = tid + i * 64 * kWgWaves, r = p / (kWgRows / 8), c = (p % (kWgRows / 8)) * 8;
+            const int64_t n = t0 + r;
+            ra[i] = u32x4{0, 0, 0, 0};
+            if (n < n1 && ob + c < O) ra[i] = *reinterpret_cast<const u32x4*>(dy + n * ldy + ob + c);
+        }
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const int p = tid + i * 64 * kWgWaves, r = p / (I / 8), c = (p % (I / 8)) * 8;
+            const int64_t n = t0 + r;
+            rb[i] = u32x4{0, 0, 0, 0};
+            if (p < BP && n < n1) rb[i] = *reinterpret_cast<const u32x4*>(x + n * ldx + c);
+        }
+    };
+    auto stage = [&](T* st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PA; ++i) {
+            const int p = tid + i * 64 * kWgWaves, r = p / (kWgRows / 8), c = (p % (kWgRows / 8)) * 8;
+            *reinterpret_cast<u32x4*>(st + r * SA + c) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const int p = tid + i * 64 * kWgWaves, r = p / (I / 8), c = (p % (I / 8)) * 8;
+            if (p < BP) *reinterpret_cast<u32x4*>(st + kWgTok * SA + r * SB + c) = rb[i];
+        }
+    };
+
+    f32x16 acc[IT];
+#pragma unroll
+    for (int t = 0; t < IT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+    if (n0 < n1) {
+        fetch(n0);
+        stage(lds);
+        __syncthreads();
+        int buf = 0;
+        for (int64_t t0 = n0; t0 < n1; t0 += kWgTok) {
+            const bool more = t0 + kWgTok < n1;
+            if (more) fetch(t0 + kWgTok);
+            const T* cur = lds + buf * STAGE;
+            // Waves past the last output row multiply the zero columns of the
+            // dy tile: no branch around the MFMAs, whose accumulators would
+            // otherwise be copied between register files at the join.
+#pragma unroll
+            for (int ks = 0; ks < kWgTok / 16; ++ks) {
+                const typename M::Frag fa = frag_tr<T>(cur, SA, 16 * ks, 32 * wave, lane);
+#pragma unroll
+                for (int t = 0; t < IT; ++t)
+                    acc[t] = M::mfma(fa, frag_tr<T>(cur + kWgTok * SA, SB, 16 * ks, 32 * t, lane), acc[t]);
+            }
+            if (more) stage(lds + (buf ^ 1) * STAGE);
+            __syncthreads();
+            buf ^= 1;
+        }
+    }
+    if (!active) return;
+    // D row acc_row(r, g) is output row ob + 32 wave + that; column lane % 32 of tile t is input 32 t + lane % 32.
+    float* out = part + (int64_t)blockIdx.y * O * I;
+#pragma unroll
+    for (int t = 0; t < IT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int o = ob + 32 * wave + acc_row(r, g);
+            if (o < O) out[(int64_t)o * I + 32 * t + (lane & 31)] = acc[t][r];
+        }
+}
+
+// dw[e] = sum over splits s (in order) of part[s][e].
+__global__ __launch_bounds__(256) void k_wgrad_reduce(const float* part, float* dw, int64_t count, int splits) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= count) return;
+    float s = 0.f;
+    for (int k = 0; k < splits; ++k) s += part[(int64_t)k * count + e];
+    dw[e] = s;
+}
+
+template <typename T>
+int launch_wgrad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float* dw, float* part, int64_t rows, int O,
+                 int I, int splits, hipStream_t s) {
+    const int64_t per = cdiv(cdiv(rows, splits), kWgTok) * kWgTok;
+    const int used = (int)cdiv(rows, per);
+    const dim3 grid((unsigned)cdiv(O, kWgRows), (unsigned)used);
+    switch (I / 32) {
+#define CASE(IT)                                                                                                \
+    case IT:                                                                                                    \
+        k_wgrad<T, IT><<<grid, 64 * kWgWaves, 0, s>>>((const T*)dy, ldy, (const T*)x, ldx, part, rows, O, per); \
+        break;
+        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+#undef CASE
+        default: return fail(P3D_EUNSUPPORTED, "in_features must be a multiple of 32, at most 256");
+    }
+    const int64_t count = (int64_t)O * I;
+    k_wgrad_reduce<<<(unsigned)cdiv(count, 256), 256, 0, s>>>(part, dw, count, used);
+    return check_launch("p3d_weight_grad");
+}
+
+}  // namespace
+}  // namespace p3d
+
+using namespace p3d;
+
+extern "C" int p3d_weight_grad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float* dw, float* workspace,
+                               int64_t rows, int32_t out_features, int32_t in_features, int32_t splits, int32_t dtype,
+                               void* stream) {
+    P3D_REQUIRE(dy && x && dw && workspace, "null pointer argument");
+    P3D_REQUIRE(dtype == P3D_F16 || dtype == P3D_BF16, "dtype must be fp16 or bf16");
+    P3D_REQUIRE(rows >= 1 && splits >= 1, "need at least one row and one split");
+    P3D_REQUIRE(out_features >= 8 && out_features % 8 == 0, "out_features must be a positive multiple of 8");
+    P3D_REQUIRE(in_features >= 32 && in_features % 32 == 0 && in_features <= 256,
+                "in_features must be a multiple of 32, at most 256");
+    P3D_REQUIRE(ldy >= out_features && ldy % 8 == 0 && ldx >= in_features && ldx % 8 == 0,
+                "row strides must cover the rows and keep 16-byte alignment");
+    P3D_REQUIRE(aligned16(dy) && aligned16(x), "dy and x must be 16-byte aligned");
+    P3D_REQUIRE(cdiv(out_features, kWgRows) < 65536 && splits < 65536, "grid too large");
+    return dtype == P3D_F16 ? launch_wgrad<_Float16>(dy, ldy, x, ldx, dw, workspace, rows, out_features, in_features,
+                                                     splits, as_stream(stream))
+                            : launch_wgrad<__bf16>(dy, ldy, x, ldx, dw, workspace, rows, out_features, in_features,
+                                                   splits, as_stream(stream));
+}

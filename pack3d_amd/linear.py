@@ -1,0 +1,122 @@
+"""The layer's linear maps under autograd in fp16 / bf16, with the weight
+gradients from the HIP kernel ``p3d_weight_grad``.
+
+For y = x W^T the weight gradient dW = dy^T x contracts over every token
+(262,144 at 64^3) into a small matrix; the library GEMM runs it with a
+handful of workgroups.  ``p3d_weight_grad`` splits the tokens over the whole
+GPU and sums fp32 partials in a fixed order.  The forward products and the
+input gradients stay torch GEMMs.  These functions replace the to_q, to_kv,
+gate (attention.py:64-67,85 of amilworks/Pack3D) and to_out + residual
+(attention.py:89) steps of ``PACK3DAttention.forward`` when it runs in a
+16-bit compute type with autograd active; weight gradients are accumulated
+in fp32 (torch's autocast path rounds them to the compute type first).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+# Rows per split: enough splits to fill the GPU at large token counts while
+# the fp32 partials ([splits, out, in]) stay a small fraction of the inputs.
+ROWS_PER_SPLIT = 2048
+MAX_SPLITS = 128
+
+
+def compute_dtype(x):
+    """The 16-bit type the layer's linear maps run in: the autocast type when
+    autocast is on for x's device, else x's own type (None when that is not
+    fp16 / bf16)."""
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+    else:
+        dt = x.dtype
+    return dt if dt in (torch.float16, torch.bfloat16) else None
+
+
+def weight_grad_supported(out_features, in_features):
+    return out_features >= 8 and out_features % 8 == 0 and in_features % 32 == 0 and 32 <= in_features <= 256
+
+
+def weight_grad(dy, x):
+    """dW = dy^T x in fp32 for dy [rows, out], x [rows, in] of one 16-bit type
+    (``p3d_weight_grad``; torch's product in fp32 where the kernel does not
+    take the shape)."""
+    rows, out_f = dy.shape
+    in_f = x.shape[1]
+    if not weight_grad_supported(out_f, in_f) or dy.dtype != x.dtype or dy.dtype not in (torch.float16,
+                                                                                           torch.bfloat16):
+        return torch.mm(dy.t().float(), x.float())
+    dy = dy if dy.stride(1) == 1 and dy.stride(0) % 8 == 0 else dy.contiguous()
+    x = x if x.stride(1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()
+    if dy.data_ptr() % 16 or x.data_ptr() % 16:
+        dy, x = dy.clone(), x.clone()
+    splits = max(1, min(MAX_SPLITS, rows // ROWS_PER_SPLIT))
+    dw = torch.empty(out_f, in_f, dtype=torch.float32, device=dy.device)
+    work = torch.empty(splits, out_f, in_f, dtype=torch.float32, device=dy.device)
+    _lib.call("p3d_weight_grad", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), dw.data_ptr(),
+              work.data_ptr(), rows, out_f, in_f, splits, _lib.DTYPES[dy.dtype], _lib.stream_of(dy.device))
+    return dw
+
+
+def _rows(t):
+    return t.reshape(-1, t.shape[-1])
+
+
+class InputProjections(torch.autograd.Function):
+    """(x Wq^T, x Wkv^T, x Wg^T + bg) of the normalised tokens x in the 16-bit
+    type dt (attention.py:64-67,85): x is rounded to dt once and shared by
+    the three products; the backward returns dx in x's dtype (the three
+    input gradients summed in fp32) and fp32 weight gradients cast to the
+    parameters' dtypes."""
+
+    @staticmethod
+    def forward(ctx, x, wq, wkv, wg, bg, dt):
+        x16 = _rows(x).to(dt).contiguous()
+        ws = [w.to(dt) for w in (wq, wkv, wg)]
+        q = torch.mm(x16, ws[0].t())
+        kv = torch.mm(x16, ws[1].t())
+        gl = torch.addmm(bg.to(dt), x16, ws[2].t())
+        ctx.save_for_backward(x16, *ws)
+        ctx.meta = (x.shape, x.dtype, wq.dtype, wkv.dtype, wg.dtype, bg.dtype)
+        lead = x.shape[:-1]
+        return q.view(*lead, -1), kv.view(*lead, -1), gl.view(*lead, -1)
+
+    @staticmethod
+    def backward(ctx, dq, dkv, dgl):
+        x16, wq, wkv, wg = ctx.saved_tensors
+        shape, x_dt, wq_dt, wkv_dt, wg_dt, bg_dt = ctx.meta
+        dx = torch.zeros(x16.shape, dtype=torch.float32, device=x16.device)
+        grads = []
+        for dy, w, w_dt in ((dq, wq, wq_dt), (dkv, wkv, wkv_dt), (dgl, wg, wg_dt)):
+            if dy is None:
+                grads.append(None)
+                continue
+            dy = _rows(dy).to(x16.dtype)
+            dx.add_(torch.mm(dy, w))
+            grads.append(weight_grad(dy, x16).to(w_dt))
+        dbg = None if dgl is None else _rows(dgl).float().sum(0).to(bg_dt)
+        return dx.view(shape).to(x_dt), grads[0], grads[1], grads[2], dbg, None
+
+
+class OutputResidual(torch.autograd.Function):
+    """x + y Wo^T in the 16-bit type dt (attention.py:89; autocast's
+    torch.addmm): x [rows, dim], y [rows, k].  The backward gives dx = dout
+    (in x's dtype), dy = dout Wo and an fp32 weight gradient."""
+
+    @staticmethod
+    def forward(ctx, x, y, wo, dt):
+        y16 = y.to(dt).contiguous()
+        wo16 = wo.to(dt)
+        out = torch.addmm(x.to(dt), y16, wo16.t())
+        ctx.save_for_backward(y16, wo16)
+        ctx.meta = (x.dtype, y.dtype, wo.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        y16, wo16 = ctx.saved_tensors
+        x_dt, y_dt, wo_dt = ctx.meta
+        d16 = dout.to(y16.dtype)
+        dy = torch.mm(d16, wo16).to(y_dt)
+        return dout.to(x_dt), dy, weight_grad(d16, y16).to(wo_dt), None

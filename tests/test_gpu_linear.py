@@ -1,0 +1,108 @@
+"""The layer's linear maps in 16-bit training: p3d_weight_grad against the
+fp32 product dy^T x, and the layer's gradients through linear.InputProjections
+/ linear.OutputResidual against the same layer on torch's nn.Linear path.
+
+Bars: the kernel accumulates in fp32 over the rows, so against an fp32 GEMM
+of the same 16-bit inputs the relative L2 error is that of fp32 summation
+order (< 1e-5).  Against torch's autocast path, which rounds each weight
+gradient to bf16 before it reaches the fp32 .grad, gradients agree to bf16
+rounding (relative L2 < 1e-2).
+"""
+import math
+
+import pytest
+import torch
+
+import pack3d_amd as p3d
+from pack3d_amd import _lib, linear
+from tests._cases import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _reference(dy, x):
+    return torch.mm(dy.float().t(), x.float())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,out_f,in_f,splits", [(37, 8, 192, 1), (1000, 200, 32, 3), (4099, 136, 256, 7),
+                                                    (70000, 384, 192, 33), (262144, 192, 192, 128)])
+def test_weight_grad_matches_fp32_product(gpu, dtype, rows, out_f, in_f, splits):
+    """Ragged row counts (not multiples of the 32-token stage or of the
+    split), output widths that leave part of a 128-row workgroup idle, every
+    split count from one to the c4 setting, and the c4 size itself."""
+    print(f"weight grad {rows}x{out_f}x{in_f} s{splits} {dtype}", flush=True)
+    gen = torch.Generator(device=gpu).manual_seed(rows + out_f)
+    dy = torch.randn(rows, out_f, device=gpu, generator=gen).to(dtype)
+    x = torch.randn(rows, in_f, device=gpu, generator=gen).to(dtype)
+    dw = torch.empty(out_f, in_f, device=gpu)
+    work = torch.empty(splits, out_f, in_f, device=gpu)
+    _lib.call("p3d_weight_grad", dy.data_ptr(), out_f, x.data_ptr(), in_f, dw.data_ptr(), work.data_ptr(), rows,
+              out_f, in_f, splits, _lib.DTYPES[dtype], _lib.stream_of(gpu))
+    err = rel_l2(dw, _reference(dy, x))
+    print(f"  rel_l2={err:.3g}", flush=True)
+    assert err < 1e-5
+
+
+def test_weight_grad_strided_rows_and_determinism(gpu):
+    """Row strides wider than the rows (column slices of wider tensors, as the
+    layer's projections are) and bit-identical repeats."""
+    print("weight grad strided", flush=True)
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    wide_dy = torch.randn(5000, 400, device=gpu, generator=gen).to(torch.bfloat16)
+    wide_x = torch.randn(5000, 264, device=gpu, generator=gen).to(torch.bfloat16)
+    dy, x = wide_dy[:, 16:208], wide_x[:, 8:200]
+    a = linear.weight_grad(dy, x)
+    b = linear.weight_grad(dy, x)
+    assert torch.equal(a, b)
+    assert rel_l2(a, _reference(dy, x)) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_layer_training_gradients_match_torch_linear(gpu, dtype):
+    """Forward and every gradient of the layer under autocast with the HIP
+    weight gradients, against the same layer with its linear maps on
+    torch's nn.Linear autograd; the kernel path must actually run."""
+    print(f"layer training linear {dtype}", flush=True)
+    torch.manual_seed(0)
+    shape = (8, 16, 12)
+    n = math.prod(shape)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64).to(gpu)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block", device=gpu)
+    x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1)).to(gpu)
+    dy = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(2)).to(gpu)
+
+    def run(hip):
+        layer.zero_grad(set_to_none=True)
+        xg = x.clone().requires_grad_()
+        if not hip:
+            layer._hip_linear = lambda _x: False
+        try:
+            with torch.autocast("cuda", dtype=dtype):
+                y = layer(xg, lay)
+            y.backward(dy.to(y.dtype))
+        finally:
+            layer.__dict__.pop("_hip_linear", None)
+        return y.detach().float(), xg.grad.detach().clone(), {k: p.grad.detach().clone()
+                                                              for k, p in layer.named_parameters()}
+
+    calls = []
+    real = _lib.call
+
+    def counting(name, *args):
+        calls.append(name)
+        return real(name, *args)
+
+    linear._lib.call = counting
+    try:
+        y_h, dx_h, g_h = run(True)
+    finally:
+        linear._lib.call = real
+    assert calls.count("p3d_weight_grad") == 4, calls
+    y_t, dx_t, g_t = run(False)
+    assert rel_l2(y_h, y_t) < 1e-2
+    assert rel_l2(dx_h, dx_t) < 1e-2
+    for k in g_t:
+        err = rel_l2(g_h[k], g_t[k])
+        print(f"  {k}: rel_l2={err:.3g}", flush=True)
+        assert err < 1e-2, (k, err)

@@ -52,6 +52,13 @@ def test_entry_points_reject_bad_arguments_before_launch():
     with pytest.raises(RuntimeError, match="dtype|counts"):
         args.dtype = 7
         _lib.call("p3d_attn_fwd_grid", args, None)
+    # Weight gradient: widths the kernel does not take (never dereferenced).
+    bf16 = _lib.DTYPES[torch.bfloat16]
+    for out_f, in_f, msg in ((12, 192, "out_features"), (8, 48, "in_features"), (8, 288, "in_features")):
+        with pytest.raises(RuntimeError, match=msg):
+            _lib.call("p3d_weight_grad", 16, out_f, 16, in_f, 16, 16, 100, out_f, in_f, 1, bf16, None)
+    with pytest.raises(RuntimeError, match="null pointer"):
+        _lib.call("p3d_weight_grad", None, 8, 16, 32, 16, 16, 100, 8, 32, 1, bf16, None)
 
 
 def test_import_without_gpu_and_no_oracle_import():

@@ -6,8 +6,8 @@
 // and each writes an fp32 partial; a second kernel sums the partials in a
 // fixed order (deterministic).
 //
-// A workgroup owns 128 output rows (4 waves x 32) and a token range, taken
-// 32 tokens per stage.  A stage of dy [32 tokens x 128 rows] and of x [32
+// A workgroup owns 256 output rows (8 waves x 32) and a token range, taken
+// 32 tokens per stage.  A stage of dy [32 tokens x 256 rows] and of x [32
 // tokens x I] is loaded with 16-byte row pieces (the next stage in flight
 // while the current one is multiplied) and stored row-major in LDS.  The
 // MFMA operands need 8 consecutive tokens of one column per lane; they come
@@ -20,7 +20,7 @@
 namespace p3d {
 namespace {
 
-constexpr int kWgWaves = 4;
+constexpr int kWgWaves = 8;
 constexpr int kWgRows = 32 * kWgWaves;  // output rows per workgroup
 constexpr int kWgTok = 32;              // tokens per stage
 
@@ -52,20 +52,25 @@ __device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* tile, int stri
     return __builtin_bit_cast(typename Mma<T>::Frag, v);
 }
 
+template <int IT>
+constexpr int wgrad_stage_elems() { return kWgTok * (tile_stride(kWgRows) + tile_stride(32 * IT)); }
+
 // Partial dW of token range [blockIdx.y * per, + per) for output rows
-// [blockIdx.x * 128, + 128), written to part[blockIdx.y][o][i].
+// [blockIdx.x * 256, + 256), written to part[blockIdx.y][o][i].  Two stages
+// of dynamic LDS (2 * wgrad_stage_elems<IT>() elements).
 template <typename T, int IT>
 __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(const T* dy, int64_t ldy, const T* x, int64_t ldx,
                                                         float* part, int64_t rows, int O, int64_t per) {
     typedef Mma<T> M;
     constexpr int I = 32 * IT;
     constexpr int SA = tile_stride(kWgRows), SB = tile_stride(I);
-    constexpr int STAGE = kWgTok * (SA + SB);             // elements
+    constexpr int STAGE = wgrad_stage_elems<IT>();         // elements
     constexpr int PA = kWgTok * (kWgRows / 8) / (64 * kWgWaves);            // dy pieces per thread
     constexpr int BP = kWgTok * (I / 8);                                     // x pieces per stage
     constexpr int PB = (BP + 64 * kWgWaves - 1) / (64 * kWgWaves);           // x pieces per thread
     static_assert(PA * 64 * kWgWaves == kWgTok * (kWgRows / 8), "dy stage pieces must divide evenly");
-    __shared__ __align__(16) T lds[2 * STAGE];
+    extern __shared__ __align__(16) unsigned char wg_smem[];
+    T* lds = reinterpret_cast<T*>(wg_smem);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
     const int ob = blockIdx.x * kWgRows;
     const int64_t n0 = (int64_t)blockIdx.y * per, n1 = min(rows, n0 + per);
@@ -142,13 +147,26 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(const T* dy, int64_t ld
         }
 }
 
-// dw[e] = sum over splits s (in order) of part[s][e].
-__global__ __launch_bounds__(256) void k_wgrad_reduce(const float* part, float* dw, int64_t count, int splits) {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= count) return;
+// dw[e] = sum over splits of part[s][e] in a fixed order: thread group j of
+// a block (64 elements x 4 groups) sums splits j, j + 4, ... in increasing
+// order, then group 0 adds the four partial sums in order (deterministic).
+constexpr int kRedElems = 64, kRedGroups = 4;
+__global__ __launch_bounds__(kRedElems * kRedGroups) void k_wgrad_reduce(const float* part, float* dw, int64_t count,
+                                                                         int splits) {
+    __shared__ float sums[kRedGroups][kRedElems];
+    const int le = threadIdx.x % kRedElems, grp = threadIdx.x / kRedElems;
+    const int64_t e = (int64_t)blockIdx.x * kRedElems + le;
     float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += part[(int64_t)k * count + e];
-    dw[e] = s;
+    if (e < count)
+        for (int k = grp; k < splits; k += kRedGroups) s += part[(int64_t)k * count + e];
+    sums[grp][le] = s;
+    __syncthreads();
+    if (grp == 0 && e < count) {
+        float t = sums[0][le];
+#pragma unroll
+        for (int j = 1; j < kRedGroups; ++j) t += sums[j][le];
+        dw[e] = t;
+    }
 }
 
 template <typename T>
@@ -158,16 +176,17 @@ int launch_wgrad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float*
     const int used = (int)cdiv(rows, per);
     const dim3 grid((unsigned)cdiv(O, kWgRows), (unsigned)used);
     switch (I / 32) {
-#define CASE(IT)                                                                                                \
-    case IT:                                                                                                    \
-        k_wgrad<T, IT><<<grid, 64 * kWgWaves, 0, s>>>((const T*)dy, ldy, (const T*)x, ldx, part, rows, O, per); \
+#define CASE(IT)                                                                                                  \
+    case IT:                                                                                                      \
+        k_wgrad<T, IT><<<grid, 64 * kWgWaves, 2 * wgrad_stage_elems<IT>() * sizeof(T), s>>>(                      \
+            (const T*)dy, ldy, (const T*)x, ldx, part, rows, O, per);                                             \
         break;
         CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
 #undef CASE
         default: return fail(P3D_EUNSUPPORTED, "in_features must be a multiple of 32, at most 256");
     }
     const int64_t count = (int64_t)O * I;
-    k_wgrad_reduce<<<(unsigned)cdiv(count, 256), 256, 0, s>>>(part, dw, count, used);
+    k_wgrad_reduce<<<(unsigned)cdiv(count, kRedElems), kRedElems * kRedGroups, 0, s>>>(part, dw, count, used);
     return check_launch("p3d_weight_grad");
 }
 

@@ -17,10 +17,18 @@ import torch
 
 from . import _lib
 
-# Rows per split: enough splits to fill the GPU at large token counts while
-# the fp32 partials ([splits, out, in]) stay a small fraction of the inputs.
-ROWS_PER_SPLIT = 2048
-MAX_SPLITS = 128
+# The kernel's workgroups own 256 output rows and a range of rows of dy / x;
+# splits are chosen for about WORKGROUPS workgroups in all (one per compute
+# unit), with at least MIN_ROWS_PER_SPLIT rows each.  The fp32 partials
+# ([splits, out, in]) stay below half of the bytes of dy and x at 64^3.
+WG_ROWS = 256
+WORKGROUPS = 256
+MIN_ROWS_PER_SPLIT = 512
+
+
+def splits_for(rows, out_features):
+    blocks = -(-out_features // WG_ROWS)
+    return max(1, min(-(-WORKGROUPS // blocks), rows // MIN_ROWS_PER_SPLIT))
 
 
 def compute_dtype(x):
@@ -51,7 +59,7 @@ def weight_grad(dy, x):
     x = x if x.stride(1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()
     if dy.data_ptr() % 16 or x.data_ptr() % 16:
         dy, x = dy.clone(), x.clone()
-    splits = max(1, min(MAX_SPLITS, rows // ROWS_PER_SPLIT))
+    splits = splits_for(rows, out_f)
     dw = torch.empty(out_f, in_f, dtype=torch.float32, device=dy.device)
     work = torch.empty(splits, out_f, in_f, dtype=torch.float32, device=dy.device)
     _lib.call("p3d_weight_grad", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), dw.data_ptr(),

@@ -189,6 +189,25 @@ int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tok
 int p3d_layer_norm(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
                    int64_t rows, int32_t dim, int32_t dtype, float eps, void* stream);
 
+/* The same LayerNorm for training (the forward of torch's layer_norm under
+ * autocast, with its output rounded to the compute type that the next
+ * linear maps cast it to): x [rows, dim] of x_dtype, y [rows, dim] of
+ * y_dtype, and each row's mean and 1/sqrt(var + eps) as fp32 [rows] for the
+ * backward.  dim a multiple of x's 16-byte piece, at most 64 pieces. */
+int p3d_layer_norm_train(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
+                         float* mean, float* rstd, int64_t rows, int32_t dim, int32_t x_dtype, int32_t y_dtype,
+                         float eps, void* stream);
+
+/* LayerNorm backward (torch's layer_norm backward): with xhat = (x - mean)
+ * rstd and g = dy * weight, dx = rstd (g - mean(g) - xhat mean(g xhat)) per
+ * row, written as dx_dtype; the affine gradients as fp32 partial sums over
+ * `parts` row ranges, partial[part][0][dim] = sum dy xhat and
+ * partial[part][1][dim] = sum dy (the caller sums the parts).  mean / rstd
+ * from p3d_layer_norm_train. */
+int p3d_layer_norm_bwd(const void* dy, const void* x, const void* weight, int32_t param_dtype, const float* mean,
+                       const float* rstd, void* dx, float* partial, int64_t rows, int32_t dim, int32_t dy_dtype,
+                       int32_t x_dtype, int32_t dx_dtype, int32_t parts, void* stream);
+
 /* Fused input projections of the layer (attention.py:64-67,85): LayerNorm
  * of x [rows, dim], then q = xn Wq^T [rows, q_out], kv = xn Wkv^T
  * [rows, kv_out] (the chunks kl | vl | kg | vg of to_kv) and, for each of

@@ -96,6 +96,10 @@ SIGNATURES = {
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
     "p3d_project": ([ctypes.POINTER(ProjectArgs), _P], c_int32),
     "p3d_out_residual": ([_P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, _P], c_int32),
+    "p3d_layer_norm_train": ([_P, _P, _P, c_int32, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_float, _P],
+                             c_int32),
+    "p3d_layer_norm_bwd": ([_P, _P, _P, c_int32, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32,
+                            c_int32, _P], c_int32),
     "p3d_weight_grad": ([_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_mix_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),

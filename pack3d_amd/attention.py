@@ -23,7 +23,7 @@ from torch import nn
 
 from . import _lib
 from .core import SUPPORTED_HEAD_DIMS, pack3d_hip_rope
-from .linear import InputProjections, OutputResidual, compute_dtype
+from .linear import InputProjections, LayerNormTrain, OutputResidual, compute_dtype, layer_norm_train_supported
 from .geometry import TokenLayout
 from .rope import axial_rope, balanced_pairs, packed_rope
 
@@ -148,13 +148,18 @@ class PACK3DAttention(nn.Module):
         if fused is not None:
             qp, kvp, gp = fused
             gate = gp.transpose(1, 2)
+        elif self._hip_linear(x):
+            dt = compute_dtype(x)
+            if layer_norm_train_supported(self.norm, x):
+                xn = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt)
+            else:
+                xn = layer_norm(self.norm, x)
+            qp, kvp, gl = InputProjections.apply(xn, self.to_q.weight, self.to_kv.weight, self.gate.weight,
+                                                 self.gate.bias, dt)
+            gate = gl.view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
         else:
             xn = layer_norm(self.norm, x)
-            if self._hip_linear(x):
-                qp, kvp, gl = InputProjections.apply(xn, self.to_q.weight, self.to_kv.weight, self.gate.weight,
-                                                     self.gate.bias, compute_dtype(x))
-            else:
-                qp, kvp, gl = self.to_q(xn), self.to_kv(xn), self.gate(xn)
+            qp, kvp, gl = self.to_q(xn), self.to_kv(xn), self.gate(xn)
             gate = gl.view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
         q = qp.view(b, n, self.heads, self.head_dim).transpose(1, 2)
         kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
@@ -193,9 +198,10 @@ class PACK3DAttention(nn.Module):
 
     def _hip_linear(self, x):
         """Whether the linear maps run as InputProjections / OutputResidual
-        (weight gradients from p3d_weight_grad): autograd active, a CUDA input
-        and a 16-bit compute type, the gate with a bias, and no hooks or
-        parametrisations on the linear modules that the functions would skip."""
+        (weight gradients from p3d_weight_grad) and LayerNorm as LayerNormTrain:
+        autograd active, a CUDA input and a 16-bit compute type, the gate with a
+        bias, and no hooks or parametrisations on the linear modules that the
+        functions would skip."""
         mods = (self.to_q, self.to_kv, self.gate, self.to_out)
         params = [m.weight for m in mods] + [self.gate.bias]
         return (torch.is_grad_enabled() and x.is_cuda and compute_dtype(x) is not None

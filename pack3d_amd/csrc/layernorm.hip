@@ -82,6 +82,236 @@ __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, c
     }
 }
 
+// ------------------------------------------------------------ training
+// The same LayerNorm with separate input and output types (fp32 tokens in,
+// the 16-bit compute type out under autocast) that also writes each row's
+// mean and 1/std for the backward.  A lane holds the 16-byte input pieces
+// j, j + 8, ... of its row (EP input elements each) and the same channels of
+// every other per-row tensor.
+template <typename T, int N>
+struct Vec {
+    typedef T type __attribute__((ext_vector_type(N)));
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_n(const T* p, float (&out)[N]) {
+    const typename Vec<T, N>::type v = *reinterpret_cast<const typename Vec<T, N>::type*>(p);
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = to_f32(v[e]);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_n(T* p, const float (&in)[N]) {
+    typename Vec<T, N>::type v;
+#pragma unroll
+    for (int e = 0; e < N; ++e) v[e] = from_f32<T>(in[e]);
+    *reinterpret_cast<typename Vec<T, N>::type*>(p) = v;
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const void* w, const void* b, int param_dtype,
+                                                          TO* y, float* mean_out, float* rstd_out, int64_t rows,
+                                                          int dim, float eps) {
+    constexpr int EP = Piece<TI>::N;
+    __shared__ __align__(16) float lw[kMaxDim], lb[kMaxDim];
+    for (int c = threadIdx.x; c < dim; c += blockDim.x) {
+        lw[c] = load_any(w, c, param_dtype);
+        lb[c] = load_any(b, c, param_dtype);
+    }
+    const int sub = threadIdx.x % kLanesPerRow;
+    const int pieces = dim / EP;
+    const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kLanesPerRow;
+    const bool live = row < rows;
+    const TI* xr = x + (live ? row : 0) * dim;
+    float v[kMaxPiecesPerLane][EP];
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPiecesPerLane; ++i) {
+        const int p = sub + kLanesPerRow * i;
+        if (p < pieces) {
+            load_n<TI, EP>(xr + p * EP, v[i]);
+#pragma unroll
+            for (int e = 0; e < EP; ++e) sum += v[i][e];
+        }
+    }
+    const float mean = group8_sum(sum) / (float)dim;
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPiecesPerLane; ++i) {
+        const int p = sub + kLanesPerRow * i;
+        if (p < pieces)
+#pragma unroll
+            for (int e = 0; e < EP; ++e) {
+                const float c = v[i][e] - mean;
+                sq += c * c;
+            }
+    }
+    const float rstd = 1.f / sqrtf(group8_sum(sq) / (float)dim + eps);
+    __syncthreads();
+    if (!live) return;
+    if (sub == 0) {
+        mean_out[row] = mean;
+        rstd_out[row] = rstd;
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxPiecesPerLane; ++i) {
+        const int p = sub + kLanesPerRow * i;
+        if (p < pieces) {
+            float o[EP];
+#pragma unroll
+            for (int e = 0; e < EP; ++e) {
+                const int c = p * EP + e;
+                o[e] = (v[i][e] - mean) * rstd * lw[c] + lb[c];
+            }
+            store_n<TO, EP>(y + row * dim + p * EP, o);
+        }
+    }
+}
+
+// LayerNorm backward (torch's formula): with xhat = (x - mean) rstd and
+// g = dy * w, dx = rstd (g - mean(g) - xhat mean(g xhat)) per row, and the
+// affine gradients dw = sum_rows dy xhat, db = sum_rows dy.  Blocks stride
+// over the rows; each writes its fp32 partial sums of dw and db to
+// part[block][0 / 1][dim], summed by the caller.  PPL: pieces per lane
+// (ceil(dim / EP / 8)), which sizes the per-lane arrays.
+template <typename TD, typename TI, typename TO, int PPL>
+__global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TI* x, const void* w, int param_dtype,
+                                                        const float* mean_in, const float* rstd_in, TO* dx,
+                                                        float* part, int64_t rows, int dim) {
+    constexpr int EP = Piece<TI>::N;
+    constexpr int GROUPS = 256 / kLanesPerRow;
+    __shared__ __align__(16) float lw[kMaxDim];
+    __shared__ float red[2][kMaxDim];
+    for (int c = threadIdx.x; c < dim; c += blockDim.x) {
+        lw[c] = load_any(w, c, param_dtype);
+        red[0][c] = red[1][c] = 0.f;
+    }
+    __syncthreads();
+    const int sub = threadIdx.x % kLanesPerRow, grp = threadIdx.x / kLanesPerRow;
+    const int pieces = dim / EP;
+    float pw[PPL][EP], pb[PPL][EP];
+#pragma unroll
+    for (int i = 0; i < PPL; ++i)
+#pragma unroll
+        for (int e = 0; e < EP; ++e) pw[i][e] = pb[i][e] = 0.f;
+    const int64_t step = (int64_t)gridDim.x * GROUPS;
+    for (int64_t row = (int64_t)blockIdx.x * GROUPS + grp; row < rows; row += step) {
+        const float mean = mean_in[row], rstd = rstd_in[row];
+        float xh[PPL][EP], g[PPL][EP];
+        float sg = 0.f, sgx = 0.f;
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+            const int p = sub + kLanesPerRow * i;
+            if (p < pieces) {
+                float xv[EP], dv[EP];
+                load_n<TI, EP>(x + row * dim + p * EP, xv);
+                load_n<TD, EP>(dy + row * dim + p * EP, dv);
+#pragma unroll
+                for (int e = 0; e < EP; ++e) {
+                    xh[i][e] = (xv[e] - mean) * rstd;
+                    g[i][e] = dv[e] * lw[p * EP + e];
+                    sg += g[i][e];
+                    sgx += g[i][e] * xh[i][e];
+                    pw[i][e] += dv[e] * xh[i][e];
+                    pb[i][e] += dv[e];
+                }
+            }
+        }
+        const float mg = group8_sum(sg) / (float)dim, mgx = group8_sum(sgx) / (float)dim;
+#pragma unroll
+        for (int i = 0; i < PPL; ++i) {
+            const int p = sub + kLanesPerRow * i;
+            if (p < pieces) {
+                float o[EP];
+#pragma unroll
+                for (int e = 0; e < EP; ++e) o[e] = rstd * (g[i][e] - mg - xh[i][e] * mgx);
+                store_n<TO, EP>(dx + row * dim + p * EP, o);
+            }
+        }
+    }
+    // Partial affine gradients of this block: the row groups in turn (fixed order).
+    for (int k = 0; k < GROUPS; ++k) {
+        if (grp == k)
+#pragma unroll
+            for (int i = 0; i < PPL; ++i) {
+                const int p = sub + kLanesPerRow * i;
+                if (p < pieces)
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) {
+                        red[0][p * EP + e] += pw[i][e];
+                        red[1][p * EP + e] += pb[i][e];
+                    }
+            }
+        __syncthreads();
+    }
+    for (int c = threadIdx.x; c < dim; c += blockDim.x) {
+        part[((int64_t)blockIdx.x * 2 + 0) * dim + c] = red[0][c];
+        part[((int64_t)blockIdx.x * 2 + 1) * dim + c] = red[1][c];
+    }
+}
+
+template <typename TI, typename TO>
+int launch_ln_train(const void* x, const void* w, const void* b, int pdt, void* y, float* mean, float* rstd,
+                    int64_t rows, int dim, float eps, hipStream_t s) {
+    const unsigned blocks = (unsigned)cdiv(rows * kLanesPerRow, 256);
+    k_layer_norm_train<TI, TO><<<blocks, 256, 0, s>>>((const TI*)x, w, b, pdt, (TO*)y, mean, rstd, rows, dim, eps);
+    return check_launch("p3d_layer_norm_train");
+}
+
+template <typename TI>
+int dispatch_ln_train(const void* x, const void* w, const void* b, int pdt, void* y, float* mean, float* rstd,
+                      int64_t rows, int dim, int y_dtype, float eps, hipStream_t s) {
+    switch (y_dtype) {
+        case P3D_F32: return launch_ln_train<TI, float>(x, w, b, pdt, y, mean, rstd, rows, dim, eps, s);
+        case P3D_F16: return launch_ln_train<TI, _Float16>(x, w, b, pdt, y, mean, rstd, rows, dim, eps, s);
+        default: return launch_ln_train<TI, __bf16>(x, w, b, pdt, y, mean, rstd, rows, dim, eps, s);
+    }
+}
+
+template <typename TD, typename TI, typename TO>
+int launch_ln_bwd(const void* dy, const void* x, const void* w, int pdt, const float* mean, const float* rstd,
+                  void* dx, float* part, int64_t rows, int dim, int parts, hipStream_t s) {
+    const int ppl = (int)cdiv(dim / Piece<TI>::N, kLanesPerRow);
+    switch (ppl) {
+#define CASE(P)                                                                                                  \
+    case P:                                                                                                      \
+        k_layer_norm_bwd<TD, TI, TO, P><<<(unsigned)parts, 256, 0, s>>>((const TD*)dy, (const TI*)x, w, pdt, mean, \
+                                                                       rstd, (TO*)dx, part, rows, dim);         \
+        break;
+        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+#undef CASE
+        default: return fail(P3D_EUNSUPPORTED, "dim too large for the LayerNorm backward");
+    }
+    return check_launch("p3d_layer_norm_bwd");
+}
+
+// Type dispatch of the backward: dy and dx in {the 16-bit type of the
+// forward output, fp32}, x in {fp32, fp16, bf16}.
+template <typename TD, typename TI>
+int dispatch_ln_bwd_out(const void* dy, const void* x, const void* w, int pdt, const float* mean, const float* rstd,
+                        void* dx, float* part, int64_t rows, int dim, int parts, int dx_dtype, hipStream_t s) {
+    switch (dx_dtype) {
+        case P3D_F32: return launch_ln_bwd<TD, TI, float>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
+        case P3D_F16: return launch_ln_bwd<TD, TI, _Float16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
+        default: return launch_ln_bwd<TD, TI, __bf16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
+    }
+}
+
+template <typename TD>
+int dispatch_ln_bwd_x(const void* dy, const void* x, const void* w, int pdt, const float* mean, const float* rstd,
+                      void* dx, float* part, int64_t rows, int dim, int parts, int x_dtype, int dx_dtype,
+                      hipStream_t s) {
+    switch (x_dtype) {
+        case P3D_F32:
+            return dispatch_ln_bwd_out<TD, float>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, dx_dtype, s);
+        case P3D_F16:
+            return dispatch_ln_bwd_out<TD, _Float16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, dx_dtype,
+                                                     s);
+        default:
+            return dispatch_ln_bwd_out<TD, __bf16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, dx_dtype, s);
+    }
+}
+
 }  // namespace
 }  // namespace p3d
 
@@ -115,4 +345,51 @@ extern "C" int p3d_layer_norm(const void* x, const void* weight, const void* bia
             break;
     }
     return check_launch("p3d_layer_norm");
+}
+
+extern "C" int p3d_layer_norm_train(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
+                                    float* mean, float* rstd, int64_t rows, int32_t dim, int32_t x_dtype,
+                                    int32_t y_dtype, float eps, void* stream) {
+    P3D_REQUIRE(x && weight && bias && y && mean && rstd, "null pointer argument");
+    P3D_REQUIRE(x_dtype >= P3D_F32 && x_dtype <= P3D_BF16 && y_dtype >= P3D_F32 && y_dtype <= P3D_BF16 &&
+                    param_dtype >= P3D_F32 && param_dtype <= P3D_BF16,
+                "unknown dtype");
+    const int ep = 16 / dtype_size(x_dtype);
+    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kLanesPerRow * kMaxPiecesPerLane && dim <= kMaxDim,
+                "dim must be a multiple of the 16-byte piece of x, at most 64 pieces and 512 channels");
+    P3D_REQUIRE(rows >= 1, "need at least one row");
+    P3D_REQUIRE(aligned16(x) && aligned16(y), "x and y must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    switch (x_dtype) {
+        case P3D_F32: return dispatch_ln_train<float>(x, weight, bias, param_dtype, y, mean, rstd, rows, dim, y_dtype,
+                                                      eps, s);
+        case P3D_F16: return dispatch_ln_train<_Float16>(x, weight, bias, param_dtype, y, mean, rstd, rows, dim,
+                                                         y_dtype, eps, s);
+        default: return dispatch_ln_train<__bf16>(x, weight, bias, param_dtype, y, mean, rstd, rows, dim, y_dtype,
+                                                  eps, s);
+    }
+}
+
+extern "C" int p3d_layer_norm_bwd(const void* dy, const void* x, const void* weight, int32_t param_dtype,
+                                  const float* mean, const float* rstd, void* dx, float* partial, int64_t rows,
+                                  int32_t dim, int32_t dy_dtype, int32_t x_dtype, int32_t dx_dtype, int32_t parts,
+                                  void* stream) {
+    P3D_REQUIRE(dy && x && weight && mean && rstd && dx && partial, "null pointer argument");
+    P3D_REQUIRE(dy_dtype >= P3D_F32 && dy_dtype <= P3D_BF16 && x_dtype >= P3D_F32 && x_dtype <= P3D_BF16 &&
+                    dx_dtype >= P3D_F32 && dx_dtype <= P3D_BF16 && param_dtype >= P3D_F32 && param_dtype <= P3D_BF16,
+                "unknown dtype");
+    const int ep = 16 / dtype_size(x_dtype);
+    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kLanesPerRow * kMaxPiecesPerLane && dim <= kMaxDim,
+                "dim must be a multiple of the 16-byte piece of x, at most 64 pieces and 512 channels");
+    P3D_REQUIRE(rows >= 1 && parts >= 1 && parts < 65536, "need at least one row and one part");
+    P3D_REQUIRE(aligned16(dy) && aligned16(x) && aligned16(dx), "dy, x and dx must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    switch (dy_dtype) {
+        case P3D_F32: return dispatch_ln_bwd_x<float>(dy, x, weight, param_dtype, mean, rstd, dx, partial, rows, dim,
+                                                      parts, x_dtype, dx_dtype, s);
+        case P3D_F16: return dispatch_ln_bwd_x<_Float16>(dy, x, weight, param_dtype, mean, rstd, dx, partial, rows,
+                                                         dim, parts, x_dtype, dx_dtype, s);
+        default: return dispatch_ln_bwd_x<__bf16>(dy, x, weight, param_dtype, mean, rstd, dx, partial, rows, dim,
+                                                  parts, x_dtype, dx_dtype, s);
+    }
 }

@@ -71,6 +71,57 @@ def _rows(t):
     return t.reshape(-1, t.shape[-1])
 
 
+def layer_norm_train_supported(norm, x):
+    """Whether LayerNormTrain takes this nn.LayerNorm and input."""
+    dim = x.shape[-1]
+    ep = 16 // x.element_size()
+    return (x.dtype in _lib.DTYPES and norm.weight is not None and norm.bias is not None
+            and norm.weight.dtype in _lib.DTYPES and norm.bias.dtype in _lib.DTYPES
+            and norm.weight.dtype == norm.bias.dtype and tuple(norm.normalized_shape) == (dim,)
+            and dim % ep == 0 and dim // ep <= 64 and dim <= 512
+            and not norm._forward_hooks and not norm._forward_pre_hooks)
+
+
+class LayerNormTrain(torch.autograd.Function):
+    """nn.LayerNorm of the layer input (attention.py:64) for 16-bit training,
+    on ``p3d_layer_norm_train`` / ``p3d_layer_norm_bwd``: fp32 statistics, the
+    output rounded straight to the compute type dt (the value the next
+    linear maps would cast it to), and a backward that returns dx in x's
+    dtype and the affine gradients summed in fp32."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, eps, dt):
+        x2 = _rows(x).contiguous()
+        rows, dim = x2.shape
+        dev = x.device
+        y = torch.empty(rows, dim, dtype=dt, device=dev)
+        mean = torch.empty(rows, dtype=torch.float32, device=dev)
+        rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+        _lib.call("p3d_layer_norm_train", x2.data_ptr(), weight.data_ptr(), bias.data_ptr(), _lib.DTYPES[weight.dtype],
+                  y.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, dim, _lib.DTYPES[x2.dtype], _lib.DTYPES[dt],
+                  float(eps), _lib.stream_of(dev))
+        ctx.save_for_backward(x2, weight, mean, rstd)
+        ctx.meta = (x.shape, bias.dtype)
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, weight, mean, rstd = ctx.saved_tensors
+        shape, b_dt = ctx.meta
+        rows, dim = x2.shape
+        dy2 = _rows(dy).contiguous()
+        if dy2.dtype not in _lib.DTYPES:
+            dy2 = dy2.float()
+        dx = torch.empty_like(x2)
+        parts = max(1, min(1024, rows // 256))
+        part = torch.empty(parts, 2, dim, dtype=torch.float32, device=x2.device)
+        _lib.call("p3d_layer_norm_bwd", dy2.data_ptr(), x2.data_ptr(), weight.data_ptr(), _lib.DTYPES[weight.dtype],
+                  mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(), part.data_ptr(), rows, dim, _lib.DTYPES[dy2.dtype],
+                  _lib.DTYPES[x2.dtype], _lib.DTYPES[dx.dtype], parts, _lib.stream_of(x2.device))
+        sums = part.sum(0)
+        return dx.view(shape), sums[0].to(weight.dtype), sums[1].to(b_dt), None, None
+
+
 class InputProjections(torch.autograd.Function):
     """(x Wq^T, x Wkv^T, x Wg^T + bg) of the normalised tokens x in the 16-bit
     type dt (attention.py:64-67,85): x is rounded to dt once and shared by
@@ -94,15 +145,24 @@ class InputProjections(torch.autograd.Function):
     def backward(ctx, dq, dkv, dgl):
         x16, wq, wkv, wg = ctx.saved_tensors
         shape, x_dt, wq_dt, wkv_dt, wg_dt, bg_dt = ctx.meta
-        dx = torch.zeros(x16.shape, dtype=torch.float32, device=x16.device)
+        # dx = dq Wq + dkv Wkv + dgl Wg: for an fp32 x (autocast) the three
+        # products are summed in fp32 as autograd would; for a 16-bit x the
+        # GEMMs accumulate into one buffer of that type.
+        wide = x_dt == torch.float32
+        dx = torch.zeros(x16.shape, dtype=torch.float32, device=x16.device) if wide else None
         grads = []
         for dy, w, w_dt in ((dq, wq, wq_dt), (dkv, wkv, wkv_dt), (dgl, wg, wg_dt)):
             if dy is None:
                 grads.append(None)
                 continue
             dy = _rows(dy).to(x16.dtype)
-            dx.add_(torch.mm(dy, w))
+            if wide:
+                dx.add_(torch.mm(dy, w))
+            else:
+                dx = torch.mm(dy, w) if dx is None else torch.addmm(dx, dy, w)
             grads.append(weight_grad(dy, x16).to(w_dt))
+        if dx is None:
+            dx = torch.zeros(x16.shape, dtype=x16.dtype, device=x16.device)
         dbg = None if dgl is None else _rows(dgl).float().sum(0).to(bg_dt)
         return dx.view(shape).to(x_dt), grads[0], grads[1], grads[2], dbg, None
 

@@ -250,6 +250,15 @@ int p3d_project(const p3d_project_args* args, void* stream);
 int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int32_t k,
                      int32_t dim, int32_t dtype, void* stream);
 
+/* Copy of a [batch, heads, tokens, head_dim] tensor between two strided
+ * views with contiguous, 16-byte aligned rows: the backward's dense gradients
+ * of q, kl, vl, kg, vg into the token-major layout of the layer's to_q /
+ * to_kv outputs (attention.py:64-67), so that autograd receives the
+ * projections' gradients whole instead of transposing and stacking five
+ * views.  batch < 65536. */
+int p3d_copy_rows(p3d_view src, p3d_view dst, int64_t batch, int32_t heads, int64_t tokens, int32_t head_dim,
+                  int32_t dtype, void* stream);
+
 /* Weight gradient of a linear map y = x W^T (the W part of the backward of
  * the layer's to_q, to_kv, gate and to_out nn.Linear maps, attention.py:64-67,
  * 85,89; torch computes it as dy^T x): dw[o][i] = sum over rows n of

@@ -100,6 +100,7 @@ SIGNATURES = {
                              c_int32),
     "p3d_layer_norm_bwd": ([_P, _P, _P, c_int32, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32,
                             c_int32, _P], c_int32),
+    "p3d_copy_rows": ([View, View, c_int64, c_int32, c_int64, c_int32, c_int32, _P], c_int32),
     "p3d_weight_grad": ([_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_mix_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),

@@ -22,7 +22,7 @@ import torch
 from torch import nn
 
 from . import _lib
-from .core import SUPPORTED_HEAD_DIMS, pack3d_hip_rope
+from .core import SUPPORTED_HEAD_DIMS, pack3d_hip_projections
 from .linear import InputProjections, LayerNormTrain, OutputResidual, compute_dtype, layer_norm_train_supported
 from .geometry import TokenLayout
 from .rope import axial_rope, balanced_pairs, packed_rope
@@ -144,6 +144,21 @@ class PACK3DAttention(nn.Module):
     def core_inputs(self, x, layout: TokenLayout):
         """Unrotated q, kl, vl, kg, vg (views of the projections), gate, and the rotation."""
         b, n = x.shape[0], x.shape[1]
+        qp, kvp, gate = self._projections(x)
+        q = qp.view(b, n, self.heads, self.head_dim).transpose(1, 2)
+        kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
+                          for t in kvp.view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
+        return q, kl, vl, kg, vg, gate, self._rope(x, layout)
+
+    def _rope(self, x, layout):
+        n = x.shape[1]
+        if self.position_encoding == "packed":
+            return packed_rope(self.head_dim, n, x.device)
+        return axial_rope(self.head_dim, layout.grid_shape, layout.coords, balanced_pairs(self.head_dim))
+
+    def _projections(self, x):
+        """qp [B, N, H*d], kvp [B, N, 4*G*d] (kl | vl | kg | vg) and the gate [B, H, N]."""
+        b, n = x.shape[0], x.shape[1]
         fused = fused_projections(self, x)
         if fused is not None:
             qp, kvp, gp = fused
@@ -161,14 +176,7 @@ class PACK3DAttention(nn.Module):
             xn = layer_norm(self.norm, x)
             qp, kvp, gl = self.to_q(xn), self.to_kv(xn), self.gate(xn)
             gate = gl.view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
-        q = qp.view(b, n, self.heads, self.head_dim).transpose(1, 2)
-        kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
-                          for t in kvp.view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
-        if self.position_encoding == "packed":
-            rope = packed_rope(self.head_dim, n, x.device)
-        else:
-            rope = axial_rope(self.head_dim, layout.grid_shape, layout.coords, balanced_pairs(self.head_dim))
-        return q, kl, vl, kg, vg, gate, rope
+        return qp, kvp, gate
 
     def forward(self, x, layout: TokenLayout):
         layout.check_unmodified()
@@ -181,9 +189,10 @@ class PACK3DAttention(nn.Module):
         if self.backend != "hip":
             raise ValueError("unknown backend; implicit fallback is disabled")
         b, n = x.shape[0], x.shape[1]
-        q, kl, vl, kg, vg, gate, rope = self.core_inputs(x, layout)
-        out = pack3d_hip_rope(q, kl, vl, kg, vg, self.pool_weight, self.slot_bias, gate, self.local_scale,
-                              self.global_scale, layout.geometry, rope, temperature=self.temperature)
+        qp, kvp, gate = self._projections(x)
+        out = pack3d_hip_projections(qp, kvp, self.heads, self.kv_heads, self.pool_weight, self.slot_bias, gate,
+                                     self.local_scale, self.global_scale, layout.geometry, self._rope(x, layout),
+                                     temperature=self.temperature)
         # x + to_out(out): one kernel in the no-grad forward, else one GEMM with the
         # residual as its C operand (to_out has no bias), with a HIP weight gradient
         # in 16-bit training.

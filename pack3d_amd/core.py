@@ -359,6 +359,68 @@ def _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, r
     return y
 
 
+class _Pack3DProjections(torch.autograd.Function):
+    """The core on views of the layer's projections, qp [B, N, H*d] and kvp
+    [B, N, 4*G*d] chunked kl | vl | kg | vg (attention.py:64-67), with
+    gradients returned for qp and kvp directly: the backward's dense
+    gradients are copied into the projections' layout by p3d_copy_rows, so
+    autograd does not transpose and stack the five views."""
+
+    @staticmethod
+    def forward(ctx, qp, kvp, weight, bias, gate, sl, sg, heads, kv_heads, geometry, temperature, rope):
+        q, kl, vl, kg, vg = _projection_views(qp, kvp, heads, kv_heads)
+        plan = ForwardPlan(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, rope,
+                           save_state=True)
+        y, saved = plan.run()
+        ctx.save_for_backward(qp, kvp, weight, bias, gate, sl, sg, saved["sk"], saved["svt"], plan.sk_norm_max,
+                              saved["o_local"], saved["o_global"], saved["lse_local"], saved["lse_global"])
+        ctx.geometry, ctx.temperature, ctx.rope, ctx.key_scale = geometry, temperature, rope, plan.key_scale
+        ctx.heads, ctx.kv_heads = heads, kv_heads
+        return y
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy):
+        ctx.geometry.check_unmodified()
+        qp, kvp, weight, bias, gate, sl, sg, *state = ctx.saved_tensors
+        views = _projection_views(qp, kvp, ctx.heads, ctx.kv_heads)
+        grads = backward(dy, *views, weight, bias, gate, sl, sg, *state, ctx.geometry, ctx.temperature, ctx.rope,
+                         ctx.rope, ctx.key_scale)
+        dqp, dkvp = torch.empty_like(qp), torch.empty_like(kvp)
+        stream = _lib.stream_of(qp.device)
+        for src, dst in zip(grads[:5], _projection_views(dqp, dkvp, ctx.heads, ctx.kv_heads)):
+            b, h, n, d = src.shape
+            _lib.call("p3d_copy_rows", _lib.view(src), _lib.view(dst), b, h, n, d, _lib.DTYPES[src.dtype], stream)
+        return (dqp, dkvp, *grads[5:], None, None, None, None, None)
+
+
+def _projection_views(qp, kvp, heads, kv_heads):
+    """q [B, H, N, d] and kl, vl, kg, vg [B, G, N, d] as views of qp and kvp."""
+    b, n = qp.shape[0], qp.shape[1]
+    d = qp.shape[2] // heads
+    q = qp.view(b, n, heads, d).transpose(1, 2)
+    kv = kvp.view(b, n, 4, kv_heads, d)
+    return (q, *(kv[:, :, i].transpose(1, 2) for i in range(4)))
+
+
+def pack3d_hip_projections(qp, kvp, heads, kv_heads, weight, bias, gate, sl, sg, geometry, rope: RopeSpec, *,
+                           temperature=1.0):
+    """The core of the layer on its projections qp [B, N, H*d] and kvp
+    [B, N, 4*G*d] (kl | vl | kg | vg) with the rotation ``rope``; the same
+    values as pack3d_hip_rope on their views.  With autograd active the
+    gradients of qp and kvp come back whole (_Pack3DProjections)."""
+    views = _projection_views(qp, kvp, heads, kv_heads)
+    inputs = (*views, weight, bias, gate, sl, sg)
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in (qp, kvp, weight, bias, gate, sl, sg))):
+        return _run(*inputs, geometry, temperature, rope, rope)
+    _validate_inputs(*inputs, geometry, temperature)
+    _check_hip(qp)
+    if any(not (t.stride(-1) == 1 and t.is_contiguous()) for t in (qp, kvp)):
+        return _run(*inputs, geometry, temperature, rope, rope)
+    return _Pack3DProjections.apply(qp, kvp, weight, bias, gate, sl, sg, heads, kv_heads, geometry,
+                                    float(temperature), rope)
+
+
 def pack3d_hip(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, *, temperature=1.0):
     """PACK3D core on the GPU with rotated q, kl, kg (the contract of reference.py:8-9).
 

@@ -139,3 +139,18 @@ def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, ro
     tol = 1e-5 if x_dtype == torch.float32 else 1e-2
     assert rel_l2(xg.grad, xd.grad) < tol, rel_l2(xg.grad, xd.grad)
     assert rel_l2(wg.grad, wd.grad) < 1e-5 and rel_l2(bg.grad, bd.grad) < 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_copy_rows_into_projection_layout(gpu, dtype):
+    """p3d_copy_rows: dense [B, G, N, d] into the strided kv-chunk views of a
+    [B, N, 4, G, d] buffer, bit-exact, other chunks untouched."""
+    print(f"copy rows {dtype}", flush=True)
+    b, g, n, d = 2, 3, 1001, 48
+    src = torch.randn(b, g, n, d, device=gpu).to(dtype)
+    dst = torch.full((b, n, 4, g, d), 7.0, device=gpu, dtype=dtype)
+    view = dst[:, :, 2].transpose(1, 2)
+    _lib.call("p3d_copy_rows", _lib.view(src), _lib.view(view), b, g, n, d, _lib.DTYPES[dtype], _lib.stream_of(gpu))
+    assert torch.equal(view, src)
+    others = dst[:, :, [0, 1, 3]]
+    assert torch.equal(others, torch.full_like(others, 7.0))

@@ -197,13 +197,15 @@ __device__ __forceinline__ uint4 round_piece<_Float16, 8>(float (&x)[8]) {
 // slot logit, and take the slot softmax as a wave reduction.
 //
 // The weighted sums over the 64 slots, sum_s a_s k_s and sum_s a_s v_s, are
-// a matrix-vector product.  For 2-byte types the lanes write their rounded
-// K row and their V row as columns of an LDS matrix X^T [2D channels][64
-// slots], and the MFMA computes W X with W = [hi(a); lo(a)], the weights
-// split into two storage-type parts (hi = round(a), lo = round(a - hi)):
-// each product of two storage-type values is exact in fp32 and the sum
-// carries a with 16 significant bits.  fp32 rows are summed across lanes by
-// a reduce-scatter butterfly instead.
+// a matrix-vector product.  For 2-byte types each lane writes its rotated,
+// rounded K row back over its staged row (the V rows stay as staged), and
+// the MFMA computes W X with W = [hi(a); lo(a)] (the weights split into two
+// storage-type parts, hi = round(a), lo = round(a - hi)) and X the staged
+// [64 slots x (K | V)] rows.  Its B operand needs 8 consecutive slots of one
+// channel per lane, read straight out of the row-major rows with
+// ds_read_b64_tr_b16 (two per fragment).  Each product of two storage-type
+// values is exact in fp32 and the sum carries a with 16 significant bits.
+// fp32 rows are summed across lanes by a reduce-scatter butterfly instead.
 
 template <typename T, int D>
 struct PoolRowCfg {
@@ -212,14 +214,11 @@ struct PoolRowCfg {
     static constexpr int PPR = D / EP;               // pieces per row
     static constexpr int PFN = (PPR + 3) & ~3;       // run flags, padded to 16 bytes
     static constexpr int RB = D * (int)sizeof(T);    // row bytes
-    // X^T row stride: 64 slots plus 16 bytes, so the 16-byte operand reads
-    // of 16 consecutive channel rows start in distinct bank groups.
-    static constexpr int XS = 64 * (int)sizeof(T) + 16;
-    static constexpr int XT_BYTES = 2 * D * XS;      // the K rows / V rows are staged inside it
-    // MFMA path: X^T, then the weight rows hi, lo and a zero row (64 slots each).
-    static constexpr int WAVE_BYTES = MF ? XT_BYTES + 3 * 64 * 2 : 2 * 64 * RB;
+    static constexpr int ROWS_BYTES = 2 * 64 * RB;   // K rows, then V rows
+    // MFMA path: the rows, then the weight rows hi, lo and a zero row (64 slots each).
+    static constexpr int WAVE_BYTES = MF ? ROWS_BYTES + 3 * 64 * 2 : ROWS_BYTES;
     static constexpr int MAX_WAVES = (159 * 1024) / WAVE_BYTES < 8 ? (159 * 1024) / WAVE_BYTES : 8;
-    static constexpr int VOFF = MF ? D * XS : 64 * RB;  // where the V rows are staged
+    static constexpr int VOFF = 64 * RB;             // where the V rows are staged
     static constexpr int NT = 2 * D / 32;            // 32-channel MFMA tiles of [k; v]
     static constexpr int NCH = D / 16;               // 16-channel chunks of the butterfly
     static constexpr int PPC = 16 / EP;              // pieces per chunk
@@ -344,19 +343,27 @@ __device__ __forceinline__ void pool_fetch(const PoolDev& a, unsigned i, int idx
     }
 }
 
-// Write the 16-bit halves of the packed row `row` (channels 2j, 2j + 1 in
-// word j) as column `lane` of rows c0, c0 + 1, ... of X^T.
-template <int PPR, int XS>
-__device__ __forceinline__ void write_column(unsigned char* xt, int c0, int lane, const u32x4 (&row)[PPR]) {
-#pragma unroll
-    for (int p = 0; p < PPR; ++p)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const unsigned word = row[p][w];
-            unsigned char* col = xt + (c0 + 8 * p + 2 * w) * XS + lane * 2;
-            *reinterpret_cast<unsigned short*>(col) = (unsigned short)word;
-            *reinterpret_cast<unsigned short*>(col + XS) = (unsigned short)(word >> 16);
-        }
+// MFMA B operand for k-step ks and 32-channel tile t of [K | V] (2-byte
+// types): lane L holds channel 32 t + L % 32 for slots 16 ks + 8 (L / 32) ..
+// + 8, read from the row-major staged rows by two ds_read_b64_tr_b16.  Within
+// a 16-lane block, lane B + 4a + e receives element e of the 8-byte windows
+// addressed by lanes B + a + 4j (j = 0..3), so lane L addresses slot
+// 16 ks + 8 (L / 32) + (L % 16) / 4 (four slots further for the second read)
+// at channel 32 t + 16 ((L / 16) % 2) + 4 (L % 4) of K or, past D, of V.
+// D is a multiple of 16, so no 4-channel window straddles K and V.
+template <typename T, int D>
+__device__ __forceinline__ typename Mma<T>::Frag pool_frag_tr(const unsigned char* rows, int ks, int t, int lane) {
+    typedef PoolRowCfg<T, D> C;
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) v4s* lds_v4s;
+    const int slot = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int ch = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const unsigned char* base = ch < D ? rows + ch * 2 : rows + C::VOFF + (ch - D) * 2;
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + slot * C::RB));
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + (slot + 4) * C::RB));
+    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(typename Mma<T>::Frag, v);
 }
 
 
@@ -370,7 +377,7 @@ __device__ __forceinline__ void write_column(unsigned char* xt, int c0, int lane
 template <typename T, int D, bool TAB_LDS>
 __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd(PoolDev a) {
     typedef PoolRowCfg<T, D> C;
-    constexpr int EP = C::EP, PPR = C::PPR, RB = C::RB, NCH = C::NCH, PPC = C::PPC, XS = C::XS;
+    constexpr int EP = C::EP, PPR = C::PPR, RB = C::RB, NCH = C::NCH, PPC = C::PPC;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int waves = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -382,7 +389,7 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
     const int tab_dw = TAB_LDS ? ((a.table_entries * 2 + 3) & ~3) : 0;
     unsigned char* rows = reinterpret_cast<unsigned char*>(reinterpret_cast<uint32_t*>(ltab) + tab_dw) +
                           (size_t)wave * C::WAVE_BYTES;
-    T* wrows = reinterpret_cast<T*>(rows + C::XT_BYTES);  // MFMA path: weight rows hi, lo, 0
+    T* wrows = reinterpret_cast<T*>(rows + C::ROWS_BYTES);  // MFMA path: weight rows hi, lo, 0
     for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(a.rope.pairs, j);
     // Piece p is a table run when its pairs read consecutive entries with one
     // stride vector: entry(j0 + t) = entry(j0) + t for every position.
@@ -468,14 +475,13 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
             store_summary<T, D>(a, pend_bg, pend_m, lane, pend_count, pend);
             pending = false;
         }
-        // The lane's own K and V rows.
+        // The lane's own K row (and V row for the fp32 butterfly).
         u32x4 kr[PPR], vr[PPR];
 #pragma unroll
         for (int p = 0; p < PPR; ++p) {
             kr[p] = *reinterpret_cast<const u32x4*>(rows + lane * RB + p * 16);
-            vr[p] = *reinterpret_cast<const u32x4*>(rows + C::VOFF + lane * RB + p * 16);
+            if constexpr (!C::MF) vr[p] = *reinterpret_cast<const u32x4*>(rows + C::VOFF + lane * RB + p * 16);
         }
-        wave_lds_sync();  // every row is read before X^T overwrites the rows
         // Next step's rows and coordinates, and the block-table row after it.
         const bool more = it1 < total;
         int ns1 = 1, pos1[3] = {0, 0, 0}, idx2 = -1;
@@ -492,7 +498,6 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
 
         if (__ballot(idx >= 0) != 0) {  // empty fine block: no mass, no count
             ++count;
-            if constexpr (C::MF) write_column<PPR, XS>(rows, D, lane, vr);
             // Rotate the slot's key, round it to the storage type, and form its
             // logit (compression.py:31-35): (k . w) / tau + bias_s.
             float dot = 0.f;
@@ -522,17 +527,20 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
             const float wgt = ex / wave_sum(ex);
             if constexpr (C::MF) {
                 typedef typename Mma<T>::Frag Frag;
-                write_column<PPR, XS>(rows, 0, lane, kr);
+                // The rotated, rounded key over the lane's own staged row (only
+                // this lane has read it).
+#pragma unroll
+                for (int p = 0; p < PPR; ++p) *reinterpret_cast<u32x4*>(rows + lane * RB + p * 16) = kr[p];
                 const T hi = from_f32<T>(wgt);
                 wrows[lane] = hi;
                 wrows[64 + lane] = from_f32<T>(wgt - to_f32(hi));
                 wave_lds_sync();
-                // D[w][c] = sum_s W[w][s] X^T[c][s] for the weight rows w = 0
+                // D[w][c] = sum_s W[w][s] X[s][c] for the weight rows w = 0
                 // (hi), 1 (lo), over 16 slots per instruction: lane l holds
                 // slots 8 (l / 32) + j of channel l % 32 (B) and, for l % 32 <
                 // 2, of weight row l % 32 (A); rows 0 and 1 of D are
                 // registers 0 and 1 of lanes 0..31.
-                const int g = lane >> 5, n = lane & 31;
+                const int g = lane >> 5;
                 f32x16 d[C::NT];
 #pragma unroll
                 for (int t = 0; t < C::NT; ++t)
@@ -542,11 +550,7 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
                 for (int ks = 0; ks < 4; ++ks) {
                     const Frag wa = __builtin_bit_cast(Frag, *reinterpret_cast<const u32x4*>(wsrc + 16 * ks + 8 * g));
 #pragma unroll
-                    for (int t = 0; t < C::NT; ++t) {
-                        const Frag xb = __builtin_bit_cast(
-                            Frag, *reinterpret_cast<const u32x4*>(rows + (32 * t + n) * XS + (16 * ks + 8 * g) * 2));
-                        d[t] = Mma<T>::mfma(wa, xb, d[t]);
-                    }
+                    for (int t = 0; t < C::NT; ++t) d[t] = Mma<T>::mfma(wa, pool_frag_tr<T, D>(rows, ks, t, lane), d[t]);
                 }
 #pragma unroll
                 for (int t = 0; t < C::NT; ++t) acc[t] += d[t][0] + d[t][1];

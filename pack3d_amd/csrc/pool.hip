@@ -419,13 +419,18 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
     unsigned it = blockIdx.x * waves + wave;
     if (it >= total) return;
 
+    // Waves walk the items from the last one down (item = total - 1 - i for
+    // the i-th of the walk): the projections that write kg / vg just before
+    // this kernel finish with the last tokens, and those rows are the likeliest
+    // to still be in the last-level cache.
+    auto item_of = [&](unsigned i) __attribute__((always_inline)) -> unsigned { return total - 1u - i; };
     auto steps_of = [&](unsigned i) __attribute__((always_inline)) -> int {
-        const int m = (int)((i / a.G) % a.Mp);
+        const int m = (int)((item_of(i) / a.G) % a.Mp);
         return m < a.M ? min(a.F, (m + 1) * a.P) - m * a.P : 1;
     };
     // The lane's slot token of step (i, fl), or -1 (empty slot, padding summary).
     auto row_of = [&](unsigned i, int fl) __attribute__((always_inline)) -> int {
-        const int m = (int)((i / a.G) % a.Mp);
+        const int m = (int)((item_of(i) / a.G) % a.Mp);
         return (m < a.M && lane < a.V) ? a.blocks[(int64_t)(m * a.P + fl) * a.V + lane] : -1;
     };
     // Pair metadata of each piece's first pair and the table-run flags, as
@@ -448,7 +453,7 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
     int idx = row_of(it, 0);
     int pos[3];
     rope_position32(a.rope, max(idx, 0), pos);
-    pool_fetch<T, D>(a, it, idx, lane, pk, pv);
+    pool_fetch<T, D>(a, item_of(it), idx, lane, pk, pv);
     unsigned it1 = ns > 1 ? it : it + stride;
     int fl1 = ns > 1 ? 1 : 0;
     int idx1 = it1 < total ? row_of(it1, fl1) : -1;
@@ -489,7 +494,7 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
         int fl2 = 0;
         if (more) {
             ns1 = steps_of(it1);
-            pool_fetch<T, D>(a, it1, idx1, lane, pk, pv);
+            pool_fetch<T, D>(a, item_of(it1), idx1, lane, pk, pv);
             rope_position32(a.rope, max(idx1, 0), pos1);
             it2 = fl1 + 1 < ns1 ? it1 : it1 + stride;
             fl2 = fl1 + 1 < ns1 ? fl1 + 1 : 0;
@@ -574,9 +579,9 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
             }
         }
         if (fl + 1 == ns) {
-            const unsigned bm = it / a.G;
+            const unsigned bm = item_of(it) / a.G;
             pending = true;
-            pend_bg = (int)(bm / a.Mp) * a.G + (int)(it % a.G);
+            pend_bg = (int)(bm / a.Mp) * a.G + (int)(item_of(it) % a.G);
             pend_m = (int)(bm % a.Mp);
             pend_count = count;
 #pragma unroll

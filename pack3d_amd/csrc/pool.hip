@@ -487,18 +487,23 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
             kr[p] = *reinterpret_cast<const u32x4*>(rows + lane * RB + p * 16);
             if constexpr (!C::MF) vr[p] = *reinterpret_cast<const u32x4*>(rows + C::VOFF + lane * RB + p * 16);
         }
-        // Next step's rows and coordinates, and the block-table row after it.
+        // Next step's coordinates, the block-table row after it, then the next
+        // step's rows.  The load counter completes in issue order, and the
+        // coordinates and table row are carried into the next iteration (a
+        // register copy that must wait for them): issued before the rows,
+        // that wait leaves the row loads in flight under this step's
+        // arithmetic instead of draining them at the end of the step.
         const bool more = it1 < total;
         int ns1 = 1, pos1[3] = {0, 0, 0}, idx2 = -1;
         unsigned it2 = total;
         int fl2 = 0;
         if (more) {
             ns1 = steps_of(it1);
-            pool_fetch<T, D>(a, item_of(it1), idx1, lane, pk, pv);
             rope_position32(a.rope, max(idx1, 0), pos1);
             it2 = fl1 + 1 < ns1 ? it1 : it1 + stride;
             fl2 = fl1 + 1 < ns1 ? fl1 + 1 : 0;
             if (it2 < total) idx2 = row_of(it2, fl2);
+            pool_fetch<T, D>(a, item_of(it1), idx1, lane, pk, pv);
         }
 
         if (__ballot(idx >= 0) != 0) {  // empty fine block: no mass, no count

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 5
+#define P3D_ABI_VERSION 6
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -193,20 +193,24 @@ int p3d_layer_norm(const void* x, const void* weight, const void* bias, int32_t 
  * autocast, with its output rounded to the compute type that the next
  * linear maps cast it to): x [rows, dim] of x_dtype, y [rows, dim] of
  * y_dtype, and each row's mean and 1/sqrt(var + eps) as fp32 [rows] for the
- * backward.  dim a multiple of x's 16-byte piece, at most 64 pieces. */
+ * backward.  x_copy (may be NULL): x rounded to y_dtype [rows, dim], the
+ * residual operand of the layer's output product under autocast
+ * (attention.py:89), written from the same read of x.  dim a multiple of
+ * x's 16-byte piece, at most 64 pieces. */
 int p3d_layer_norm_train(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
-                         float* mean, float* rstd, int64_t rows, int32_t dim, int32_t x_dtype, int32_t y_dtype,
-                         float eps, void* stream);
+                         void* x_copy, float* mean, float* rstd, int64_t rows, int32_t dim, int32_t x_dtype,
+                         int32_t y_dtype, float eps, void* stream);
 
 /* LayerNorm backward (torch's layer_norm backward): with xhat = (x - mean)
  * rstd and g = dy * weight, dx = rstd (g - mean(g) - xhat mean(g xhat)) per
- * row, written as dx_dtype; the affine gradients as fp32 partial sums over
- * `parts` row ranges, partial[part][0][dim] = sum dy xhat and
- * partial[part][1][dim] = sum dy (the caller sums the parts).  mean / rstd
- * from p3d_layer_norm_train. */
-int p3d_layer_norm_bwd(const void* dy, const void* x, const void* weight, int32_t param_dtype, const float* mean,
-                       const float* rstd, void* dx, float* partial, int64_t rows, int32_t dim, int32_t dy_dtype,
-                       int32_t x_dtype, int32_t dx_dtype, int32_t parts, void* stream);
+ * row, plus dres (may be NULL; [rows, dim] of dy_dtype: the gradient that
+ * reaches x through the residual branch) added in fp32, written as dx_dtype;
+ * the affine gradients as fp32 partial sums over `parts` row ranges,
+ * partial[part][0][dim] = sum dy xhat and partial[part][1][dim] = sum dy (the
+ * caller sums the parts).  mean / rstd from p3d_layer_norm_train. */
+int p3d_layer_norm_bwd(const void* dy, const void* dres, const void* x, const void* weight, int32_t param_dtype,
+                       const float* mean, const float* rstd, void* dx, float* partial, int64_t rows, int32_t dim,
+                       int32_t dy_dtype, int32_t x_dtype, int32_t dx_dtype, int32_t parts, void* stream);
 
 /* Fused input projections of the layer (attention.py:64-67,85): LayerNorm
  * of x [rows, dim], then q = xn Wq^T [rows, q_out], kv = xn Wkv^T

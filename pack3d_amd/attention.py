@@ -144,7 +144,7 @@ class PACK3DAttention(nn.Module):
     def core_inputs(self, x, layout: TokenLayout):
         """Unrotated q, kl, vl, kg, vg (views of the projections), gate, and the rotation."""
         b, n = x.shape[0], x.shape[1]
-        qp, kvp, gate = self._projections(x)
+        qp, kvp, gate, _ = self._projections(x)
         q = qp.view(b, n, self.heads, self.head_dim).transpose(1, 2)
         kl, vl, kg, vg = (t.view(b, n, self.kv_heads, self.head_dim).transpose(1, 2)
                           for t in kvp.view(b, n, 4, self.kv_heads * self.head_dim).unbind(2))
@@ -157,8 +157,12 @@ class PACK3DAttention(nn.Module):
         return axial_rope(self.head_dim, layout.grid_shape, layout.coords, balanced_pairs(self.head_dim))
 
     def _projections(self, x):
-        """qp [B, N, H*d], kvp [B, N, 4*G*d] (kl | vl | kg | vg) and the gate [B, H, N]."""
+        """qp [B, N, H*d], kvp [B, N, 4*G*d] (kl | vl | kg | vg), the gate
+        [B, H, N], and the residual operand of the output product when
+        LayerNormTrain wrote it (x rounded to the compute type, [B*N, dim];
+        else None)."""
         b, n = x.shape[0], x.shape[1]
+        res = None
         fused = fused_projections(self, x)
         if fused is not None:
             qp, kvp, gp = fused
@@ -166,7 +170,7 @@ class PACK3DAttention(nn.Module):
         elif self._hip_linear(x):
             dt = compute_dtype(x)
             if layer_norm_train_supported(self.norm, x):
-                xn = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt)
+                xn, res = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt, True)
             else:
                 xn = layer_norm(self.norm, x)
             qp, kvp, gl = InputProjections.apply(xn, self.to_q.weight, self.to_kv.weight, self.gate.weight,
@@ -176,7 +180,7 @@ class PACK3DAttention(nn.Module):
             xn = layer_norm(self.norm, x)
             qp, kvp, gl = self.to_q(xn), self.to_kv(xn), self.gate(xn)
             gate = gl.view(b, n, self.heads, 2).softmax(-1)[..., 1].transpose(1, 2)
-        return qp, kvp, gate
+        return qp, kvp, gate, res
 
     def forward(self, x, layout: TokenLayout):
         layout.check_unmodified()
@@ -189,7 +193,7 @@ class PACK3DAttention(nn.Module):
         if self.backend != "hip":
             raise ValueError("unknown backend; implicit fallback is disabled")
         b, n = x.shape[0], x.shape[1]
-        qp, kvp, gate = self._projections(x)
+        qp, kvp, gate, res = self._projections(x)
         out = pack3d_hip_projections(qp, kvp, self.heads, self.kv_heads, self.pool_weight, self.slot_bias, gate,
                                      self.local_scale, self.global_scale, layout.geometry, self._rope(x, layout),
                                      temperature=self.temperature)
@@ -201,6 +205,8 @@ class PACK3DAttention(nn.Module):
         if fused is not None:
             return fused.view(b, n, self.dim)
         if self._hip_linear(x):
+            if res is not None:  # LayerNormTrain's dt copy of x, owned by this step
+                return OutputResidual.apply(res, o, self.to_out.weight, compute_dtype(x), True).view(b, n, self.dim)
             return OutputResidual.apply(x.reshape(b * n, self.dim), o, self.to_out.weight,
                                         compute_dtype(x)).view(b, n, self.dim)
         return torch.addmm(x.reshape(b * n, self.dim), o, self.to_out.weight.t()).view(b, n, self.dim)

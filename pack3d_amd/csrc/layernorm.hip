@@ -110,8 +110,8 @@ __device__ __forceinline__ void store_n(T* p, const float (&in)[N]) {
 
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const void* w, const void* b, int param_dtype,
-                                                          TO* y, float* mean_out, float* rstd_out, int64_t rows,
-                                                          int dim, float eps) {
+                                                          TO* y, TO* x_copy, float* mean_out, float* rstd_out,
+                                                          int64_t rows, int dim, float eps) {
     constexpr int EP = Piece<TI>::N;
     __shared__ __align__(16) float lw[kMaxDim], lb[kMaxDim];
     for (int c = threadIdx.x; c < dim; c += blockDim.x) {
@@ -164,6 +164,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const voi
                 o[e] = (v[i][e] - mean) * rstd * lw[c] + lb[c];
             }
             store_n<TO, EP>(y + row * dim + p * EP, o);
+            if (x_copy) store_n<TO, EP>(x_copy + row * dim + p * EP, v[i]);
         }
     }
 }
@@ -175,9 +176,9 @@ __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const voi
 // part[block][0 / 1][dim], summed by the caller.  PPL: pieces per lane
 // (ceil(dim / EP / 8)), which sizes the per-lane arrays.
 template <typename TD, typename TI, typename TO, int PPL>
-__global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TI* x, const void* w, int param_dtype,
-                                                        const float* mean_in, const float* rstd_in, TO* dx,
-                                                        float* part, int64_t rows, int dim) {
+__global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TD* dres, const TI* x, const void* w,
+                                                        int param_dtype, const float* mean_in, const float* rstd_in,
+                                                        TO* dx, float* part, int64_t rows, int dim) {
     constexpr int EP = Piece<TI>::N;
     constexpr int GROUPS = 256 / kLanesPerRow;
     __shared__ __align__(16) float lw[kMaxDim];
@@ -225,6 +226,12 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TI* 
                 float o[EP];
 #pragma unroll
                 for (int e = 0; e < EP; ++e) o[e] = rstd * (g[i][e] - mg - xh[i][e] * mgx);
+                if (dres) {
+                    float r[EP];
+                    load_n<TD, EP>(dres + row * dim + p * EP, r);
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) o[e] += r[e];
+                }
                 store_n<TO, EP>(dx + row * dim + p * EP, o);
             }
         }
@@ -251,32 +258,34 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TI* 
 }
 
 template <typename TI, typename TO>
-int launch_ln_train(const void* x, const void* w, const void* b, int pdt, void* y, float* mean, float* rstd,
+int launch_ln_train(const void* x, const void* w, const void* b, int pdt, void* y, void* xc, float* mean, float* rstd,
                     int64_t rows, int dim, float eps, hipStream_t s) {
     const unsigned blocks = (unsigned)cdiv(rows * kLanesPerRow, 256);
-    k_layer_norm_train<TI, TO><<<blocks, 256, 0, s>>>((const TI*)x, w, b, pdt, (TO*)y, mean, rstd, rows, dim, eps);
+    k_layer_norm_train<TI, TO><<<blocks, 256, 0, s>>>((const TI*)x, w, b, pdt, (TO*)y, (TO*)xc, mean, rstd, rows, dim,
+                                                      eps);
     return check_launch("p3d_layer_norm_train");
 }
 
 template <typename TI>
-int dispatch_ln_train(const void* x, const void* w, const void* b, int pdt, void* y, float* mean, float* rstd,
-                      int64_t rows, int dim, int y_dtype, float eps, hipStream_t s) {
+int dispatch_ln_train(const void* x, const void* w, const void* b, int pdt, void* y, void* xc, float* mean,
+                      float* rstd, int64_t rows, int dim, int y_dtype, float eps, hipStream_t s) {
     switch (y_dtype) {
-        case P3D_F32: return launch_ln_train<TI, float>(x, w, b, pdt, y, mean, rstd, rows, dim, eps, s);
-        case P3D_F16: return launch_ln_train<TI, _Float16>(x, w, b, pdt, y, mean, rstd, rows, dim, eps, s);
-        default: return launch_ln_train<TI, __bf16>(x, w, b, pdt, y, mean, rstd, rows, dim, eps, s);
+        case P3D_F32: return launch_ln_train<TI, float>(x, w, b, pdt, y, xc, mean, rstd, rows, dim, eps, s);
+        case P3D_F16: return launch_ln_train<TI, _Float16>(x, w, b, pdt, y, xc, mean, rstd, rows, dim, eps, s);
+        default: return launch_ln_train<TI, __bf16>(x, w, b, pdt, y, xc, mean, rstd, rows, dim, eps, s);
     }
 }
 
 template <typename TD, typename TI, typename TO>
-int launch_ln_bwd(const void* dy, const void* x, const void* w, int pdt, const float* mean, const float* rstd,
-                  void* dx, float* part, int64_t rows, int dim, int parts, hipStream_t s) {
+int launch_ln_bwd(const void* dy, const void* dres, const void* x, const void* w, int pdt, const float* mean,
+                  const float* rstd, void* dx, float* part, int64_t rows, int dim, int parts, hipStream_t s) {
     const int ppl = (int)cdiv(dim / Piece<TI>::N, kLanesPerRow);
     switch (ppl) {
 #define CASE(P)                                                                                                  \
     case P:                                                                                                      \
-        k_layer_norm_bwd<TD, TI, TO, P><<<(unsigned)parts, 256, 0, s>>>((const TD*)dy, (const TI*)x, w, pdt, mean, \
-                                                                       rstd, (TO*)dx, part, rows, dim);         \
+        k_layer_norm_bwd<TD, TI, TO, P><<<(unsigned)parts, 256, 0, s>>>((const TD*)dy, (const TD*)dres,          \
+                                                                       (const TI*)x, w, pdt, mean, rstd, (TO*)dx, \
+                                                                       part, rows, dim);                        \
         break;
         CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
 #undef CASE
@@ -288,27 +297,33 @@ int launch_ln_bwd(const void* dy, const void* x, const void* w, int pdt, const f
 // Type dispatch of the backward: dy and dx in {the 16-bit type of the
 // forward output, fp32}, x in {fp32, fp16, bf16}.
 template <typename TD, typename TI>
-int dispatch_ln_bwd_out(const void* dy, const void* x, const void* w, int pdt, const float* mean, const float* rstd,
-                        void* dx, float* part, int64_t rows, int dim, int parts, int dx_dtype, hipStream_t s) {
+int dispatch_ln_bwd_out(const void* dy, const void* dres, const void* x, const void* w, int pdt, const float* mean,
+                        const float* rstd, void* dx, float* part, int64_t rows, int dim, int parts, int dx_dtype,
+                        hipStream_t s) {
     switch (dx_dtype) {
-        case P3D_F32: return launch_ln_bwd<TD, TI, float>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
-        case P3D_F16: return launch_ln_bwd<TD, TI, _Float16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
-        default: return launch_ln_bwd<TD, TI, __bf16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
+        case P3D_F32:
+            return launch_ln_bwd<TD, TI, float>(dy, dres, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
+        case P3D_F16:
+            return launch_ln_bwd<TD, TI, _Float16>(dy, dres, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
+        default:
+            return launch_ln_bwd<TD, TI, __bf16>(dy, dres, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, s);
     }
 }
 
 template <typename TD>
-int dispatch_ln_bwd_x(const void* dy, const void* x, const void* w, int pdt, const float* mean, const float* rstd,
-                      void* dx, float* part, int64_t rows, int dim, int parts, int x_dtype, int dx_dtype,
-                      hipStream_t s) {
+int dispatch_ln_bwd_x(const void* dy, const void* dres, const void* x, const void* w, int pdt, const float* mean,
+                      const float* rstd, void* dx, float* part, int64_t rows, int dim, int parts, int x_dtype,
+                      int dx_dtype, hipStream_t s) {
     switch (x_dtype) {
         case P3D_F32:
-            return dispatch_ln_bwd_out<TD, float>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, dx_dtype, s);
+            return dispatch_ln_bwd_out<TD, float>(dy, dres, x, w, pdt, mean, rstd, dx, part, rows, dim, parts,
+                                                  dx_dtype, s);
         case P3D_F16:
-            return dispatch_ln_bwd_out<TD, _Float16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, dx_dtype,
-                                                     s);
+            return dispatch_ln_bwd_out<TD, _Float16>(dy, dres, x, w, pdt, mean, rstd, dx, part, rows, dim, parts,
+                                                     dx_dtype, s);
         default:
-            return dispatch_ln_bwd_out<TD, __bf16>(dy, x, w, pdt, mean, rstd, dx, part, rows, dim, parts, dx_dtype, s);
+            return dispatch_ln_bwd_out<TD, __bf16>(dy, dres, x, w, pdt, mean, rstd, dx, part, rows, dim, parts,
+                                                   dx_dtype, s);
     }
 }
 
@@ -348,8 +363,8 @@ extern "C" int p3d_layer_norm(const void* x, const void* weight, const void* bia
 }
 
 extern "C" int p3d_layer_norm_train(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
-                                    float* mean, float* rstd, int64_t rows, int32_t dim, int32_t x_dtype,
-                                    int32_t y_dtype, float eps, void* stream) {
+                                    void* x_copy, float* mean, float* rstd, int64_t rows, int32_t dim,
+                                    int32_t x_dtype, int32_t y_dtype, float eps, void* stream) {
     P3D_REQUIRE(x && weight && bias && y && mean && rstd, "null pointer argument");
     P3D_REQUIRE(x_dtype >= P3D_F32 && x_dtype <= P3D_BF16 && y_dtype >= P3D_F32 && y_dtype <= P3D_BF16 &&
                     param_dtype >= P3D_F32 && param_dtype <= P3D_BF16,
@@ -359,18 +374,19 @@ extern "C" int p3d_layer_norm_train(const void* x, const void* weight, const voi
                 "dim must be a multiple of the 16-byte piece of x, at most 64 pieces and 512 channels");
     P3D_REQUIRE(rows >= 1, "need at least one row");
     P3D_REQUIRE(aligned16(x) && aligned16(y), "x and y must be 16-byte aligned");
+    P3D_REQUIRE(!x_copy || aligned16(x_copy), "x_copy must be 16-byte aligned");
     hipStream_t s = as_stream(stream);
     switch (x_dtype) {
-        case P3D_F32: return dispatch_ln_train<float>(x, weight, bias, param_dtype, y, mean, rstd, rows, dim, y_dtype,
-                                                      eps, s);
-        case P3D_F16: return dispatch_ln_train<_Float16>(x, weight, bias, param_dtype, y, mean, rstd, rows, dim,
-                                                         y_dtype, eps, s);
-        default: return dispatch_ln_train<__bf16>(x, weight, bias, param_dtype, y, mean, rstd, rows, dim, y_dtype,
-                                                  eps, s);
+        case P3D_F32: return dispatch_ln_train<float>(x, weight, bias, param_dtype, y, x_copy, mean, rstd, rows, dim,
+                                                      y_dtype, eps, s);
+        case P3D_F16: return dispatch_ln_train<_Float16>(x, weight, bias, param_dtype, y, x_copy, mean, rstd, rows,
+                                                         dim, y_dtype, eps, s);
+        default: return dispatch_ln_train<__bf16>(x, weight, bias, param_dtype, y, x_copy, mean, rstd, rows, dim,
+                                                  y_dtype, eps, s);
     }
 }
 
-extern "C" int p3d_layer_norm_bwd(const void* dy, const void* x, const void* weight, int32_t param_dtype,
+extern "C" int p3d_layer_norm_bwd(const void* dy, const void* dres, const void* x, const void* weight, int32_t param_dtype,
                                   const float* mean, const float* rstd, void* dx, float* partial, int64_t rows,
                                   int32_t dim, int32_t dy_dtype, int32_t x_dtype, int32_t dx_dtype, int32_t parts,
                                   void* stream) {
@@ -383,13 +399,14 @@ extern "C" int p3d_layer_norm_bwd(const void* dy, const void* x, const void* wei
                 "dim must be a multiple of the 16-byte piece of x, at most 64 pieces and 512 channels");
     P3D_REQUIRE(rows >= 1 && parts >= 1 && parts < 65536, "need at least one row and one part");
     P3D_REQUIRE(aligned16(dy) && aligned16(x) && aligned16(dx), "dy, x and dx must be 16-byte aligned");
+    P3D_REQUIRE(!dres || aligned16(dres), "dres must be 16-byte aligned");
     hipStream_t s = as_stream(stream);
     switch (dy_dtype) {
-        case P3D_F32: return dispatch_ln_bwd_x<float>(dy, x, weight, param_dtype, mean, rstd, dx, partial, rows, dim,
-                                                      parts, x_dtype, dx_dtype, s);
-        case P3D_F16: return dispatch_ln_bwd_x<_Float16>(dy, x, weight, param_dtype, mean, rstd, dx, partial, rows,
-                                                         dim, parts, x_dtype, dx_dtype, s);
-        default: return dispatch_ln_bwd_x<__bf16>(dy, x, weight, param_dtype, mean, rstd, dx, partial, rows, dim,
-                                                  parts, x_dtype, dx_dtype, s);
+        case P3D_F32: return dispatch_ln_bwd_x<float>(dy, dres, x, weight, param_dtype, mean, rstd, dx, partial, rows,
+                                                      dim, parts, x_dtype, dx_dtype, s);
+        case P3D_F16: return dispatch_ln_bwd_x<_Float16>(dy, dres, x, weight, param_dtype, mean, rstd, dx, partial,
+                                                         rows, dim, parts, x_dtype, dx_dtype, s);
+        default: return dispatch_ln_bwd_x<__bf16>(dy, dres, x, weight, param_dtype, mean, rstd, dx, partial, rows,
+                                                  dim, parts, x_dtype, dx_dtype, s);
     }
 }

@@ -87,39 +87,54 @@ class LayerNormTrain(torch.autograd.Function):
     on ``p3d_layer_norm_train`` / ``p3d_layer_norm_bwd``: fp32 statistics, the
     output rounded straight to the compute type dt (the value the next
     linear maps would cast it to), and a backward that returns dx in x's
-    dtype and the affine gradients summed in fp32."""
+    dtype and the affine gradients summed in fp32.
+
+    With residual=True the forward also returns x rounded to dt as a
+    [rows, dim] tensor, written from the same read of x: the residual operand
+    of the output product (OutputResidual with x_owned=True).  The backward
+    then adds that output's gradient into dx inside the kernel, where autograd
+    would otherwise cast it to x's dtype and sum the two gradients of x in a
+    separate pass."""
 
     @staticmethod
-    def forward(ctx, x, weight, bias, eps, dt):
+    def forward(ctx, x, weight, bias, eps, dt, residual=False):
         x2 = _rows(x).contiguous()
         rows, dim = x2.shape
         dev = x.device
         y = torch.empty(rows, dim, dtype=dt, device=dev)
+        xc = torch.empty(rows, dim, dtype=dt, device=dev) if residual else None
         mean = torch.empty(rows, dtype=torch.float32, device=dev)
         rstd = torch.empty(rows, dtype=torch.float32, device=dev)
         _lib.call("p3d_layer_norm_train", x2.data_ptr(), weight.data_ptr(), bias.data_ptr(), _lib.DTYPES[weight.dtype],
-                  y.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, dim, _lib.DTYPES[x2.dtype], _lib.DTYPES[dt],
-                  float(eps), _lib.stream_of(dev))
+                  y.data_ptr(), 0 if xc is None else xc.data_ptr(), mean.data_ptr(), rstd.data_ptr(), rows, dim,
+                  _lib.DTYPES[x2.dtype], _lib.DTYPES[dt], float(eps), _lib.stream_of(dev))
         ctx.save_for_backward(x2, weight, mean, rstd)
         ctx.meta = (x.shape, bias.dtype)
+        ctx.set_materialize_grads(False)
+        if residual:
+            return y.view(x.shape), xc
         return y.view(x.shape)
 
     @staticmethod
-    def backward(ctx, dy):
+    def backward(ctx, dy, dres=None):
         x2, weight, mean, rstd = ctx.saved_tensors
         shape, b_dt = ctx.meta
         rows, dim = x2.shape
+        if dy is None:
+            dy = torch.zeros(rows, dim, dtype=torch.float32, device=x2.device)
         dy2 = _rows(dy).contiguous()
         if dy2.dtype not in _lib.DTYPES:
             dy2 = dy2.float()
+        dr = None if dres is None else _rows(dres).to(dy2.dtype).contiguous()
         dx = torch.empty_like(x2)
         parts = max(1, min(1024, rows // 256))
         part = torch.empty(parts, 2, dim, dtype=torch.float32, device=x2.device)
-        _lib.call("p3d_layer_norm_bwd", dy2.data_ptr(), x2.data_ptr(), weight.data_ptr(), _lib.DTYPES[weight.dtype],
-                  mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(), part.data_ptr(), rows, dim, _lib.DTYPES[dy2.dtype],
-                  _lib.DTYPES[x2.dtype], _lib.DTYPES[dx.dtype], parts, _lib.stream_of(x2.device))
+        _lib.call("p3d_layer_norm_bwd", dy2.data_ptr(), 0 if dr is None else dr.data_ptr(), x2.data_ptr(),
+                  weight.data_ptr(), _lib.DTYPES[weight.dtype], mean.data_ptr(), rstd.data_ptr(), dx.data_ptr(),
+                  part.data_ptr(), rows, dim, _lib.DTYPES[dy2.dtype], _lib.DTYPES[x2.dtype], _lib.DTYPES[dx.dtype],
+                  parts, _lib.stream_of(x2.device))
         sums = part.sum(0)
-        return dx.view(shape), sums[0].to(weight.dtype), sums[1].to(b_dt), None, None
+        return dx.view(shape), sums[0].to(weight.dtype), sums[1].to(b_dt), None, None, None
 
 
 class InputProjections(torch.autograd.Function):
@@ -158,8 +173,10 @@ class InputProjections(torch.autograd.Function):
             dy = _rows(dy).to(x16.dtype)
             if wide:
                 dx.add_(torch.mm(dy, w))
+            elif dx is None:
+                dx = torch.mm(dy, w)
             else:
-                dx = torch.mm(dy, w) if dx is None else torch.addmm(dx, dy, w)
+                dx.addmm_(dy, w)  # in place: no copy of dx into a new result
             grads.append(weight_grad(dy, x16).to(w_dt))
         if dx is None:
             dx = torch.zeros(x16.shape, dtype=x16.dtype, device=x16.device)
@@ -169,14 +186,23 @@ class InputProjections(torch.autograd.Function):
 
 class OutputResidual(torch.autograd.Function):
     """x + y Wo^T in the 16-bit type dt (attention.py:89; autocast's
-    torch.addmm): x [rows, dim], y [rows, k].  The backward gives dx = dout
-    (in x's dtype), dy = dout Wo and an fp32 weight gradient."""
+    torch.addmm): x [rows, dim], y [rows, k].  The product accumulates into
+    the residual in place: into x itself when the caller owns it (x_owned:
+    x is already a dt copy, such as the one LayerNormTrain returns; it is
+    marked dirty and returned), else into a dt copy of x (addmm with a full
+    matrix would copy it into a new result first).  The backward gives
+    dx = dout (in x's dtype), dy = dout Wo and an fp32 weight gradient."""
 
     @staticmethod
-    def forward(ctx, x, y, wo, dt):
+    def forward(ctx, x, y, wo, dt, x_owned=False):
         y16 = y.to(dt).contiguous()
         wo16 = wo.to(dt)
-        out = torch.addmm(x.to(dt), y16, wo16.t())
+        if x_owned and x.dtype == dt and x.dim() == 2 and x.is_contiguous():
+            ctx.mark_dirty(x)
+            out = x
+        else:
+            out = x.to(dt, copy=True)
+        out.addmm_(y16, wo16.t())
         ctx.save_for_backward(y16, wo16)
         ctx.meta = (x.dtype, y.dtype, wo.dtype)
         return out
@@ -187,4 +213,4 @@ class OutputResidual(torch.autograd.Function):
         x_dt, y_dt, wo_dt = ctx.meta
         d16 = dout.to(y16.dtype)
         dy = torch.mm(d16, wo16).to(y_dt)
-        return dout.to(x_dt), dy, weight_grad(d16, y16).to(wo_dt), None
+        return dout.to(x_dt), dy, weight_grad(d16, y16).to(wo_dt), None, None

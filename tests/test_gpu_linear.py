@@ -111,24 +111,35 @@ def test_layer_training_gradients_match_torch_linear(gpu, dtype):
 @pytest.mark.parametrize("x_dtype,y_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float16),
                                               (torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32)])
 @pytest.mark.parametrize("rows,dim", [(1, 192), (1003, 192), (517, 64), (300, 512)])
-def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, rows, dim):
+@pytest.mark.parametrize("residual", [False, True])
+def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, rows, dim, residual):
     """LayerNormTrain against torch.layer_norm in fp64 on the same inputs: the
     output to one rounding of the output type, dx to fp32 accuracy, the
-    affine gradients summed over the rows."""
+    affine gradients summed over the rows.  With the residual copy: the copy
+    is x cast to the output type (bit-exact), and its gradient is added to
+    dx."""
     if dim // (16 // torch.tensor([], dtype=x_dtype).element_size()) > 64:
         pytest.skip("more than 64 pieces per row")
-    print(f"layer norm train {rows}x{dim} {x_dtype}->{y_dtype}", flush=True)
+    print(f"layer norm train {rows}x{dim} {x_dtype}->{y_dtype} residual={residual}", flush=True)
     gen = torch.Generator(device=gpu).manual_seed(rows + dim)
     x = (torch.randn(rows, dim, device=gpu, generator=gen) * 2 + 0.5).to(x_dtype)
     w = torch.randn(dim, device=gpu, generator=gen)
     b = torch.randn(dim, device=gpu, generator=gen)
     dy = torch.randn(rows, dim, device=gpu, generator=gen).to(y_dtype)
+    dres = torch.randn(rows, dim, device=gpu, generator=gen).to(y_dtype)
     xg, wg, bg = (t.clone().requires_grad_() for t in (x, w, b))
-    y = linear.LayerNormTrain.apply(xg, wg, bg, 1e-5, y_dtype)
-    y.backward(dy)
+    if residual:
+        y, xc = linear.LayerNormTrain.apply(xg, wg, bg, 1e-5, y_dtype, True)
+        assert xc.dtype == y_dtype and torch.equal(xc, x.to(y_dtype))
+        torch.autograd.backward([y, xc], [dy, dres])
+    else:
+        y = linear.LayerNormTrain.apply(xg, wg, bg, 1e-5, y_dtype)
+        y.backward(dy)
     xd, wd, bd = (t.detach().double().requires_grad_() for t in (x, w, b))
     e = torch.nn.functional.layer_norm(xd, (dim,), wd, bd, 1e-5)
     e.backward(dy.double())
+    if residual:
+        xd.grad += dres.double()
     ulp = {torch.bfloat16: 2 ** -8, torch.float16: 2 ** -10, torch.float32: 2 ** -18}[y_dtype]
     assert y.dtype == y_dtype
     # One rounding of the output type, plus fp32 arithmetic on terms of order

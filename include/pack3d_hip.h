@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 6
+#define P3D_ABI_VERSION 7
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -112,7 +112,11 @@ int p3d_check_layout(const int64_t grid[3], const int64_t* order, const int64_t*
  *   sk_norm_max [B, G, 64] (fp32)  maxima of the 2-norms of the stored
  *                               (rounded) sk rows, summary m reducing into
  *                               slot m % 64; their max bounds every summary
- *                               score of a query (Cauchy-Schwarz) */
+ *                               score of a query (Cauchy-Schwarz)
+ * The call clears sk_norm_max with a launch of its own before pooling,
+ * unless norms_cleared is nonzero: the caller then guarantees that the 64
+ * slots per (batch, kv head) hold zeros (a buffer allocated zeroed for this
+ * call, say). */
 typedef struct p3d_pool_args {
     int32_t batch, kv_heads, tokens, head_dim, dtype;
     int32_t fine_blocks, slots, pool_size, summaries;
@@ -127,6 +131,7 @@ typedef struct p3d_pool_args {
     void* sk;
     void* svt;
     float* sk_norm_max;
+    int32_t norms_cleared;      /* nonzero: sk_norm_max already zero, no clear */
 } p3d_pool_args;
 int p3d_pool_fwd(const p3d_pool_args* args, void* stream);
 

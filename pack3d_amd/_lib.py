@@ -22,7 +22,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 6  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 7  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -36,7 +36,7 @@ class PoolArgs(ctypes.Structure):
                 ("summaries", c_int32), ("temperature", c_float), ("key_scale", c_float),
                 ("kg", View), ("vg", View),
                 ("blocks", c_void_p), ("weight", c_void_p), ("bias", c_void_p), ("rope", Rope),
-                ("sk", c_void_p), ("svt", c_void_p), ("sk_norm_max", c_void_p)]
+                ("sk", c_void_p), ("svt", c_void_p), ("sk_norm_max", c_void_p), ("norms_cleared", c_int32)]
 
 
 class AttnArgs(ctypes.Structure):

@@ -116,7 +116,8 @@ class ForwardPlan:
         mp = -(-m // 32) * 32
         self.sk = torch.empty(b, g, mp, d, dtype=q.dtype, device=dev)
         self.svt = torch.empty(b, g, mp // 32, d, 32, dtype=q.dtype, device=dev)
-        self.sk_norm_max = torch.empty(b * g * 64, dtype=torch.float32, device=dev)
+        # Allocated zeroed, so the first pooling launch needs no clear of its own.
+        self.sk_norm_max = torch.zeros(b * g * 64, dtype=torch.float32, device=dev)
         self._keep = [q, kl, vl, kg, vg, geometry, rope, pool_rope]
         w32 = param_f32(weight)
         b32 = param_f32(bias)
@@ -126,7 +127,7 @@ class ForwardPlan:
         self.pool_args = _lib.PoolArgs(b, g, n, d, dt, f, slots, geometry.pool_size, m, float(temperature),
                                        self.key_scale, _lib.view(kg), _lib.view(vg), geometry.blocks.data_ptr(),
                                        w32.data_ptr(), b32.data_ptr(), pool_rope.struct(),
-                                       self.sk.data_ptr(), self.svt.data_ptr(), self.sk_norm_max.data_ptr())
+                                       self.sk.data_ptr(), self.svt.data_ptr(), self.sk_norm_max.data_ptr(), 1)
         self.y = torch.empty(b, n, h, d, dtype=q.dtype, device=dev).transpose(1, 2)
         sl32, sg32 = param_f32(sl), param_f32(sg)
         if gate.dtype not in _lib.DTYPES:
@@ -188,6 +189,7 @@ class ForwardPlan:
 
     def pool(self):
         _lib.call("p3d_pool_fwd", self.pool_args, _lib.stream_of(self.device))
+        self.pool_args.norms_cleared = 0  # a repeated call must clear the slots again
 
     def attention(self):
         stream = _lib.stream_of(self.device)

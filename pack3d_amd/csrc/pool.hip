@@ -4,13 +4,13 @@
 // One wave pools one coarse summary of one (batch, kv head).  For each of its
 // fine blocks the wave issues every 16-byte load of the block's K and V rows
 // at once (lane l holds pieces l, l + 64, ... of the 64 x D/EP piece grid)
-// and writes the K and V rows to two LDS row buffers with 16-byte stores.
-// Then one lane per slot reads its K row (conflict-free 16-byte reads),
-// rotates it, rounds it to the storage type (the reference pools rotated keys
-// stored in that type), writes it back and forms the slot logit; the slot
-// softmax is a wave reduction.  The weighted sums are column reads of the K
-// and V rows.  The coarse mean divides by the number of non-empty fine
-// blocks.
+// and writes them to LDS as rows with 16-byte stores.  Then one lane per
+// slot reads its K row, rotates it, rounds it to the storage type (the
+// reference pools rotated keys stored in that type), writes it back and
+// forms the slot logit; the slot softmax is a wave reduction.  The forward
+// takes the weighted sums over the slots on MFMA (k_pool_fwd); the backward
+// forms its column sums with one lane per column dword (column_sums_w).  The
+// coarse mean divides by the number of non-empty fine blocks.
 #include <algorithm>
 
 #include "rope.hpp"
@@ -967,7 +967,7 @@ extern "C" int p3d_pool_fwd(const p3d_pool_args* args, void* stream) {
     const p3d_pool_args& a = *args;
     hipStream_t s = as_stream(stream);
     const int bgn = a.batch * a.kv_heads * kNormSlots;
-    k_zero_f32<<<(unsigned)cdiv(bgn, 256), 256, 0, s>>>(a.sk_norm_max, bgn);
+    if (!a.norms_cleared) k_zero_f32<<<(unsigned)cdiv(bgn, 256), 256, 0, s>>>(a.sk_norm_max, bgn);
     switch (a.head_dim) {
         case 16: launch_pool<16>(d, a.dtype, s); break;
         case 32: launch_pool<32>(d, a.dtype, s); break;

@@ -323,3 +323,37 @@ def test_fused_out_residual_matches_addmm(gpu, dtype, dim, heads, d):
     tol = {torch.bfloat16: 2 ** -7, torch.float16: 2 ** -10}[dtype]
     g32, e32 = got.float(), exp.float()
     assert ((g32 - e32).abs() <= tol * (e32.abs() + 1.0)).all(), float((g32 - e32).abs().max())
+
+
+def test_pool_norm_slots_first_and_repeated_call(gpu):
+    """The plan's first pooling launch takes the zero-allocated norm slots
+    as they are (no clear launch); a repeated launch clears them itself, so
+    slots overwritten in between come out the same.  Both equal the maxima of
+    the stored summary-key norms, summary m reducing into slot m % 64."""
+    from pack3d_amd.core import ForwardPlan
+
+    print("pool norm slots", flush=True)
+    torch.manual_seed(0)
+    shape = (8, 16, 12)
+    n = math.prod(shape)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64).to(gpu)
+    lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block", device=gpu)
+    x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1)).to(gpu, torch.bfloat16)
+    layer = layer.to(torch.bfloat16)
+    with torch.inference_mode():
+        q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, lay)
+        plan = ForwardPlan(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate, layer.local_scale,
+                           layer.global_scale, lay.geometry, layer.temperature, rope, rope)
+        assert plan.pool_args.norms_cleared == 1
+        plan.pool()
+        assert plan.pool_args.norms_cleared == 0
+        first = plan.sk_norm_max.clone()
+        plan.sk_norm_max.fill_(1e30)
+        plan.pool()
+        torch.cuda.synchronize()
+    assert torch.equal(plan.sk_norm_max, first)
+    m = lay.geometry.num_summaries
+    norms = plan.sk[:, :, :m].float().pow(2).sum(-1).sqrt() * (1 + 1e-6)  # [B, G, M]
+    exp = torch.zeros(norms.shape[0], norms.shape[1], 64, device=gpu)
+    exp.scatter_reduce_(2, (torch.arange(m, device=gpu) % 64).expand_as(norms), norms, reduce="amax")
+    assert torch.allclose(first.view_as(exp), exp, rtol=1e-5, atol=0), (first.view_as(exp) - exp).abs().max()

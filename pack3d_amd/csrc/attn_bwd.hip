@@ -730,30 +730,52 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
 
 // ------------------------------------------------------------------ finish
 // dQ = R^T round(round(dQ_L) + round(dQ_G)) and dK_L = R^T round(dK_L), each
-// rounded to the storage type; one 16-byte piece per thread.
-template <typename T>
-__global__ void k_finish_bwd(BwdDev a, RopeDev rope, int D, T* dq, T* dkl) {
+// rounded to the storage type; one 16-byte output piece per thread.  Grid y
+// walks the (batch, head) planes of dq and then those of dkl; grid x the
+// pieces of a plane's rows.  The fp32 inputs are read 16 bytes at a time and
+// the rotation's pair descriptors come from LDS.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_finish_bwd(BwdDev a, RopeDev rope, int plane0, T* dq, T* dkl) {
     constexpr int EP = Piece<T>::N;
-    const int ppr = D / EP;
-    const int64_t qpieces = (int64_t)a.B * a.H * a.N * ppr;
-    const int64_t kpieces = (int64_t)a.B * a.G * a.N * ppr;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= qpieces + kpieces) return;
-    const bool isq = e < qpieces;
-    const int64_t pe = isq ? e : e - qpieces;
-    const int piece = (int)(pe % ppr);
-    const int64_t row = pe / ppr;  // (b, head) * N + n
-    const int64_t n = row % a.N;
+    constexpr int PPR = D / EP;  // pieces per row
+    __shared__ int4 meta[D / 2];
+    for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(rope.pairs, j);
+    __syncthreads();
+    // Plane p: (b, head) of dq for p < B*H, else (b, kv head) of dkl.  Rows
+    // of a plane times its pieces fit in 31 bits (checked on the host).
+    const int p = plane0 + (int)blockIdx.y;
+    const int idx = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (idx >= a.N * PPR) return;
+    const int n = idx / PPR, piece = idx - n * PPR;
+    const bool isq = p < a.B * a.H;
+    const int64_t off = (int64_t)(isq ? p : p - a.B * a.H) * a.N * D + (int64_t)n * D + piece * EP;
     float x[EP];
-    const int64_t off = row * D + piece * EP;
+    if (isq) {
+        const f32x4* l = reinterpret_cast<const f32x4*>(a.dq_l + off);
+        const f32x4* g = reinterpret_cast<const f32x4*>(a.dq_g + off);
 #pragma unroll
-    for (int i = 0; i < EP; ++i) {
-        x[i] = isq ? round_to<T>(round_to<T>(a.dq_l[off + i]) + round_to<T>(a.dq_g[off + i]))
-                   : round_to<T>(a.dk_l[off + i]);
+        for (int v = 0; v < EP / 4; ++v) {
+            const f32x4 lv = l[v], gv = g[v];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[4 * v + i] = round_to<T>(round_to<T>(lv[i]) + round_to<T>(gv[i]));
+        }
+    } else {
+        const f32x4* l = reinterpret_cast<const f32x4*>(a.dk_l + off);
+#pragma unroll
+        for (int v = 0; v < EP / 4; ++v) {
+            const f32x4 lv = l[v];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[4 * v + i] = round_to<T>(lv[i]);
+        }
     }
-    int64_t pos[3];
-    rope_position(rope, n, pos);
-    rope_apply(rope, pos, piece * EP, x, EP, true);
+    int pos[3];
+    rope_position32(rope, n, pos);
+#pragma unroll
+    for (int e = 0; e < EP; e += 2) {
+        const int4 m = meta[(piece * EP + e) >> 1];
+        const float2 cs = rope.table[m.x + m.y * pos[0] + m.z * pos[1] + m.w * pos[2]];
+        rotate_pair(x[e], x[e + 1], cs.x, -cs.y);
+    }
     store_piece<T>((isq ? dq : dkl) + off, x);
 }
 
@@ -911,6 +933,28 @@ extern "C" int p3d_global_bwd(const p3d_bwd_args* args, void* stream) {
     return check_launch("p3d_global_bwd");
 }
 
+template <typename T, int D>
+void launch_finish(const BwdDev& d, const RopeDev& r, void* dq, void* dkl, hipStream_t s) {
+    constexpr int PPR = D / Piece<T>::N;
+    const unsigned bx = (unsigned)cdiv((int64_t)d.N * PPR, 256);
+    const int planes = d.B * (d.H + d.G);
+    for (int p0 = 0; p0 < planes; p0 += 65535) {
+        const unsigned by = (unsigned)(planes - p0 < 65535 ? planes - p0 : 65535);
+        k_finish_bwd<T, D><<<dim3(bx, by), 256, 0, s>>>(d, r, p0, (T*)dq, (T*)dkl);
+    }
+}
+
+template <typename T>
+void dispatch_finish(const BwdDev& d, const RopeDev& r, int head_dim, void* dq, void* dkl, hipStream_t s) {
+    switch (head_dim) {
+        case 16: launch_finish<T, 16>(d, r, dq, dkl, s); break;
+        case 32: launch_finish<T, 32>(d, r, dq, dkl, s); break;
+        case 48: launch_finish<T, 48>(d, r, dq, dkl, s); break;
+        case 64: launch_finish<T, 64>(d, r, dq, dkl, s); break;
+        default: launch_finish<T, 128>(d, r, dq, dkl, s); break;
+    }
+}
+
 extern "C" int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, void* dq, void* dkl, void* stream) {
     P3D_REQUIRE(args && rope && dq && dkl, "null argument");
     BwdDev d;
@@ -918,20 +962,13 @@ extern "C" int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, vo
     P3D_REQUIRE(args->dq_local && args->dq_global && args->dk_local, "null pointer argument");
     P3D_REQUIRE(rope->table && rope->pairs && (rope->packed || rope->coords), "bad rope arguments");
     const int ep = 16 / dtype_size(args->dtype);
-    const int64_t pieces = ((int64_t)d.B * d.H * d.N + (int64_t)d.B * d.G * d.N) * (args->head_dim / ep);
-    const unsigned blocks = (unsigned)cdiv(pieces, 256);
+    P3D_REQUIRE((int64_t)d.N * (args->head_dim / ep) < ((int64_t)1 << 31), "tokens * pieces per row must be below 2^31");
     hipStream_t s = as_stream(stream);
     const RopeDev r = rope_dev(*rope);
     switch (args->dtype) {
-        case P3D_F32:
-            k_finish_bwd<float><<<blocks, 256, 0, s>>>(d, r, args->head_dim, (float*)dq, (float*)dkl);
-            break;
-        case P3D_F16:
-            k_finish_bwd<_Float16><<<blocks, 256, 0, s>>>(d, r, args->head_dim, (_Float16*)dq, (_Float16*)dkl);
-            break;
-        default:
-            k_finish_bwd<__bf16><<<blocks, 256, 0, s>>>(d, r, args->head_dim, (__bf16*)dq, (__bf16*)dkl);
-            break;
+        case P3D_F32: dispatch_finish<float>(d, r, args->head_dim, dq, dkl, s); break;
+        case P3D_F16: dispatch_finish<_Float16>(d, r, args->head_dim, dq, dkl, s); break;
+        default: dispatch_finish<__bf16>(d, r, args->head_dim, dq, dkl, s); break;
     }
     return check_launch("p3d_finish_bwd");
 }

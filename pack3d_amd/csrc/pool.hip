@@ -65,15 +65,6 @@ __device__ __forceinline__ void stage_rows(uint32_t* rows, const uint4 (&r)[C::P
     }
 }
 
-// Rotary metadata of pair j as staged in LDS: {base, stride along axis 0,
-// along axis 1, along axis 2}, where only the pair's own axis has a non-zero
-// stride, so the table index is base + sum_a stride_a * pos[a] with no
-// per-pair branch on the axis.
-__device__ __forceinline__ int4 pair_meta(const int32_t* pairs, int j) {
-    const int base = pairs[3 * j], stride = pairs[3 * j + 1], axis = pairs[3 * j + 2];
-    return int4{base, axis == 0 ? stride : 0, axis == 1 ? stride : 0, axis == 2 ? stride : 0};
-}
-
 // Product of two non-negative values below 2^24, as one 24-bit multiply
 // (v_mul_u32_u24; HIP's __mul24 is an out-of-line library call here).
 __device__ __forceinline__ int mul_u24(int x, int y) {

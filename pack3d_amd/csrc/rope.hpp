@@ -49,6 +49,15 @@ __device__ __forceinline__ void rope_apply(const RopeDev& r, const int64_t pos[3
     }
 }
 
+// Rotary metadata of pair j, for staging in LDS: {base, stride along axis 0,
+// along axis 1, along axis 2}, where only the pair's own axis has a non-zero
+// stride, so the table index is base + sum_a stride_a * pos[a] with no
+// per-pair branch on the axis.
+__device__ __forceinline__ int4 pair_meta(const int32_t* pairs, int j) {
+    const int base = pairs[3 * j], stride = pairs[3 * j + 1], axis = pairs[3 * j + 2];
+    return int4{base, axis == 0 ? stride : 0, axis == 1 ? stride : 0, axis == 2 ? stride : 0};
+}
+
 // 32-bit forms for kernels that keep positions of many rows in registers.
 // Table indices are base + stride * coordinate < 2^31: coordinates are below
 // the token count and the hosts validate rows * head_dim < 2^31.

@@ -181,7 +181,8 @@ int p3d_local_fwd_indexed(const p3d_attn_args* args, const int32_t* neighbors, i
                           float* o_local, void* stream);
 
 /* Standalone rotation (rotary.py:10-45): y = R(pos) x, or R(pos)^T x when
- * inverse != 0, for x and y [B, H, N, D] views of dtype. */
+ * inverse != 0, for x and y [B, H, N, D] views of dtype; D in {16, 32, 48,
+ * 64, 128}, as for the attention kernels. */
 int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tokens,
                int32_t head_dim, int32_t dtype, const p3d_rope* rope, int32_t inverse, void* stream);
 

@@ -789,26 +789,60 @@ struct RotDev {
     RopeDev rope;
 };
 
-template <typename T>
-__global__ void k_rotate(RotDev a) {
+// One 16-byte piece per thread.  Grid y walks the (batch, head) planes from
+// plane0, grid x the pieces of a plane's rows (tokens * pieces per row below
+// 2^31, checked on the host); the pair descriptors come from LDS.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_rotate(RotDev a, int plane0) {
     constexpr int EP = Piece<T>::N;
-    const int ppr = a.D / EP;
-    const int64_t total = (int64_t)a.B * a.H * a.N * ppr;
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= total) return;
-    const int piece = (int)(e % ppr);
-    const int64_t row = e / ppr;
-    const int64_t n = row % a.N;
-    const int64_t bh = row / a.N;
-    const int64_t b = bh / a.H, h = bh % a.H;
+    constexpr int PPR = D / EP;
+    __shared__ int4 meta[D / 2];
+    for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(a.rope.pairs, j);
+    __syncthreads();
+    const int p = plane0 + (int)blockIdx.y;
+    const int idx = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (idx >= a.N * PPR) return;
+    const int n = idx / PPR, piece = idx - n * PPR;
+    const int b = p / a.H, h = p - b * a.H;
     float x[EP];
-    load_piece<T>(reinterpret_cast<const T*>(a.x) + b * a.xsb + h * a.xsh + n * a.xsn + piece * EP, x);
-    int64_t pos[3];
-    rope_position(a.rope, n, pos);
-    rope_apply(a.rope, pos, piece * EP, x, EP, a.inverse != 0);
-    T* y = reinterpret_cast<T*>(a.y) + b * a.ysb + h * a.ysh + n * a.ysn + piece * EP;
+    load_piece<T>(reinterpret_cast<const T*>(a.x) + b * a.xsb + h * a.xsh + (int64_t)n * a.xsn + piece * EP, x);
+    int pos[3];
+    rope_position32(a.rope, n, pos);
+    const float sgn = a.inverse ? -1.f : 1.f;
 #pragma unroll
-    for (int i = 0; i < EP; ++i) y[i] = from_f32<T>(x[i]);
+    for (int e = 0; e < EP; e += 2) {
+        const int4 m = meta[(piece * EP + e) >> 1];
+        const float2 cs = a.rope.table[m.x + m.y * pos[0] + m.z * pos[1] + m.w * pos[2]];
+        rotate_pair(x[e], x[e + 1], cs.x, sgn * cs.y);
+    }
+    uint4 raw;
+    T* v = reinterpret_cast<T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < EP; ++e) v[e] = from_f32<T>(x[e]);
+    *reinterpret_cast<uint4*>(reinterpret_cast<T*>(a.y) + b * a.ysb + h * a.ysh + (int64_t)n * a.ysn + piece * EP) =
+        raw;
+}
+
+template <typename T, int D>
+void launch_rotate(const RotDev& d, hipStream_t s) {
+    constexpr int PPR = D / Piece<T>::N;
+    const unsigned bx = (unsigned)cdiv((int64_t)d.N * PPR, 256);
+    const int planes = d.B * d.H;
+    for (int p0 = 0; p0 < planes; p0 += 65535) {
+        const unsigned by = (unsigned)(planes - p0 < 65535 ? planes - p0 : 65535);
+        k_rotate<T, D><<<dim3(bx, by), 256, 0, s>>>(d, p0);
+    }
+}
+
+template <typename T>
+void dispatch_rotate(const RotDev& d, hipStream_t s) {
+    switch (d.D) {
+        case 16: launch_rotate<T, 16>(d, s); break;
+        case 32: launch_rotate<T, 32>(d, s); break;
+        case 48: launch_rotate<T, 48>(d, s); break;
+        case 64: launch_rotate<T, 64>(d, s); break;
+        default: launch_rotate<T, 128>(d, s); break;
+    }
 }
 
 // Rope tables up to this size are staged in LDS by every pool block.
@@ -973,20 +1007,23 @@ extern "C" int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, 
                           int32_t head_dim, int32_t dtype, const p3d_rope* rope, int32_t inverse, void* stream) {
     P3D_REQUIRE(rope && rope->table && rope->pairs && (rope->packed || rope->coords), "bad rope");
     const int es = dtype_size(dtype);
-    P3D_REQUIRE(head_dim % (16 / es) == 0 && head_dim % 2 == 0, "head_dim must be a multiple of 16 bytes");
+    P3D_REQUIRE(dtype >= P3D_F32 && dtype <= P3D_BF16, "unknown dtype");
+    P3D_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 48 || head_dim == 64 || head_dim == 128,
+                "head_dim must be 16, 32, 48, 64 or 128");
+    P3D_REQUIRE(batch >= 1 && heads >= 1 && tokens >= 1, "empty rotation problem");
+    P3D_REQUIRE((int64_t)tokens * (head_dim / (16 / es)) < ((int64_t)1 << 31),
+                "tokens * pieces per row must be below 2^31");
     P3D_REQUIRE(view_ok(x, es) && view_ok(y, es), "rows must be 16-byte aligned");
     RotDev d{};
     d.B = batch, d.H = heads, d.N = tokens, d.D = head_dim, d.inverse = inverse;
     d.x = (const char*)x.data, d.xsb = x.sb, d.xsh = x.sh, d.xsn = x.sn;
     d.y = (char*)y.data, d.ysb = y.sb, d.ysh = y.sh, d.ysn = y.sn;
     d.rope = rope_dev(*rope);
-    const int64_t total = (int64_t)batch * heads * tokens * (head_dim / (16 / es));
-    const unsigned g = (unsigned)cdiv(total, 256);
     hipStream_t s = as_stream(stream);
     switch (dtype) {
-        case P3D_F32: k_rotate<float><<<g, 256, 0, s>>>(d); break;
-        case P3D_F16: k_rotate<_Float16><<<g, 256, 0, s>>>(d); break;
-        default: k_rotate<__bf16><<<g, 256, 0, s>>>(d); break;
+        case P3D_F32: dispatch_rotate<float>(d, s); break;
+        case P3D_F16: dispatch_rotate<_Float16>(d, s); break;
+        default: dispatch_rotate<__bf16>(d, s); break;
     }
     return check_launch("p3d_rotate");
 }

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 7
+#define P3D_ABI_VERSION 8
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -348,16 +348,17 @@ int p3d_local_bwd_grid(const p3d_bwd_args* args, const int32_t grid[3], const in
 int p3d_global_bwd(const p3d_bwd_args* args, void* stream);
 
 /* dq = R^T round(round(dq_local) + round(dq_global)) and dkl = R^T round(dk_local)
- * (kernels.py:202-206 rounding; R^T the inverse rotation of rope), both
- * [B,*,N,D] contiguous in dtype. */
-int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, void* dq, void* dkl, void* stream);
+ * (kernels.py:202-206 rounding; R^T the inverse rotation of rope), written
+ * into the views dq [B,H,N,D] and dkl [B,G,N,D] of dtype (16-byte aligned
+ * rows; e.g. the q and kl column ranges of the projections' gradients). */
+int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, p3d_view dq, p3d_view dkl, void* stream);
 
 /* Pooling backward (kernels.py:240-270): from the split partials of dsk / dsv,
- * writes dkg (gradient of the UNROTATED kg: R^T applied) and dvg, both
- * [B,G,N,D] contiguous in dtype, and per-summary partials dw_part
- * [B*G*Mp, D] and db_part [B*G*Mp, slots]. */
+ * writes dkg (gradient of the UNROTATED kg: R^T applied) and dvg into
+ * [B,G,N,D] views of dtype (16-byte aligned rows), and per-summary partials
+ * dw_part [B*G*Mp, D] and db_part [B*G*Mp, slots]. */
 int p3d_pool_bwd(const p3d_pool_args* pool, const float* dsk_part, const float* dsv_part, int32_t splits,
-                 void* dkg, void* dvg, float* dw_part, float* db_part, void* stream);
+                 p3d_view dkg, p3d_view dvg, float* dw_part, float* db_part, void* stream);
 
 /* ---- self-tests (no counterpart in the reference) ---------------------- */
 

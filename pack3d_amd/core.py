@@ -264,10 +264,13 @@ def _splits(n, m, bg):
 
 
 def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm_max, o_local, o_global,
-             lse_local, lse_global, geometry, temperature, rope, pool_rope, key_scale):
+             lse_local, lse_global, geometry, temperature, rope, pool_rope, key_scale, out=None):
     """The ten gradients of the core (kernels.py:313-356 of amilworks/Pack3D):
     dq, dkl, dkg with respect to the unrotated inputs (the rotation's backward
-    is fused), dvl, dvg, dweight, dbias, dgate, dsl, dsg."""
+    is fused), dvl, dvg, dweight, dbias, dgate, dsl, dsg.  `out` may give
+    (dq, dkl, dkg, dvg) as [B, *, N, d] views (16-byte aligned rows) that the
+    kernels write in place, such as column ranges of the projections'
+    gradients; they are returned in their place."""
     b, h, n, d = q.shape
     g = kl.shape[1]
     dev, dt = q.device, _lib.DTYPES[q.dtype]
@@ -327,9 +330,10 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
         nb, rev = geometry.neighbors, geometry.reverse_neighbors
         _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)
     _lib.call("p3d_global_bwd", a, stream)
-    dq = empty(b, h, n, d)
-    dkl = empty(b, g, n, d)
-    _lib.call("p3d_finish_bwd", a, rope.struct(), dq.data_ptr(), dkl.data_ptr(), stream)
+    if out is None:
+        out = (empty(b, h, n, d), empty(b, g, n, d), empty(b, g, n, d), empty(b, g, n, d))
+    dq, dkl, dkg, dvg = out
+    _lib.call("p3d_finish_bwd", a, rope.struct(), _lib.view(dq), _lib.view(dkl), stream)
 
     w32 = param_f32(weight)
     b32 = param_f32(bias)
@@ -337,11 +341,10 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
                               _lib.view(kg), _lib.view(vg), geometry.blocks.data_ptr(), w32.data_ptr(),
                               b32.data_ptr(), pool_rope.struct(), sk.data_ptr(), svt.data_ptr(),
                               sk_norm_max.data_ptr())
-    dkg, dvg = empty(b, g, n, d), empty(b, g, n, d)
     dwp = empty(b * g * mp, d, dtype=f32)
     dbp = empty(b * g * mp, slots, dtype=f32)
     _lib.call("p3d_pool_bwd", pool_args, bufs["dskp"].data_ptr(), bufs["dsvp"].data_ptr(), splits,
-              dkg.data_ptr(), dvg.data_ptr(), dwp.data_ptr(), dbp.data_ptr(), stream)
+              _lib.view(dkg), _lib.view(dvg), dwp.data_ptr(), dbp.data_ptr(), stream)
     keep += [w32, b32]
     dweight = dwp.sum(0).to(weight.dtype)
     dbias = dbp.sum(0).to(bias.dtype)
@@ -364,8 +367,9 @@ def _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, r
 class _Pack3DProjections(torch.autograd.Function):
     """The core on views of the layer's projections, qp [B, N, H*d] and kvp
     [B, N, 4*G*d] chunked kl | vl | kg | vg (attention.py:64-67), with
-    gradients returned for qp and kvp directly: the backward's dense
-    gradients are copied into the projections' layout by p3d_copy_rows, so
+    gradients returned for qp and kvp directly: the finishing and pooling
+    backward kernels write dq, dkl, dkg and dvg straight into the
+    projections' layout, and dvl is copied there by p3d_copy_rows, so
     autograd does not transpose and stack the five views."""
 
     @staticmethod
@@ -386,13 +390,14 @@ class _Pack3DProjections(torch.autograd.Function):
         ctx.geometry.check_unmodified()
         qp, kvp, weight, bias, gate, sl, sg, *state = ctx.saved_tensors
         views = _projection_views(qp, kvp, ctx.heads, ctx.kv_heads)
-        grads = backward(dy, *views, weight, bias, gate, sl, sg, *state, ctx.geometry, ctx.temperature, ctx.rope,
-                         ctx.rope, ctx.key_scale)
         dqp, dkvp = torch.empty_like(qp), torch.empty_like(kvp)
-        stream = _lib.stream_of(qp.device)
-        for src, dst in zip(grads[:5], _projection_views(dqp, dkvp, ctx.heads, ctx.kv_heads)):
-            b, h, n, d = src.shape
-            _lib.call("p3d_copy_rows", _lib.view(src), _lib.view(dst), b, h, n, d, _lib.DTYPES[src.dtype], stream)
+        dq, dkl, dvl, dkg, dvg = _projection_views(dqp, dkvp, ctx.heads, ctx.kv_heads)
+        grads = backward(dy, *views, weight, bias, gate, sl, sg, *state, ctx.geometry, ctx.temperature, ctx.rope,
+                         ctx.rope, ctx.key_scale, out=(dq, dkl, dkg, dvg))
+        src = grads[2]  # dvl, dense from the local dK/dV pass
+        b, g, n, d = src.shape
+        _lib.call("p3d_copy_rows", _lib.view(src), _lib.view(dvl), b, g, n, d, _lib.DTYPES[src.dtype],
+                  _lib.stream_of(qp.device))
         return (dqp, dkvp, *grads[5:], None, None, None, None, None)
 
 

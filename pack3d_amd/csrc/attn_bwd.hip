@@ -735,7 +735,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
 // pieces of a plane's rows.  The fp32 inputs are read 16 bytes at a time and
 // the rotation's pair descriptors come from LDS.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_finish_bwd(BwdDev a, RopeDev rope, int plane0, T* dq, T* dkl) {
+__global__ __launch_bounds__(256) void k_finish_bwd(BwdDev a, RopeDev rope, int plane0, p3d_view dq, p3d_view dkl) {
     constexpr int EP = Piece<T>::N;
     constexpr int PPR = D / EP;  // pieces per row
     __shared__ int4 meta[D / 2];
@@ -748,7 +748,8 @@ __global__ __launch_bounds__(256) void k_finish_bwd(BwdDev a, RopeDev rope, int 
     if (idx >= a.N * PPR) return;
     const int n = idx / PPR, piece = idx - n * PPR;
     const bool isq = p < a.B * a.H;
-    const int64_t off = (int64_t)(isq ? p : p - a.B * a.H) * a.N * D + (int64_t)n * D + piece * EP;
+    const int pp = isq ? p : p - a.B * a.H, heads = isq ? a.H : a.G;
+    const int64_t off = (int64_t)pp * a.N * D + (int64_t)n * D + piece * EP;  // dense fp32 inputs
     float x[EP];
     if (isq) {
         const f32x4* l = reinterpret_cast<const f32x4*>(a.dq_l + off);
@@ -776,7 +777,9 @@ __global__ __launch_bounds__(256) void k_finish_bwd(BwdDev a, RopeDev rope, int 
         const float2 cs = rope.table[m.x + m.y * pos[0] + m.z * pos[1] + m.w * pos[2]];
         rotate_pair(x[e], x[e + 1], cs.x, -cs.y);
     }
-    store_piece<T>((isq ? dq : dkl) + off, x);
+    const p3d_view& o = isq ? dq : dkl;
+    const int b = pp / heads, h = pp - b * heads;
+    store_piece<T>(reinterpret_cast<T*>(o.data) + b * o.sb + h * o.sh + (int64_t)n * o.sn + piece * EP, x);
 }
 
 int fill_bwd(const p3d_bwd_args& x, BwdDev& d) {
@@ -934,18 +937,19 @@ extern "C" int p3d_global_bwd(const p3d_bwd_args* args, void* stream) {
 }
 
 template <typename T, int D>
-void launch_finish(const BwdDev& d, const RopeDev& r, void* dq, void* dkl, hipStream_t s) {
+void launch_finish(const BwdDev& d, const RopeDev& r, const p3d_view& dq, const p3d_view& dkl, hipStream_t s) {
     constexpr int PPR = D / Piece<T>::N;
     const unsigned bx = (unsigned)cdiv((int64_t)d.N * PPR, 256);
     const int planes = d.B * (d.H + d.G);
     for (int p0 = 0; p0 < planes; p0 += 65535) {
         const unsigned by = (unsigned)(planes - p0 < 65535 ? planes - p0 : 65535);
-        k_finish_bwd<T, D><<<dim3(bx, by), 256, 0, s>>>(d, r, p0, (T*)dq, (T*)dkl);
+        k_finish_bwd<T, D><<<dim3(bx, by), 256, 0, s>>>(d, r, p0, dq, dkl);
     }
 }
 
 template <typename T>
-void dispatch_finish(const BwdDev& d, const RopeDev& r, int head_dim, void* dq, void* dkl, hipStream_t s) {
+void dispatch_finish(const BwdDev& d, const RopeDev& r, int head_dim, const p3d_view& dq, const p3d_view& dkl,
+                     hipStream_t s) {
     switch (head_dim) {
         case 16: launch_finish<T, 16>(d, r, dq, dkl, s); break;
         case 32: launch_finish<T, 32>(d, r, dq, dkl, s); break;
@@ -955,14 +959,17 @@ void dispatch_finish(const BwdDev& d, const RopeDev& r, int head_dim, void* dq, 
     }
 }
 
-extern "C" int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, void* dq, void* dkl, void* stream) {
-    P3D_REQUIRE(args && rope && dq && dkl, "null argument");
+extern "C" int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, p3d_view dq, p3d_view dkl,
+                              void* stream) {
+    P3D_REQUIRE(args && rope, "null argument");
     BwdDev d;
     if (int rc = fill_bwd(*args, d)) return rc;
     P3D_REQUIRE(args->dq_local && args->dq_global && args->dk_local, "null pointer argument");
     P3D_REQUIRE(rope->table && rope->pairs && (rope->packed || rope->coords), "bad rope arguments");
     const int ep = 16 / dtype_size(args->dtype);
     P3D_REQUIRE((int64_t)d.N * (args->head_dim / ep) < ((int64_t)1 << 31), "tokens * pieces per row must be below 2^31");
+    P3D_REQUIRE(view_ok(dq, dtype_size(args->dtype)) && view_ok(dkl, dtype_size(args->dtype)),
+                "dq / dkl rows must be 16-byte aligned");
     hipStream_t s = as_stream(stream);
     const RopeDev r = rope_dev(*rope);
     switch (args->dtype) {

@@ -610,7 +610,7 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
 struct PoolBwdDev {
     const float *dsk_part, *dsv_part;
     int splits;
-    char *dkg, *dvg;   // [B, G, N, D] contiguous, storage type
+    p3d_view dkg, dvg;  // [B, G, N, D] views, storage type, 16-byte aligned rows
     float *dw_part;    // [B * G * Mp, D]
     float *db_part;    // [B * G * Mp, V]
 };
@@ -678,8 +678,8 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
         }
         const T* K = reinterpret_cast<const T*>(a.kg) + b * a.ksb + g * a.ksh;
         const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
-        T* DK = reinterpret_cast<T*>(bd.dkg) + bg * a.N * D;
-        T* DV = reinterpret_cast<T*>(bd.dvg) + bg * a.N * D;
+        T* DK = reinterpret_cast<T*>(bd.dkg.data) + b * bd.dkg.sb + g * bd.dkg.sh;
+        T* DV = reinterpret_cast<T*>(bd.dvg.data) + b * bd.dvg.sb + g * bd.dvg.sh;
         for (int f = f0; f < f_end; ++f) {
             const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
             if (__ballot(idx >= 0) == 0) continue;
@@ -754,8 +754,8 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
                         kt[e] = from_f32<T>(dk[e]);
                         vt[e] = from_f32<T>(dv[e]);
                     }
-                    *reinterpret_cast<uint4*>(DK + (int64_t)idx * D + p * EP) = ko;
-                    *reinterpret_cast<uint4*>(DV + (int64_t)idx * D + p * EP) = vo;
+                    *reinterpret_cast<uint4*>(DK + (int64_t)idx * bd.dkg.sn + p * EP) = ko;
+                    *reinterpret_cast<uint4*>(DV + (int64_t)idx * bd.dvg.sn + p * EP) = vo;
                 }
             }
             wave_lds_sync();  // rotated rows and dl / tau are read across lanes below
@@ -1029,12 +1029,15 @@ extern "C" int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, 
 }
 
 extern "C" int p3d_pool_bwd(const p3d_pool_args* args, const float* dsk_part, const float* dsv_part,
-                            int32_t splits, void* dkg, void* dvg, float* dw_part, float* db_part, void* stream) {
+                            int32_t splits, p3d_view dkg, p3d_view dvg, float* dw_part, float* db_part,
+                            void* stream) {
     PoolDev d;
     if (int rc = fill_pool(args, d)) return rc;
-    P3D_REQUIRE(dsk_part && dsv_part && dkg && dvg && dw_part && db_part, "null pointer argument");
+    P3D_REQUIRE(dsk_part && dsv_part && dw_part && db_part, "null pointer argument");
+    P3D_REQUIRE(view_ok(dkg, dtype_size(args->dtype)) && view_ok(dvg, dtype_size(args->dtype)),
+                "dkg / dvg rows must be 16-byte aligned");
     P3D_REQUIRE(splits >= 1, "splits must be positive");
-    PoolBwdDev bd{dsk_part, dsv_part, splits, (char*)dkg, (char*)dvg, dw_part, db_part};
+    PoolBwdDev bd{dsk_part, dsv_part, splits, dkg, dvg, dw_part, db_part};
     const int64_t items = (int64_t)d.B * d.G * d.Mp;
     hipStream_t s = as_stream(stream);
     switch (args->head_dim) {

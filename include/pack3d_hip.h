@@ -261,11 +261,11 @@ int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, in
                      int32_t dim, int32_t dtype, void* stream);
 
 /* Copy of a [batch, heads, tokens, head_dim] tensor between two strided
- * views with contiguous, 16-byte aligned rows: the backward's dense gradients
- * of q, kl, vl, kg, vg into the token-major layout of the layer's to_q /
- * to_kv outputs (attention.py:64-67), so that autograd receives the
- * projections' gradients whole instead of transposing and stacking five
- * views.  batch < 65536. */
+ * views with contiguous, 16-byte aligned rows: a dense gradient of the
+ * backward (the local pass's dvl) into the token-major layout of the layer's
+ * to_kv output (attention.py:64-67), so that autograd receives the
+ * projections' gradients whole instead of transposing and stacking views.
+ * batch < 65536. */
 int p3d_copy_rows(p3d_view src, p3d_view dst, int64_t batch, int32_t heads, int64_t tokens, int32_t head_dim,
                   int32_t dtype, void* stream);
 

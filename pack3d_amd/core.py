@@ -370,7 +370,7 @@ class _Pack3DProjections(torch.autograd.Function):
     gradients returned for qp and kvp directly: the finishing and pooling
     backward kernels write dq, dkl, dkg and dvg straight into the
     projections' layout, and dvl is copied there by p3d_copy_rows, so
-    autograd does not transpose and stack the five views."""
+    autograd does not transpose and stack five views."""
 
     @staticmethod
     def forward(ctx, qp, kvp, weight, bias, gate, sl, sg, heads, kv_heads, geometry, temperature, rope):

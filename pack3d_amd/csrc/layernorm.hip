@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const voi
 template <typename TD, typename TI, typename TO, int PPL>
 __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TD* dres, const TI* x, const void* w,
                                                         int param_dtype, const float* mean_in, const float* rstd_in,
-                                                        TO* dx, float* part, int64_t rows, int dim) {
+                                                        TO* dx, float* part, int64_t rows, int dim, int parts) {
     constexpr int EP = Piece<TI>::N;
     constexpr int GROUPS = 256 / kLanesPerRow;
     __shared__ __align__(16) float lw[kMaxDim];
@@ -255,6 +255,10 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TD* 
         part[((int64_t)blockIdx.x * 2 + 0) * dim + c] = red[0][c];
         part[((int64_t)blockIdx.x * 2 + 1) * dim + c] = red[1][c];
     }
+    // Partial rows past the launched grid hold zeros, so the caller's sum
+    // over all `parts` rows is the same whatever grid ran.
+    for (int q = blockIdx.x + gridDim.x; q < parts; q += gridDim.x)
+        for (int c = threadIdx.x; c < 2 * dim; c += blockDim.x) part[(int64_t)q * 2 * dim + c] = 0.f;
 }
 
 template <typename TI, typename TO>
@@ -280,12 +284,24 @@ template <typename TD, typename TI, typename TO>
 int launch_ln_bwd(const void* dy, const void* dres, const void* x, const void* w, int pdt, const float* mean,
                   const float* rstd, void* dx, float* part, int64_t rows, int dim, int parts, hipStream_t s) {
     const int ppl = (int)cdiv(dim / Piece<TI>::N, kLanesPerRow);
+    // At most one round of resident blocks: the blocks stride over the rows,
+    // and a partly filled second round would leave most of the GPU idle.
+    int dev = 0, cus = 0;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    auto grid_for = [&](const void* kernel) {
+        int per_cu = 0;
+        (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0);
+        const int64_t resident = (int64_t)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
+        return (unsigned)(parts < resident ? parts : resident);
+    };
     switch (ppl) {
 #define CASE(P)                                                                                                  \
     case P:                                                                                                      \
-        k_layer_norm_bwd<TD, TI, TO, P><<<(unsigned)parts, 256, 0, s>>>((const TD*)dy, (const TD*)dres,          \
-                                                                       (const TI*)x, w, pdt, mean, rstd, (TO*)dx, \
-                                                                       part, rows, dim);                        \
+        k_layer_norm_bwd<TD, TI, TO, P>                                                                          \
+            <<<grid_for(reinterpret_cast<const void*>(k_layer_norm_bwd<TD, TI, TO, P>)), 256, 0, s>>>(          \
+                (const TD*)dy, (const TD*)dres, (const TI*)x, w, pdt, mean, rstd, (TO*)dx, part, rows, dim,      \
+                parts);                                                                                          \
         break;
         CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
 #undef CASE

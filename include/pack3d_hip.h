@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 8
+#define P3D_ABI_VERSION 9
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -319,7 +319,7 @@ typedef struct p3d_bwd_args {
     float* dq_local;            /* out: [B,H,N,D] fp32, rotated space */
     float* dq_global;           /* out: [B,H,N,D] fp32, rotated space */
     float* dk_local;            /* out: [B,G,N,D] fp32, rotated space */
-    void* dv_local;             /* out: [B,G,N,D] (dtype) */
+    p3d_view dv_local;          /* out: [B,G,N,D] view (dtype), 16-byte aligned rows */
     float* dsk_part;            /* out: [splits,B,G,Mp,D] fp32, true key units */
     float* dsv_part;            /* out: [splits,B,G,Mp,D] fp32 */
 } p3d_bwd_args;

@@ -22,7 +22,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 8  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 9  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -62,7 +62,7 @@ class BwdArgs(ctypes.Structure):
                 ("dy", View), ("dol", c_void_p), ("dog", c_void_p), ("delta_local", c_void_p),
                 ("delta_global", c_void_p), ("dgate", c_void_p), ("dsl_part", c_void_p), ("dsg_part", c_void_p),
                 ("sv_rows", c_void_p), ("skt", c_void_p), ("dq_local", c_void_p), ("dq_global", c_void_p),
-                ("dk_local", c_void_p), ("dv_local", c_void_p), ("dsk_part", c_void_p), ("dsv_part", c_void_p)]
+                ("dk_local", c_void_p), ("dv_local", View), ("dsk_part", c_void_p), ("dsv_part", c_void_p)]
 
 
 class ProjectArgs(ctypes.Structure):

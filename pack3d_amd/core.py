@@ -268,9 +268,9 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     """The ten gradients of the core (kernels.py:313-356 of amilworks/Pack3D):
     dq, dkl, dkg with respect to the unrotated inputs (the rotation's backward
     is fused), dvl, dvg, dweight, dbias, dgate, dsl, dsg.  `out` may give
-    (dq, dkl, dkg, dvg) as [B, *, N, d] views (16-byte aligned rows) that the
-    kernels write in place, such as column ranges of the projections'
-    gradients; they are returned in their place."""
+    (dq, dkl, dvl, dkg, dvg) as [B, *, N, d] views (16-byte aligned rows)
+    that the kernels write in place, such as column ranges of the
+    projections' gradients; they are returned in their place."""
     b, h, n, d = q.shape
     g = kl.shape[1]
     dev, dt = q.device, _lib.DTYPES[q.dtype]
@@ -302,7 +302,7 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
                 dslp=empty(parts, d, dtype=f32), dsgp=empty(parts, d, dtype=f32),
                 sv_rows=empty(b, g, mp, d), skt=empty(b, g, mp // 32, d, 32),
                 dql=empty(b, h, n, d, dtype=f32), dqg=empty(b, h, n, d, dtype=f32),
-                dkl=empty(b, g, n, d, dtype=f32), dvl=empty(b, g, n, d),
+                dkl=empty(b, g, n, d, dtype=f32),
                 dskp=empty(splits, b, g, mp, d, dtype=f32), dsvp=empty(splits, b, g, mp, d, dtype=f32))
     a = _lib.BwdArgs()
     a.batch, a.heads, a.kv_heads, a.tokens, a.head_dim, a.dtype = b, h, g, n, d, dt
@@ -317,7 +317,11 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     a.dgate, a.dsl_part, a.dsg_part = (bufs[k].data_ptr() for k in ("dgate", "dslp", "dsgp"))
     a.sv_rows, a.skt = bufs["sv_rows"].data_ptr(), bufs["skt"].data_ptr()
     a.dq_local, a.dq_global, a.dk_local = (bufs[k].data_ptr() for k in ("dql", "dqg", "dkl"))
-    a.dv_local, a.dsk_part, a.dsv_part = (bufs[k].data_ptr() for k in ("dvl", "dskp", "dsvp"))
+    if out is None:
+        out = tuple(empty(b, hh, n, d) for hh in (h, g, g, g, g))
+    dq, dkl, dvl, dkg, dvg = out
+    a.dv_local = _lib.view(dvl)
+    a.dsk_part, a.dsv_part = bufs["dskp"].data_ptr(), bufs["dsvp"].data_ptr()
     keep += [qr, klr, gate_k, sl32, sg32, dy]
 
     _lib.call("p3d_mix_bwd", a, stream)
@@ -330,9 +334,6 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
         nb, rev = geometry.neighbors, geometry.reverse_neighbors
         _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)
     _lib.call("p3d_global_bwd", a, stream)
-    if out is None:
-        out = (empty(b, h, n, d), empty(b, g, n, d), empty(b, g, n, d), empty(b, g, n, d))
-    dq, dkl, dkg, dvg = out
     _lib.call("p3d_finish_bwd", a, rope.struct(), _lib.view(dq), _lib.view(dkl), stream)
 
     w32 = param_f32(weight)
@@ -351,7 +352,7 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     dsl = bufs["dslp"].sum(0).to(sl.dtype)
     dsg = bufs["dsgp"].sum(0).to(sg.dtype)
     dgate = bufs["dgate"] if bufs["dgate"].dtype == gate.dtype else bufs["dgate"].to(gate.dtype)
-    return dq, dkl, bufs["dvl"], dkg, dvg, dweight, dbias, dgate, dsl, dsg
+    return dq, dkl, dvl, dkg, dvg, dweight, dbias, dgate, dsl, dsg
 
 
 def _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, pool_rope):
@@ -367,9 +368,8 @@ def _run(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, r
 class _Pack3DProjections(torch.autograd.Function):
     """The core on views of the layer's projections, qp [B, N, H*d] and kvp
     [B, N, 4*G*d] chunked kl | vl | kg | vg (attention.py:64-67), with
-    gradients returned for qp and kvp directly: the finishing and pooling
-    backward kernels write dq, dkl, dkg and dvg straight into the
-    projections' layout, and dvl is copied there by p3d_copy_rows, so
+    gradients returned for qp and kvp directly: the backward kernels write
+    dq, dkl, dvl, dkg and dvg straight into the projections' layout, so
     autograd does not transpose and stack five views."""
 
     @staticmethod
@@ -391,13 +391,8 @@ class _Pack3DProjections(torch.autograd.Function):
         qp, kvp, weight, bias, gate, sl, sg, *state = ctx.saved_tensors
         views = _projection_views(qp, kvp, ctx.heads, ctx.kv_heads)
         dqp, dkvp = torch.empty_like(qp), torch.empty_like(kvp)
-        dq, dkl, dvl, dkg, dvg = _projection_views(dqp, dkvp, ctx.heads, ctx.kv_heads)
         grads = backward(dy, *views, weight, bias, gate, sl, sg, *state, ctx.geometry, ctx.temperature, ctx.rope,
-                         ctx.rope, ctx.key_scale, out=(dq, dkl, dkg, dvg))
-        src = grads[2]  # dvl, dense from the local dK/dV pass
-        b, g, n, d = src.shape
-        _lib.call("p3d_copy_rows", _lib.view(src), _lib.view(dvl), b, g, n, d, _lib.DTYPES[src.dtype],
-                  _lib.stream_of(qp.device))
+                         ctx.rope, ctx.key_scale, out=_projection_views(dqp, dkvp, ctx.heads, ctx.kv_heads))
         return (dqp, dkvp, *grads[5:], None, None, None, None, None)
 
 

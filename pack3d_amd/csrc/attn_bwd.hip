@@ -41,6 +41,7 @@ struct BwdDev {
     char *sv_rows, *skt;
     float *dq_l, *dq_g, *dk_l;
     char* dv_l;
+    int64_t dvsb, dvsh, dvsn;
     float *dsk_part, *dsv_part;
 };
 
@@ -276,7 +277,7 @@ __global__ __launch_bounds__(64) void k_local_dkv(BwdDev a, const int32_t* rev, 
         }
     }
     float* dko = a.dk_l + (bg * a.N + row) * D;
-    T* dvo = reinterpret_cast<T*>(a.dv_l) + (bg * a.N + row) * D;
+    T* dvo = reinterpret_cast<T*>(a.dv_l) + (bg / a.G) * a.dvsb + (bg % a.G) * a.dvsh + row * a.dvsn;
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
         const int c = lane + 64 * cc;
@@ -814,7 +815,7 @@ int fill_bwd(const p3d_bwd_args& x, BwdDev& d) {
     d.dsl_part = x.dsl_part, d.dsg_part = x.dsg_part;
     d.sv_rows = (char*)x.sv_rows, d.skt = (char*)x.skt;
     d.dq_l = x.dq_local, d.dq_g = x.dq_global, d.dk_l = x.dk_local;
-    d.dv_l = (char*)x.dv_local;
+    d.dv_l = (char*)x.dv_local.data, d.dvsb = x.dv_local.sb, d.dvsh = x.dv_local.sh, d.dvsn = x.dv_local.sn;
     d.dsk_part = x.dsk_part, d.dsv_part = x.dsv_part;
     return P3D_OK;
 }
@@ -893,8 +894,8 @@ extern "C" int p3d_local_bwd_indexed(const p3d_bwd_args* args, const int32_t* ne
     P3D_REQUIRE(neighbors && reverse && width >= 1 && width <= 128 && rwidth >= 1 && rwidth <= 128,
                 "neighbour tables must have 1..128 columns");
     P3D_REQUIRE(args->dol && args->lse_local && args->delta_local && args->dq_local && args->dk_local &&
-                    args->dv_local,
-                "null pointer argument");
+                    view_ok(args->dv_local, dtype_size(args->dtype)),
+                "null pointer argument or misaligned dv_local");
     const float scale = 1.f / sqrtf((float)args->head_dim);
     const unsigned qitems = (unsigned)((int64_t)d.B * d.H * d.N);
     const unsigned kitems = (unsigned)((int64_t)d.B * d.G * d.N);

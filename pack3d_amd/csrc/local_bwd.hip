@@ -36,7 +36,8 @@ struct LbDev {
     const int32_t* map;        // raster -> packed row, or null
     float* dq;                 // [B,H,N,D] fp32
     float* dk;                 // [B,G,N,D] fp32
-    char* dv;                  // [B,G,N,D] storage type
+    char* dv;                  // [B,G,N,D] view, storage type
+    int64_t dvsb, dvsh, dvsn;
     float scale_log2, scale;   // log2(e)/sqrt(D), 1/sqrt(D)
 };
 
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dkv_grid(LbDev a) {
     if (!kok) return;
     const int64_t kidx = (int64_t)bg * a.N + krow;
     float* dk = a.dk + kidx * D;
-    T* dv = reinterpret_cast<T*>(a.dv) + kidx * D;
+    T* dv = reinterpret_cast<T*>(a.dv) + b * a.dvsb + kvh * a.dvsh + (int64_t)krow * a.dvsn;
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
@@ -409,7 +410,7 @@ extern "C" int p3d_local_bwd_grid(const p3d_bwd_args* args, const int32_t grid[3
                     radius[2] <= 2,
                 "grid radius must be 0..2 per axis");
     P3D_REQUIRE(view_ok(x.q, es) && view_ok(x.kl, es) && view_ok(x.vl, es), "q/k/v rows must be 16-byte aligned");
-    P3D_REQUIRE(x.dol && x.lse_local && x.delta_local && x.dq_local && x.dk_local && x.dv_local,
+    P3D_REQUIRE(x.dol && x.lse_local && x.delta_local && x.dq_local && x.dk_local && view_ok(x.dv_local, es),
                 "null pointer argument");
     LbDev d{};
     d.B = x.batch, d.H = x.heads, d.G = x.kv_heads, d.N = x.tokens;
@@ -422,7 +423,8 @@ extern "C" int p3d_local_bwd_grid(const p3d_bwd_args* args, const int32_t grid[3
     d.dol = (const char*)x.dol;
     d.lse = x.lse_local, d.delta = x.delta_local;
     d.map = raster_to_packed;
-    d.dq = x.dq_local, d.dk = x.dk_local, d.dv = (char*)x.dv_local;
+    d.dq = x.dq_local, d.dk = x.dk_local, d.dv = (char*)x.dv_local.data;
+    d.dvsb = x.dv_local.sb, d.dvsh = x.dv_local.sh, d.dvsn = x.dv_local.sn;
     d.scale = 1.f / sqrtf((float)x.head_dim);
     d.scale_log2 = kLog2e * d.scale;
     hipStream_t s = as_stream(stream);

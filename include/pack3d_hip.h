@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 9
+#define P3D_ABI_VERSION 10
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -101,6 +101,21 @@ int p3d_repack(const int64_t* perm, int64_t n, const int32_t* neighbors, int32_t
  * order.  scratch[n] is cleared by the call. */
 int p3d_check_layout(const int64_t grid[3], const int64_t* order, const int64_t* coords,
                      int32_t* scratch, int32_t* flags, void* stream);
+
+/* Whether a neighbour table is a complete grid stencil.  The reference tags
+ * only the radius-one stencils that build_layout makes (geometry.py:262-265,
+ * _radius_one_grid) and transports the tag through repack (geometry.py:211-
+ * 217); this call proves the tag for any radius from a layout's order, so a
+ * reference-built layout can take the brick kernels.  It writes
+ * raster_to_packed[t] = packed row of raster index t (-1 when order misses
+ * t) and counts into flags[8] (cleared by the call):
+ *   [0] order entries outside [0, n)
+ *   [1] entries of neighbors [n, width] that differ from the product-order
+ *       stencil of `radius` on `grid` (geometry.py:253-259).
+ * width must equal prod(2 radius + 1).  The caller reads flags back. */
+int p3d_stencil_match(const int64_t grid[3], const int64_t radius[3], const int64_t* order,
+                      const int32_t* neighbors, int32_t width, int32_t* raster_to_packed,
+                      int32_t* flags, void* stream);
 
 /* ---- forward (replaces kernels.py:289-311 and rotary.py:94-106) -------- */
 

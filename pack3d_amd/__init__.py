@@ -7,9 +7,10 @@ backend: ``PACK3DAttention``, ``Pack3DGeometry``, ``TokenLayout``,
 """
 from .attention import PACK3DAttention
 from .core import pack3d_hip, pack3d_hip_rope
-from .geometry import Pack3DGeometry, TokenLayout, build_layout, grid_coordinates, prepare_geometry
+from .geometry import (Pack3DGeometry, TokenLayout, adopt_layout, build_layout, grid_coordinates, grid_tag,
+                       prepare_geometry)
 from .rope import balanced_pairs
 
 __version__ = "0.1.0"
-__all__ = ["PACK3DAttention", "Pack3DGeometry", "TokenLayout", "balanced_pairs", "build_layout",
-           "grid_coordinates", "pack3d_hip", "pack3d_hip_rope", "prepare_geometry"]
+__all__ = ["PACK3DAttention", "Pack3DGeometry", "TokenLayout", "adopt_layout", "balanced_pairs", "build_layout",
+           "grid_coordinates", "grid_tag", "pack3d_hip", "pack3d_hip_rope", "prepare_geometry"]

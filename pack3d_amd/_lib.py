@@ -22,7 +22,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 9  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 10  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -84,6 +84,7 @@ SIGNATURES = {
     "p3d_repack": ([_P, c_int64, _P, c_int32, _P, c_int64, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                     _P, _P], c_int32),
     "p3d_check_layout": ([_P, _P, _P, _P, _P, _P], c_int32),
+    "p3d_stencil_match": ([_P, _P, _P, _P, c_int32, _P, _P, _P], c_int32),
     "p3d_pool_fwd": ([ctypes.POINTER(PoolArgs), _P], c_int32),
     "p3d_attn_fwd_grid": ([ctypes.POINTER(AttnArgs), _P], c_int32),
     "p3d_attn_fwd_rows": ([ctypes.POINTER(AttnArgs), _P], c_int32),

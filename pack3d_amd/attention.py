@@ -170,7 +170,10 @@ class PACK3DAttention(nn.Module):
         elif self._hip_linear(x):
             dt = compute_dtype(x)
             if layer_norm_train_supported(self.norm, x):
-                xn, res = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt, True)
+                if x.dtype == dt:  # the residual copy is the output product's accumulator
+                    xn, res = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt, True)
+                else:
+                    xn = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt)
             else:
                 xn = layer_norm(self.norm, x)
             qp, kvp, gl = InputProjections.apply(xn, self.to_q.weight, self.to_kv.weight, self.gate.weight,
@@ -205,10 +208,16 @@ class PACK3DAttention(nn.Module):
         if fused is not None:
             return fused.view(b, n, self.dim)
         if self._hip_linear(x):
+            dt = compute_dtype(x)
+            if x.dtype != dt:
+                # Autocast over a wider x: the residual keeps x's type and is
+                # not rounded, as in the reference's sum (attention.py:89).
+                return x + OutputResidual.apply(None, o, self.to_out.weight, dt).view(b, n, self.dim)
             if res is not None:  # LayerNormTrain's dt copy of x, owned by this step
-                return OutputResidual.apply(res, o, self.to_out.weight, compute_dtype(x), True).view(b, n, self.dim)
-            return OutputResidual.apply(x.reshape(b * n, self.dim), o, self.to_out.weight,
-                                        compute_dtype(x)).view(b, n, self.dim)
+                return OutputResidual.apply(res, o, self.to_out.weight, dt, True).view(b, n, self.dim)
+            return OutputResidual.apply(x.reshape(b * n, self.dim), o, self.to_out.weight, dt).view(b, n, self.dim)
+        if x.is_cuda and torch.is_autocast_enabled("cuda") and x.dtype != torch.get_autocast_dtype("cuda"):
+            return x + self.to_out(o).view(b, n, self.dim)
         return torch.addmm(x.reshape(b * n, self.dim), o, self.to_out.weight.t()).view(b, n, self.dim)
 
     def _hip_linear(self, x):

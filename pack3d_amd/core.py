@@ -16,6 +16,7 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from . import _lib
+from .geometry import grid_tag
 from .rope import RopeSpec, identity_rope
 
 SUPPORTED_HEAD_DIMS = (16, 32, 48, 64, 128)
@@ -45,6 +46,8 @@ def _validate_inputs(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, te
         raise ValueError("gate or channelwise branch scale shape mismatch")
     if n != geometry.num_tokens:
         raise ValueError("geometry token count does not match Q")
+    if any(t.dtype != torch.int32 or not t.is_contiguous() for t in geometry.tensors):
+        raise ValueError("prepared geometry tables must be contiguous int32; use prepare_geometry()")
     every = (q, kl, vl, kg, vg, weight, bias, gate, sl, sg, *geometry.tensors)
     if any(t.device != q.device for t in every):
         raise ValueError("all tensors and prepared geometry must be on the same device")
@@ -71,10 +74,14 @@ def _kernel_view(t):
     return t if _rows_ok(t) else t.contiguous()
 
 
-def grid_kernel_applies(geometry):
-    """Complete-grid stencils with radius <= 2 per axis take the brick kernel."""
-    grid = geometry._grid
-    return grid is not None and all(r <= 2 for r in grid[1])
+def brick_tag(geometry):
+    """The grid tag (shape, radius, raster_to_packed) when the brick kernels
+    apply: a neighbour table known to be a complete grid stencil of radius
+    at most 2 per axis (``geometry.grid_tag``); else None."""
+    tag = grid_tag(geometry)
+    if tag is None or any(r > 2 for r in tag[1]):
+        return None
+    return tag
 
 
 def param_f32(t):
@@ -153,15 +160,17 @@ class ForwardPlan:
         a.o_global = _lib.ptr(self.saved.get("o_global"))
         a.vl = _lib.view(vl)
         self.attn_args = a
-        self.grid = grid_kernel_applies(geometry)
+        tag = brick_tag(geometry)
+        self.grid = tag is not None
         self.pre = []  # (name, args) launched before the attention kernel
         if self.grid:
-            shape, radius = geometry._grid
+            shape, radius, mapping = tag
             a.q, a.kl = _lib.view(q), _lib.view(kl)
             a.rope = rope.struct()
             a.grid[:] = list(shape)
             a.radius[:] = list(radius)
-            a.raster_to_packed = _lib.ptr(geometry._raster_to_packed)
+            a.raster_to_packed = _lib.ptr(mapping)
+            self._keep.append(mapping)
             self.attn_name = "p3d_attn_fwd_grid"
         else:
             # Arbitrary graph: rotate Q and local K once, indexed local branch
@@ -325,11 +334,11 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     keep += [qr, klr, gate_k, sl32, sg32, dy]
 
     _lib.call("p3d_mix_bwd", a, stream)
-    if grid_kernel_applies(geometry) and not (q.dtype == torch.float32 and d == 128):
+    tag = brick_tag(geometry)
+    if tag is not None and not (q.dtype == torch.float32 and d == 128):
         # Brick-tiled on MFMA; fp32 planes of head_dim 128 do not fit in LDS.
-        shape, radius = geometry._grid
-        _lib.call("p3d_local_bwd_grid", a, _lib.i32x3(shape), _lib.i32x3(radius),
-                  _lib.ptr(geometry._raster_to_packed), stream)
+        shape, radius, mapping = tag
+        _lib.call("p3d_local_bwd_grid", a, _lib.i32x3(shape), _lib.i32x3(radius), _lib.ptr(mapping), stream)
     else:
         nb, rev = geometry.neighbors, geometry.reverse_neighbors
         _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)

@@ -226,9 +226,23 @@ __device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typen
 // softmax reference point, fed to the score MFMA as its initial accumulator.
 // If it is so loose that a query's denominator underflows, the workgroup
 // redoes the sweep with the exact online softmax.
+//
+// The probabilities are rounded to the storage type before the PV product.
+// bf16 keeps fp32's exponent range, so every probability above the
+// underflow check keeps its 8 significant bits, however loose the bound.
+// fp16 does not: below 2^-14 a probability is subnormal and keeps only a few
+// bits, so a bound 14-24 log2 units above the true maximum would degrade
+// every probability of the query.  fp16 therefore takes the running max,
+// which keeps the largest probability of each query in [1, 2^8].
 template <typename C>
 __device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typename C::T_* lds,
                                             const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
+    if constexpr (std::is_same<typename C::T_, _Float16>::value) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) st[nb].reset();
+        global_sweep<C, false>(a, bg, lds, qf, st, lane);
+        return;
+    }
     const float kmax = wave_max(a.sk_norm_max[bg * 64 + lane]);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {

@@ -286,6 +286,45 @@ __global__ void k_check_layout(LayoutDims d, const int64_t* order, const int64_t
     if (coords[3 * i] != z || coords[3 * i + 1] != y || coords[3 * i + 2] != x) atomicAdd(&flags[0], 1);
 }
 
+// ------------------------------------------------------ stencil match
+// raster index -> packed row from a layout's order (order[i] = raster index of
+// row i); entries outside [0, n) are counted in flags[0].
+__global__ void k_scatter_order(const int64_t* order, int64_t n, int32_t* map, int32_t* flags) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t t = order[i];
+    if (t < 0 || t >= n) {
+        atomicAdd(&flags[0], 1);
+        return;
+    }
+    map[t] = (int32_t)i;
+}
+
+// Counts in flags[1] the entries of nb [N, W] that differ from the complete
+// product-order stencil of radius d.r on grid d.g, evaluated at each row's
+// raster coordinate (the table build_layout makes, geometry.py:253-259).
+__global__ void k_compare_stencil(LayoutDims d, int64_t width, const int64_t* order, const int32_t* map,
+                                  const int32_t* nb, int32_t* flags) {
+    int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= d.n * width) return;
+    int64_t i = e / width;
+    int64_t k = e - i * width;
+    int64_t t = order[i];
+    if (t < 0 || t >= d.n) return;  // counted by k_scatter_order
+    int64_t c[3] = {t / (d.g[2] * d.g[1]), (t / d.g[2]) % d.g[1], t % d.g[2]};
+    int64_t wy = 2 * d.r[1] + 1, wx = 2 * d.r[2] + 1;
+    int64_t off[3] = {k / (wy * wx) - d.r[0], (k / wx) % wy - d.r[1], k % wx - d.r[2]};
+    int64_t raster = 0;
+    bool inside = true;
+    for (int a = 0; a < 3; ++a) {
+        int64_t v = c[a] + off[a];
+        inside = inside && v >= 0 && v < d.g[a];
+        raster = raster * d.g[a] + (inside ? v : 0);
+    }
+    int32_t expect = inside ? map[raster] : -1;
+    if (nb[e] != expect) atomicAdd(&flags[1], 1);
+}
+
 }  // namespace
 }  // namespace p3d
 
@@ -392,4 +431,28 @@ extern "C" int p3d_check_layout(const int64_t grid[3], const int64_t* order, con
     k_fill_i32<<<grid1d(d.n), kThreads, 0, s>>>(scratch, d.n, 0);
     k_check_layout<<<grid1d(d.n), kThreads, 0, s>>>(d, order, coords, scratch, flags);
     return check_launch("p3d_check_layout");
+}
+
+extern "C" int p3d_stencil_match(const int64_t grid[3], const int64_t radius[3], const int64_t* order,
+                                 const int32_t* neighbors, int32_t width, int32_t* raster_to_packed,
+                                 int32_t* flags, void* stream) {
+    LayoutDims d{};
+    d.n = 1;
+    int64_t w = 1;
+    for (int a = 0; a < 3; ++a) {
+        P3D_REQUIRE(grid[a] >= 1 && radius[a] >= 0, "invalid grid or radius");
+        d.g[a] = grid[a];
+        d.r[a] = radius[a];
+        d.n *= grid[a];
+        w *= 2 * radius[a] + 1;
+    }
+    P3D_REQUIRE(w == width, "neighbour width does not match the stencil radius");
+    P3D_REQUIRE(d.n * w < ((int64_t)1 << 31), "geometry exceeds the 32-bit kernel indexing limit");
+    P3D_REQUIRE(order && neighbors && raster_to_packed && flags, "null argument");
+    hipStream_t s = as_stream(stream);
+    k_fill_i32<<<1, 64, 0, s>>>(flags, 8, 0);
+    k_fill_i32<<<grid1d(d.n), kThreads, 0, s>>>(raster_to_packed, d.n, -1);
+    k_scatter_order<<<grid1d(d.n), kThreads, 0, s>>>(order, d.n, raster_to_packed, flags);
+    k_compare_stencil<<<grid1d(d.n * w), kThreads, 0, s>>>(d, w, order, raster_to_packed, neighbors, flags);
+    return check_launch("p3d_stencil_match");
 }

@@ -79,6 +79,42 @@ __device__ __forceinline__ int chunk_pos(int wy, int wx, int c, int kappa) {
     return (4 * wy + 4 * c + kappa / 8) * kPlane + 4 * wx + kappa % 8;
 }
 
+// fp16 score gradients can exceed the type's range (65504) while dQ and dK
+// stay finite, e.g. tiny q, k against large v and dO.  In fp16 the dS of a
+// query (dQ kernel) or key (dK kernel) enters the MFMA as dS * 2^-shift, with
+// shift >= 0 raised, lazily and per lane column, until the largest |dS| seen
+// fits below 2^15; the accumulator is rescaled when the shift grows and the
+// result multiplied back by 2^shift.  The lane pair (l, l + 32) holds the
+// same column, so both take the larger of their maxima.  Other types keep
+// shift 0 (bf16 and fp32 have fp32's exponent range).
+template <typename C>
+__device__ __forceinline__ void fit_fp16(float* ds, int& shift, f32x16* acc) {
+    if constexpr (std::is_same<typename C::T_, _Float16>::value) {
+        float tmax = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, fabsf(ds[r]));
+        tmax = fmaxf(tmax, swap_half(tmax));
+        int e;
+        frexpf(tmax, &e);  // tmax < 2^e
+        const int need = e > 15 ? e - 15 : 0;
+        if (__builtin_amdgcn_ballot_w64(need > shift)) {
+            if (need > shift) {
+                const float f = ldexpf(1.f, shift - need);
+#pragma unroll
+                for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[mb][r] *= f;
+                shift = need;
+            }
+        }
+        if (shift) {
+            const float f = ldexpf(1.f, -shift);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds[r] *= f;
+        }
+    }
+}
+
 // Stage one halo plane of two row tensors: rows (stride KSTR) of both and the
 // transposes (stride TPS) of the tensors selected by TRANS_A / TRANS_B.
 // Positions outside the grid or the halo are zero.
@@ -190,6 +226,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dq_grid(LbDev a) {
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
+    int shift = 0;
 
     const T* KL = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
     const T* VL = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
@@ -222,6 +259,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dq_grid(LbDev a) {
                 const bool ok = zok && ((kmask[c] >> r) & 1);
                 ds[r] = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], a.scale_log2, -lse2)) * (dp[r] - delta) : 0.f;
             }
+            fit_fp16<C>(ds, shift, acc);
 #pragma unroll
             for (int ks = 0; ks < C::KSTEPS; ++ks) {
                 const typename C::Frag pf = frag_from_p<T>(ds, ks);
@@ -232,12 +270,13 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dq_grid(LbDev a) {
     }
     if (!qok) return;
     float* dq = a.dq + qidx * D;
+    const float out_scale = ldexpf(a.scale, shift);
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int c = 32 * mb + acc_row(r, g);
-            if (c < D) dq[c] = acc[mb][r] * a.scale;
+            if (c < D) dq[c] = acc[mb][r] * out_scale;
         }
 }
 
@@ -275,6 +314,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dkv_grid(LbDev a) {
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acck[mb][r] = accv[mb][r] = 0.f;
+    int shift = 0;
 
     const uint32_t qmask[2] = {chunk_mask<C>(a, 0, g, ky, kx, Y0 + 4 * wy, X0 + 4 * wx),
                                chunk_mask<C>(a, 1, g, ky, kx, Y0 + 4 * wy, X0 + 4 * wx)};
@@ -328,6 +368,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dkv_grid(LbDev a) {
                     p[r] = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], a.scale_log2, -lse2s[pos])) : 0.f;
                     ds[r] = p[r] * (dp[r] - dlts[pos]);
                 }
+                fit_fp16<C>(ds, shift, acck);
 #pragma unroll
                 for (int ks = 0; ks < C::KSTEPS; ++ks) {
                     const typename C::Frag dsf = frag_from_p<T>(ds, ks);
@@ -345,13 +386,14 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dkv_grid(LbDev a) {
     const int64_t kidx = (int64_t)bg * a.N + krow;
     float* dk = a.dk + kidx * D;
     T* dv = reinterpret_cast<T*>(a.dv) + b * a.dvsb + kvh * a.dvsh + (int64_t)krow * a.dvsn;
+    const float out_scale = ldexpf(a.scale, shift);
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int c = 32 * mb + acc_row(r, g);
             if (c < D) {
-                dk[c] = acck[mb][r] * a.scale;
+                dk[c] = acck[mb][r] * out_scale;
                 dv[c] = from_f32<T>(accv[mb][r]);
             }
         }

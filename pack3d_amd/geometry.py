@@ -16,7 +16,9 @@ on a HIP device; ``.to("cpu")`` copies it out for inspection.
 """
 from __future__ import annotations
 
+import itertools
 import math
+import weakref
 from dataclasses import dataclass, field, replace
 
 import torch
@@ -341,3 +343,94 @@ def build_layout(grid_shape, block_shape=(2, 2, 2), *, radius=1, pool_size=4,
     geom = Pack3DGeometry(nb, _reverse(nb, rwidth), blocks, pool_size, n, _SEAL,
                           _grid=(shape, rad), _raster_to_packed=mapping)
     return TokenLayout(shape, order, coords, geom, _SEAL)
+
+
+# Brick tags proven for geometry objects that do not carry one (the
+# reference's Pack3DGeometry): id(geometry) -> (weak reference, tensor
+# versions at proof time, tag).  An entry dies with its geometry.
+_TAGS = {}
+
+
+def _remember(geometry, tag):
+    key = id(geometry)
+    try:
+        ref = weakref.ref(geometry, lambda _r, key=key: _TAGS.pop(key, None))
+    except TypeError:
+        return
+    _TAGS[key] = (ref, _versions_of(geometry.tensors), tag)
+
+
+def _map_for(mapping, like):
+    """A raster->packed map as a contiguous int32 tensor on ``like``'s device."""
+    if mapping is None:
+        return None
+    if mapping.dtype == torch.int32 and mapping.device == like.device and mapping.is_contiguous():
+        return mapping
+    return mapping.to(device=like.device, dtype=torch.int32).contiguous()
+
+
+def grid_tag(geometry):
+    """``(grid_shape, radius, raster_to_packed)`` when the geometry's neighbour
+    table is known to be the complete product-order stencil of ``radius`` on
+    ``grid_shape`` (raster_to_packed None = identity); else None.
+
+    Three sources, in order: the tag this package's ``build_layout`` and
+    ``repack`` attach (``_grid``); a tag proven by ``adopt_layout``; the
+    reference's radius-one tag ``_radius_one_grid`` with its
+    ``_raster_to_packed`` map (geometry.py:18-19,262-265), which the
+    reference's ``build_layout`` sets and its ``repack`` transports.
+    """
+    grid = getattr(geometry, "_grid", None)
+    if grid is not None:
+        return tuple(grid[0]), tuple(grid[1]), geometry._raster_to_packed
+    hit = _TAGS.get(id(geometry))
+    if hit is not None and hit[0]() is geometry and hit[1] == _versions_of(geometry.tensors):
+        return hit[2]
+    shape = getattr(geometry, "_radius_one_grid", None)
+    if shape is not None:
+        mapping = getattr(geometry, "_raster_to_packed", None)
+        tag = (tuple(int(v) for v in shape), (1, 1, 1), _map_for(mapping, geometry.neighbors))
+        if tag[2] is not mapping:
+            _remember(geometry, tag)  # keeps the converted map alive with the geometry
+        return tag
+    return None
+
+
+def _stencil_radii(width):
+    """Per-axis radii of at most 2 whose product-order stencil has ``width`` columns."""
+    return [r for r in itertools.product(range(3), repeat=3) if math.prod(2 * v + 1 for v in r) == width]
+
+
+@torch.inference_mode(False)
+def adopt_layout(layout):
+    """Prove on the GPU that ``layout.geometry``'s neighbour table is the
+    complete grid stencil of some radius (at most 2 per axis) for the layout's
+    token order, and record that tag for the geometry object, so that the
+    brick kernels take it.  Works for any object with the reference
+    TokenLayout's fields (``grid_shape``, ``order``, ``geometry`` with
+    ``neighbors``); a table that is not such a stencil gets no tag and keeps
+    the indexed kernels.  Returns ``layout``.  Costs one comparison pass over
+    the table and one small read-back per candidate radius, once per
+    geometry object."""
+    geom = layout.geometry
+    if grid_tag(geom) is not None:
+        return layout
+    nb = geom.neighbors
+    if nb.device.type != "cuda" or nb.dtype != torch.int32 or not nb.is_contiguous():
+        return layout
+    shape = _triple(tuple(int(v) for v in layout.grid_shape), "grid_shape")
+    n = math.prod(shape)
+    if n != nb.shape[0]:
+        return layout
+    order = layout.order.to(device=nb.device, dtype=torch.int64).contiguous()
+    mapping = torch.empty(n, dtype=torch.int32, device=nb.device)
+    flags = torch.empty(8, dtype=torch.int32, device=nb.device)
+    for radius in _stencil_radii(nb.shape[1]):
+        _lib.call("p3d_stencil_match", _lib.i64x3(shape), _lib.i64x3(radius), order.data_ptr(), nb.data_ptr(),
+                  nb.shape[1], mapping.data_ptr(), flags.data_ptr(), _lib.stream_of(nb.device))
+        f = _flags(flags)
+        if f[0] == 0 and f[1] == 0:
+            identity = torch.equal(mapping, torch.arange(n, dtype=torch.int32, device=nb.device))
+            _remember(geom, (shape, radius, None if identity else mapping))
+            break
+    return layout

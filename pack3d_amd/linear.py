@@ -185,26 +185,32 @@ class InputProjections(torch.autograd.Function):
 
 
 class OutputResidual(torch.autograd.Function):
-    """x + y Wo^T in the 16-bit type dt (attention.py:89; autocast's
-    torch.addmm): x [rows, dim], y [rows, k].  The product accumulates into
-    the residual in place: into x itself when the caller owns it (x_owned:
-    x is already a dt copy, such as the one LayerNormTrain returns; it is
-    marked dirty and returned), else into a dt copy of x (addmm with a full
-    matrix would copy it into a new result first).  The backward gives
-    dx = dout (in x's dtype), dy = dout Wo and an fp32 weight gradient."""
+    """x + y Wo^T in the 16-bit type dt (attention.py:89 with a 16-bit x):
+    x [rows, dim], y [rows, k].  The product accumulates into the residual in
+    place: into x itself when the caller owns it (x_owned: x is already a dt
+    copy, such as the one LayerNormTrain returns; it is marked dirty and
+    returned), else into a dt copy of x (addmm with a full matrix would copy
+    it into a new result first).  With x None it returns the product y Wo^T
+    alone, rounded to dt: the caller adds a residual of a wider type itself,
+    as the reference's ``residual + to_out(...)`` does under autocast.  The
+    backward gives dx = dout (in x's dtype), dy = dout Wo and an fp32 weight
+    gradient."""
 
     @staticmethod
     def forward(ctx, x, y, wo, dt, x_owned=False):
         y16 = y.to(dt).contiguous()
         wo16 = wo.to(dt)
-        if x_owned and x.dtype == dt and x.dim() == 2 and x.is_contiguous():
+        if x is None:
+            out = torch.mm(y16, wo16.t())
+        elif x_owned and x.dtype == dt and x.dim() == 2 and x.is_contiguous():
             ctx.mark_dirty(x)
             out = x
+            out.addmm_(y16, wo16.t())
         else:
             out = x.to(dt, copy=True)
-        out.addmm_(y16, wo16.t())
+            out.addmm_(y16, wo16.t())
         ctx.save_for_backward(y16, wo16)
-        ctx.meta = (x.dtype, y.dtype, wo.dtype)
+        ctx.meta = (None if x is None else x.dtype, y.dtype, wo.dtype)
         return out
 
     @staticmethod
@@ -213,4 +219,5 @@ class OutputResidual(torch.autograd.Function):
         x_dt, y_dt, wo_dt = ctx.meta
         d16 = dout.to(y16.dtype)
         dy = torch.mm(d16, wo16).to(y_dt)
-        return dout.to(x_dt), dy, weight_grad(d16, y16).to(wo_dt), None, None
+        dx = None if x_dt is None else dout.to(x_dt)
+        return dx, dy, weight_grad(d16, y16).to(wo_dt), None, None

@@ -165,3 +165,36 @@ def test_copy_rows_into_projection_layout(gpu, dtype):
     assert torch.equal(view, src)
     others = dst[:, :, [0, 1, 3]]
     assert torch.equal(others, torch.full_like(others, 7.0))
+
+
+@pytest.mark.parametrize("grad", [True, False])
+def test_layer_autocast_keeps_the_wide_residual(gpu, grad):
+    """Under autocast with an fp32 input the reference returns
+    ``residual + to_out(...)`` in fp32 with the residual unrounded
+    (attention.py:89).  Inputs of scale 4 make a bf16-rounded residual miss
+    the bound by a factor of ~3 while the bf16 attention branch stays inside."""
+    import oracle.pack3d_oracle as ref
+    from tests._cases import max_abs
+    print(f"layer autocast residual grad={grad}", flush=True)
+    torch.manual_seed(0)
+    shape = (8, 16, 12)
+    n = math.prod(shape)
+    oracle = ref.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    layer.load_state_dict(oracle.state_dict())
+    layer = layer.to(gpu)
+    lay_h = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block", device=gpu)
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1)) * 4
+    xg = x.to(gpu).requires_grad_(grad)
+    with torch.set_grad_enabled(grad), torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(xg, lay_h)
+    with torch.no_grad():
+        exp = oracle(x, lay_r)
+    assert y.dtype == torch.float32
+    m = max_abs(y.detach(), exp)
+    print(f"  max_abs={m:.3g}", flush=True)
+    assert m < 1e-2
+    if grad:
+        y.backward(torch.ones_like(y))
+        assert xg.grad.dtype == torch.float32 and torch.isfinite(xg.grad).all()

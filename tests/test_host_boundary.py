@@ -148,3 +148,34 @@ def test_param_f32_cache_follows_updates():
     assert b is not a and torch.equal(b, p.detach().float())  # in-place update: a fresh copy
     q = torch.arange(4, dtype=torch.float32)
     assert param_f32(q).data_ptr() == q.data_ptr()  # fp32 contiguous: no copy
+
+
+def test_grid_tag_reads_the_reference_radius_one_tag():
+    """A geometry shaped like the reference's (no ``_grid``): its radius-one tag
+    (geometry.py:18-19,262-265) selects the brick kernels; other radii carry no
+    tag until adopt_layout proves one."""
+    import oracle.pack3d_oracle as ref
+    from pack3d_amd.geometry import _stencil_radii, grid_tag
+    from tests._refobjects import reference_layout
+    lay = reference_layout(ref.build_layout((4, 16, 64), (2, 2, 2), radius=1, pool_size=2))
+    tag = grid_tag(lay.geometry)
+    assert tag[0] == (4, 16, 64) and tag[1] == (1, 1, 1)
+    assert tag[2].dtype == torch.int32 and torch.equal(tag[2], lay.order.argsort().to(torch.int32))
+    raster = reference_layout(ref.build_layout((4, 16, 64), (2, 2, 2), radius=1, layout="raster_block"))
+    assert grid_tag(raster.geometry) == ((4, 16, 64), (1, 1, 1), None)
+    assert grid_tag(reference_layout(ref.build_layout((8, 8, 8), (4, 4, 4), radius=2)).geometry) is None
+    assert grid_tag(reference_layout(ref.build_layout((2, 4, 4), (2, 2, 2), radius=1)).geometry) is None
+    assert _stencil_radii(125) == [(2, 2, 2)]
+    assert sorted(_stencil_radii(45)) == [(1, 1, 2), (1, 2, 1), (2, 1, 1)]
+
+
+def test_core_rejects_geometry_tables_that_are_not_int32():
+    import oracle.pack3d_oracle as ref
+    from pack3d_amd import pack3d_hip
+    from tests._cases import make_case
+    from tests._refobjects import RefGeometry
+    inputs, nb, blocks, pool = make_case()
+    g = ref.prepare_geometry(nb, blocks, pool)
+    wide = RefGeometry(g.neighbors.long(), g.reverse_neighbors, g.blocks, g.pool_size, g.num_tokens)
+    with pytest.raises(ValueError, match="int32"):
+        pack3d_hip(*inputs, wide)

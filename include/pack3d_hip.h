@@ -188,6 +188,22 @@ typedef struct p3d_attn_args {
 int p3d_attn_fwd_grid(const p3d_attn_args* args, void* stream);
 int p3d_attn_fwd_rows(const p3d_attn_args* args, void* stream);
 
+/* p3d_pool_fwd followed by p3d_attn_fwd_grid, allocating nothing.  No
+ * counterpart in the reference: it serves callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The pooled summaries and the norm
+ * slots -- the forward's only memory beyond its inputs and outputs -- live
+ * in a file-scope device array of 8 MiB that each GPU holds until the
+ * process ends; the sk, svt, sk_norm_max and norms_cleared fields of both
+ * argument blocks are ignored.  The summaries must fit: 2 *
+ * round256(B * G * ceil32(M) * D * element size) + round256(B * G * 256)
+ * bytes <= 8 MiB (c2 in bf16 needs 3.2 MB), else P3D_EINVAL before any
+ * launch.  Every call on a GPU uses that GPU's one array, so calls that
+ * overlap on one GPU race; the stream must belong to the current device.
+ * The two argument blocks must agree on batch, kv_heads, tokens, head_dim,
+ * dtype and summaries. */
+int p3d_attn_fwd_grid_noalloc(const p3d_pool_args* pool, const p3d_attn_args* args, void* stream);
+
 /* Indexed local attention for arbitrary validated graphs (reference.py:23-30,
  * kernels.py:43-66).  q and kl must already be rotated (rope identity) or are
  * rotated with args->rope.  Writes fp32 o_local [B,H,N,D] and, if non-NULL,

@@ -88,6 +88,7 @@ SIGNATURES = {
     "p3d_pool_fwd": ([ctypes.POINTER(PoolArgs), _P], c_int32),
     "p3d_attn_fwd_grid": ([ctypes.POINTER(AttnArgs), _P], c_int32),
     "p3d_attn_fwd_rows": ([ctypes.POINTER(AttnArgs), _P], c_int32),
+    "p3d_attn_fwd_grid_noalloc": ([ctypes.POINTER(PoolArgs), ctypes.POINTER(AttnArgs), _P], c_int32),
     "p3d_local_fwd_indexed": ([ctypes.POINTER(AttnArgs), _P, c_int32, _P, _P], c_int32),
     "p3d_selftest_mfma": ([c_int32, _P, _P, _P, _P], c_int32),
     "p3d_struct_sizes": ([_P], c_int32),

@@ -43,6 +43,36 @@ def validate_inputs(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, tem
         raise ValueError("temperature must be finite and positive")
 
 
+def _rows_branches(qf, klr, vlr, sk, sv, nb, r, root):
+    """(o_L, o_G) of query rows r: reference.py:20-30 on one chunk of rows.
+
+    qf [B, H, N, d]; klr, vlr, sk, sv already repeated to the H query heads.
+    Global: softmax over all summaries of q.sk/sqrt(d), times sv.  Local:
+    softmax over the valid entries of the neighbour row, times v; an
+    all-masked row gives 0.
+    """
+    qc = qf[:, :, r]
+    og = ((qc @ sk.transpose(-1, -2)) / root).softmax(-1) @ sv
+    idx = nb[r]
+    ok = idx >= 0
+    safe = idx.clamp_min(0)
+    lk, lv = klr[:, :, safe], vlr[:, :, safe]          # [B, H, c, W, d]
+    s = (qc[..., None, :] * lk).sum(-1) / root
+    s = s.masked_fill(~ok, -torch.inf)
+    s = torch.where(ok.any(-1)[None, None, :, None], s, torch.zeros_like(s))
+    p = s.softmax(-1) * ok
+    ol = (p[..., None] * lv).sum(-2)
+    return ol, og
+
+
+def _prepared(q, kl, vl, kg, vg, weight, bias, geometry, temperature, work):
+    g, h = kl.shape[1], q.shape[1]
+    rep = h // g
+    qf, klf, vlf, kgf, vgf = (t.to(work) for t in (q, kl, vl, kg, vg))
+    sk, sv = compress_summaries(kgf, vgf, weight, bias, geometry, temperature=temperature)
+    return qf, klf.repeat_interleave(rep, 1), vlf.repeat_interleave(rep, 1), sk, sv, rep
+
+
 def pack3d_reference(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, *,
                      temperature=1.0, rows=None, chunk=2048, return_branches=False):
     """``y = sl * o_L + gate * sg * o_G`` in fp32 (fp64 for fp64), cast to q.dtype.
@@ -57,14 +87,10 @@ def pack3d_reference(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, *,
     in the working precision.
     """
     validate_inputs(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature)
-    b, h, n, d = q.shape
-    g = kl.shape[1]
-    rep = h // g
+    n, d = q.shape[2], q.shape[3]
     work = torch.float64 if q.dtype == torch.float64 else torch.float32
-    qf, klf, vlf, kgf, vgf = (t.to(work) for t in (q, kl, vl, kg, vg))
-    sk, sv = compress_summaries(kgf, vgf, weight, bias, geometry, temperature=temperature)
+    qf, klr, vlr, sk, sv, rep = _prepared(q, kl, vl, kg, vg, weight, bias, geometry, temperature, work)
     sk, sv = sk.repeat_interleave(rep, 1), sv.repeat_interleave(rep, 1)
-    klr, vlr = klf.repeat_interleave(rep, 1), vlf.repeat_interleave(rep, 1)
     nb = geometry.neighbors.long()
     if rows is None:
         rows = torch.arange(n)
@@ -72,20 +98,67 @@ def pack3d_reference(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, *,
     root = math.sqrt(d)
     ol_parts, og_parts = [], []
     for start in range(0, rows.numel(), chunk):
-        r = rows[start:start + chunk]
-        qc = qf[:, :, r]
-        og_parts.append(((qc @ sk.transpose(-1, -2)) / root).softmax(-1) @ sv)
-        idx = nb[r]
-        ok = idx >= 0
-        safe = idx.clamp_min(0)
-        lk, lv = klr[:, :, safe], vlr[:, :, safe]          # [B, H, c, W, d]
-        s = (qc[..., None, :] * lk).sum(-1) / root
-        s = s.masked_fill(~ok, -torch.inf)
-        s = torch.where(ok.any(-1)[None, None, :, None], s, torch.zeros_like(s))
-        p = s.softmax(-1) * ok
-        ol_parts.append((p[..., None] * lv).sum(-2))
+        ol, og = _rows_branches(qf, klr, vlr, sk, sv, nb, rows[start:start + chunk], root)
+        ol_parts.append(ol)
+        og_parts.append(og)
     ol = torch.cat(ol_parts, 2)
     og = torch.cat(og_parts, 2)
     gr = gate.to(work)[:, :, rows]
     y = (sl.to(work) * ol + gr[..., None] * sg.to(work) * og).to(q.dtype)
     return (y, ol, og) if return_branches else y
+
+
+def pack3d_reference_grads(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, dy, *,
+                           temperature=1.0, chunk=2048):
+    """The ten input gradients of ``pack3d_reference`` for the upstream
+    gradient ``dy`` (the reference's autograd of reference.py:16-31), each in
+    its input's dtype, evaluated so that no autograd graph spans more than
+    one chunk of query rows.  The summaries are computed once.  Each chunk
+    differentiates the same ``_rows_branches`` math on leaf copies of the
+    rows it touches -- its queries and gates, the neighbours it gathers
+    (remapped to a local table), the summaries -- and the leaves' gradients
+    are added into full-size accumulators; the summaries' gradients then go
+    through the pooling's graph once.  The same values as
+    ``torch.autograd.grad`` of ``pack3d_reference`` (up to summation order),
+    at the memory cost of one chunk, so it runs at 262,144 tokens.
+    """
+    validate_inputs(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature)
+    n, d = q.shape[2], q.shape[3]
+    work = torch.float64 if q.dtype == torch.float64 else torch.float32
+    inputs = (q, kl, vl, kg, vg, weight, bias, gate, sl, sg)
+    qf, klf, vlf, kgf, vgf, w, b, gt, slf, sgf = (t.detach().to(work) for t in inputs)
+    pooled = [t.requires_grad_() for t in (kgf, vgf, w, b)]
+    slf.requires_grad_()
+    sgf.requires_grad_()
+    dq, dkl, dvl, dgate = (torch.zeros_like(t) for t in (qf, klf, vlf, gt))
+    nb = geometry.neighbors.long()
+    root = math.sqrt(d)
+    dyw = dy.detach().to(work)
+    with torch.enable_grad():
+        sk, sv = compress_summaries(*pooled, geometry, temperature=temperature)
+        rep = q.shape[1] // kl.shape[1]
+        sk_leaf, sv_leaf = sk.detach().requires_grad_(), sv.detach().requires_grad_()
+        skr, svr = sk_leaf.repeat_interleave(rep, 1), sv_leaf.repeat_interleave(rep, 1)
+        for start in range(0, n, chunk):
+            r = torch.arange(start, min(n, start + chunk))
+            idx = nb[r]
+            ok = idx >= 0
+            uniq, inv = torch.unique(idx.clamp_min(0), return_inverse=True)
+            local_nb = torch.where(ok, inv, -1)
+            qc = qf[:, :, r].requires_grad_()
+            gc = gt[:, :, r].requires_grad_()
+            kc = klf[:, :, uniq].requires_grad_()
+            vc = vlf[:, :, uniq].requires_grad_()
+            ol, og = _rows_branches(qc, kc.repeat_interleave(rep, 1), vc.repeat_interleave(rep, 1), skr, svr,
+                                    local_nb, torch.arange(r.numel()), root)
+            y = slf * ol + gc[..., None] * sgf * og
+            # The summary repeat nodes are shared by every chunk's graph.
+            torch.autograd.backward(y, dyw[:, :, r], retain_graph=start + chunk < n)
+            dq[:, :, r] = qc.grad
+            dgate[:, :, r] = gc.grad
+            dkl.index_add_(2, uniq, kc.grad)
+            dvl.index_add_(2, uniq, vc.grad)
+        torch.autograd.backward([sk, sv], [sk_leaf.grad, sv_leaf.grad])
+    grads = (dq, dkl, dvl, pooled[0].grad, pooled[1].grad, pooled[2].grad, pooled[3].grad, dgate, slf.grad,
+             sgf.grad)
+    return [g.to(t.dtype) for g, t in zip(grads, inputs)]

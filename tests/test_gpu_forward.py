@@ -97,6 +97,10 @@ def test_core_rope_fused(gpu, dtype, kind):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_layer_matches_oracle(gpu, dtype):
+    """The whole layer (LayerNorm, projections, gate, core, to_out, residual)
+    against the oracle layer in fp32 on the same (rounded) weights and input.
+    fp32: assert_close 2e-5.  bf16: max-abs <= 2e-2 plus the output's own
+    rounding (half an ulp of |y|, 2^-8 |y| in bf16)."""
     print(f"layer {dtype}", flush=True)
     torch.manual_seed(0)
     shape = (16, 16, 16) if dtype == torch.float32 else (8, 16, 16)
@@ -104,17 +108,19 @@ def test_layer_matches_oracle(gpu, dtype):
     layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
     layer.load_state_dict(oracle.state_dict())
     layer = layer.to(gpu, dtype)
-    oracle = oracle.to(dtype)
+    oracle = oracle.to(dtype).float()
     lay_h = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
     lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
     x = torch.randn(1, math.prod(shape), 192, generator=torch.Generator().manual_seed(1)).to(dtype)
     with torch.no_grad():
-        got = layer(x.to(gpu), lay_h)
-        exp = oracle(x, lay_r)
-    # Compare the attention branch (the residual is added exactly by both).
+        got = layer(x.to(gpu), lay_h).float().cpu()
+        exp = oracle(x.float(), lay_r)
     if dtype == torch.float32:
-        torch.testing.assert_close(got.cpu(), exp, atol=2e-5, rtol=2e-5)
-    assert rel_l2(got.float().cpu() - x.float(), exp.float() - x.float()) < REL[dtype] * 2
+        torch.testing.assert_close(got, exp, atol=2e-5, rtol=2e-5)
+    else:
+        excess = float(((got - exp).abs() - 2 ** -8 * exp.abs()).max())
+        print(f"  max_abs={max_abs(got, exp):.3g} beyond rounding={excess:.3g}", flush=True)
+        assert excess <= 2e-2
 
 
 def test_repack_permutes_outputs_exactly(gpu):
@@ -151,56 +157,61 @@ def _xavier_layer(shape, batch, dtype, gpu):
     return layer.to(gpu, dtype), x.to(gpu, dtype)
 
 
-def _core_sampled_vs_oracle(layer, x, lay, shape, kind, dtype, what, nrows=1024):
-    """Core output of the layer at full size; 1024 random rows plus corner rows
-    are compared with the oracle evaluated on those rows only."""
+def _oracle_y32(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, coords):
+    """The oracle core on every row, rotating q, kl, kg like the reference,
+    with y = sl o_L + gate sg o_G kept in fp32 (the oracle's own output is
+    rounded to the storage type, which would add a second rounding)."""
+    rot = [ref.axial_rope(t, coords) if i in (0, 1, 3) else t for i, t in enumerate((q, kl, vl, kg, vg))]
+    _, ol, og = ref.pack3d_reference(*rot, weight, bias, gate, sl, sg, geometry, chunk=4096,
+                                     return_branches=True)
+    return sl.float() * ol + gate.float()[..., None] * sg.float() * og
+
+
+def _core_vs_oracle(layer, x, lay, shape, kind, dtype, what):
+    """Core output of the layer at full size against the oracle on every row:
+    max-abs <= the dtype's bar and relative L2 below the reference's."""
     with torch.no_grad():
         core = layer.core_inputs(x, lay)
         q, kl, vl, kg, vg, gate, rope = core
         y = p3d.pack3d_hip_rope(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate,
                                 layer.local_scale, layer.global_scale, lay.geometry, rope)
-    n = math.prod(shape)
-    rows = torch.randperm(n, generator=torch.Generator().manual_seed(2))[:nrows]
-    rows = torch.cat((rows, torch.tensor([0, n - 1, shape[2] - 1, shape[1] * shape[2] - 1])))
     lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout=kind)
-    cpu = [t.cpu() for t in (q, kl, vl, kg, vg)]
-    rot = [ref.axial_rope(t, lay_r.coords) if i in (0, 1, 3) else t for i, t in enumerate(cpu)]
     params = [t.detach().cpu() for t in (layer.pool_weight, layer.slot_bias)]
-    exp = ref.pack3d_reference(*rot, *params, gate.cpu(), layer.local_scale.detach().cpu(),
-                               layer.global_scale.detach().cpu(), lay_r.geometry, rows=rows, chunk=512)
-    _check(y[:, :, rows.to(y.device)], exp, dtype, what)
+    exp = _oracle_y32(*(t.cpu() for t in (q, kl, vl, kg, vg)), *params, gate.cpu(), layer.local_scale.detach().cpu(),
+                      layer.global_scale.detach().cpu(), lay_r.geometry, lay_r.coords)
+    _check(y, exp, dtype, what)
     return y, core
 
 
-def test_full_size_headline_sampled(gpu):
-    """c2: 64^3 bf16, batch 1, raster: sampled rows vs the oracle."""
-    print("full size c2 sampled", flush=True)
+def test_full_size_headline(gpu):
+    """c2: 64^3 bf16, batch 1, raster: every row against the oracle."""
+    print("full size c2", flush=True)
     shape = (64, 64, 64)
     layer, x = _xavier_layer(shape, 1, torch.bfloat16, gpu)
     lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
-    _core_sampled_vs_oracle(layer, x, lay, shape, "raster_block", torch.bfloat16, "c2 sampled y")
+    _core_vs_oracle(layer, x, lay, shape, "raster_block", torch.bfloat16, "c2 y")
 
 
-def test_full_size_c1_sampled(gpu):
-    """c1: 16 x 64 x 64 bf16, batch 2, raster: sampled rows vs the oracle."""
-    print("full size c1 sampled", flush=True)
+def test_full_size_c1(gpu):
+    """c1: 16 x 64 x 64 bf16, batch 2, raster: every row against the oracle."""
+    print("full size c1", flush=True)
     shape = (16, 64, 64)
     layer, x = _xavier_layer(shape, 2, torch.bfloat16, gpu)
     lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
-    _core_sampled_vs_oracle(layer, x, lay, shape, "raster_block", torch.bfloat16, "c1 sampled y")
+    _core_vs_oracle(layer, x, lay, shape, "raster_block", torch.bfloat16, "c1 y")
 
 
 def test_full_size_c3_morton_repack(gpu):
-    """c3: 64^3 fp16 in Morton order: sampled rows vs the oracle, then a seeded
-    pure repack (block permutation + slot shuffle) must permute the core
-    output bit for bit."""
+    """c3: 64^3 fp16 in Morton order: every row against the oracle, then a
+    seeded pure repack (block permutation + slot shuffle) must permute the
+    core output bit for bit."""
     print("full size c3 morton + repack", flush=True)
     shape = (64, 64, 64)
     n = math.prod(shape)
     layer, x = _xavier_layer(shape, 1, torch.float16, gpu)
     lay = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="native_block_morton")
-    y, (q, kl, vl, kg, vg, gate, _) = _core_sampled_vs_oracle(layer, x, lay, shape, "native_block_morton",
-                                                              torch.float16, "c3 sampled y")
+    y, (q, kl, vl, kg, vg, gate, _) = _core_vs_oracle(layer, x, lay, shape, "native_block_morton",
+                                                      torch.float16, "c3 y")
     gen = torch.Generator().manual_seed(3)
     fine = n // 64
     slots = torch.argsort(torch.rand(fine, 64, generator=gen), dim=1)

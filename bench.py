@@ -113,11 +113,9 @@ def summary_pathway_ms(plan, steps, stream):
     the summary pathway's cost plus that extra read (4 B x H x N x d).
     """
     from pack3d_amd import _lib
-    from pack3d_amd.core import ctypes_copy
 
     a = plan.attn_args
-    rows = _lib.AttnArgs()
-    ctypes_copy(rows, a)
+    rows = _lib.AttnArgs.from_buffer_copy(a)
     o_local = torch.zeros(a.batch * a.heads * a.tokens * a.head_dim, dtype=torch.float32, device=plan.device)
     rows.o_local_in = o_local.data_ptr()
     rows.lse_local = None

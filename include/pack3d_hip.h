@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 10
+#define P3D_ABI_VERSION 11
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -160,8 +160,9 @@ int p3d_pool_fwd(const p3d_pool_args* args, void* stream);
  *   reads the radius (<= 2 per axis) stencil from an LDS halo, so the
  *   neighbour table is not read.  raster_to_packed may be NULL (identity).
  * p3d_attn_fwd_rows: any validated geometry.  Queries are tiled by packed
- *   rows; o_local (fp32 [B,H,N,D], from p3d_local_fwd_indexed) supplies the
- *   local branch. */
+ *   rows; the local branch is y itself when o_local_in is NULL (y holds
+ *   sl * o_L from p3d_local_fwd_indexed), else o_local_in (fp32 [B,H,N,D],
+ *   contiguous). */
 typedef struct p3d_attn_args {
     int32_t batch, heads, kv_heads, tokens, head_dim, dtype;
     int32_t summaries;          /* M */
@@ -204,12 +205,15 @@ int p3d_attn_fwd_rows(const p3d_attn_args* args, void* stream);
  * dtype and summaries. */
 int p3d_attn_fwd_grid_noalloc(const p3d_pool_args* pool, const p3d_attn_args* args, void* stream);
 
-/* Indexed local attention for arbitrary validated graphs (reference.py:23-30,
- * kernels.py:43-66).  q and kl must already be rotated (rope identity) or are
- * rotated with args->rope.  Writes fp32 o_local [B,H,N,D] and, if non-NULL,
- * lse_local [B,H,N].  An all-masked row gives 0 and lse = -inf. */
-int p3d_local_fwd_indexed(const p3d_attn_args* args, const int32_t* neighbors, int32_t width,
-                          float* o_local, void* stream);
+/* Indexed local attention for arbitrary validated graphs (reference.py:23-30;
+ * replaces the reference's _local_fwd, kernels.py:43-66), neighbours
+ * neighbors [N, width], -1 = absent.  q is rotated on load with args->rope
+ * (identity for pre-rotated q); kl must already be rotated.  Writes
+ * y = sl * o_L in the storage type (the rows kernel's epilogue then adds the
+ * global branch, with o_local_in NULL) and, if non-NULL, o_local [B,H,N,D]
+ * in the storage type and lse_local [B,H,N].  An all-masked row gives 0 and
+ * lse = -inf.  The sk / svt / norm fields of args are not read. */
+int p3d_local_fwd_indexed(const p3d_attn_args* args, const int32_t* neighbors, int32_t width, void* stream);
 
 /* Standalone rotation (rotary.py:10-45): y = R(pos) x, or R(pos)^T x when
  * inverse != 0, for x and y [B, H, N, D] views of dtype; D in {16, 32, 48,

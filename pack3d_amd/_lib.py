@@ -22,7 +22,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 10  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 11  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -89,7 +89,7 @@ SIGNATURES = {
     "p3d_attn_fwd_grid": ([ctypes.POINTER(AttnArgs), _P], c_int32),
     "p3d_attn_fwd_rows": ([ctypes.POINTER(AttnArgs), _P], c_int32),
     "p3d_attn_fwd_grid_noalloc": ([ctypes.POINTER(PoolArgs), ctypes.POINTER(AttnArgs), _P], c_int32),
-    "p3d_local_fwd_indexed": ([ctypes.POINTER(AttnArgs), _P, c_int32, _P, _P], c_int32),
+    "p3d_local_fwd_indexed": ([ctypes.POINTER(AttnArgs), _P, c_int32, _P], c_int32),
     "p3d_selftest_mfma": ([c_int32, _P, _P, _P, _P], c_int32),
     "p3d_struct_sizes": ([_P], c_int32),
     "p3d_probe_issue_rates": ([c_int32, c_int64, c_int32, _P, _P], c_int32),

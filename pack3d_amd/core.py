@@ -173,27 +173,19 @@ class ForwardPlan:
             self._keep.append(mapping)
             self.attn_name = "p3d_attn_fwd_grid"
         else:
-            # Arbitrary graph: rotate Q and local K once, indexed local branch
-            # on VALU, then the summary branch and the epilogue by packed rows.
+            # Arbitrary graph: local K rotated once into a copy (it is
+            # gathered per edge); q rotates on load in both kernels.  The
+            # indexed local kernel writes sl * o_L into y, and the rows kernel
+            # adds the summary branch in its epilogue.
             if not rope.identity:
-                qr = torch.empty(q.shape, dtype=q.dtype, device=dev)
                 klr = torch.empty(kl.shape, dtype=kl.dtype, device=dev)
-                for src, dst, heads in ((q, qr, h), (kl, klr, g)):
-                    self.pre.append(("p3d_rotate", (_lib.view(src), _lib.view(dst), b, heads, n, d, dt,
-                                                    rope.struct(), 0)))
-                q, kl = qr, klr
-                self._keep += [qr, klr]
-            ident = identity_rope(d, dev)
+                self.pre.append(("p3d_rotate", (_lib.view(kl), _lib.view(klr), b, g, n, d, dt, rope.struct(), 0)))
+                kl = klr
+                self._keep.append(klr)
             a.q, a.kl = _lib.view(q), _lib.view(kl)
-            a.rope = ident.struct()
-            self.o_local = torch.empty(b, h, n, d, dtype=torch.float32, device=dev)
-            self._keep += [ident]
-            self.pre.append(("p3d_local_fwd_indexed", (a, geometry.neighbors.data_ptr(),
-                                                       geometry.neighbors.shape[1], self.o_local.data_ptr())))
-            self.rows_args = _lib.AttnArgs()
-            ctypes_copy(self.rows_args, a)
-            self.rows_args.o_local_in = self.o_local.data_ptr()
-            self.rows_args.lse_local = None
+            a.rope = rope.struct()
+            a.o_local_in = None
+            self.pre.append(("p3d_local_fwd_indexed", (a, geometry.neighbors.data_ptr(), geometry.neighbors.shape[1])))
             self.attn_name = "p3d_attn_fwd_rows"
 
     def pool(self):
@@ -204,12 +196,7 @@ class ForwardPlan:
         stream = _lib.stream_of(self.device)
         for name, args in self.pre:
             _lib.call(name, *args, stream)
-        if self.grid:
-            _lib.call(self.attn_name, self.attn_args, stream)
-        else:
-            _lib.call(self.attn_name, self.rows_args, stream)
-            if self.saved:
-                self.saved["o_local"].copy_(self.o_local)
+        _lib.call(self.attn_name, self.attn_args, stream)
 
     def run(self):
         self.pool()
@@ -217,11 +204,6 @@ class ForwardPlan:
         saved = dict(self.saved)
         saved.update({"sk": self.sk, "svt": self.svt})
         return self.y, saved
-
-
-def ctypes_copy(dst, src):
-    import ctypes
-    ctypes.memmove(ctypes.addressof(dst), ctypes.addressof(src), ctypes.sizeof(src))
 
 
 def forward(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature,

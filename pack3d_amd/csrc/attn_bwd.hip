@@ -155,138 +155,6 @@ __global__ __launch_bounds__(256) void k_mix_bwd(BwdDev a) {
     }
 }
 
-// ------------------------------------------------------------ local (VALU)
-// Local dQ for one (batch, head, query row): recompute the local scores over
-// the neighbour row, P = exp(s - lse_L), dS = P (dO_L . v - Delta_L) / sqrt(d),
-// dQ = sum dS k (kernels.py:130-151).  Lanes own neighbour columns, then
-// channels.
-template <typename T>
-__global__ __launch_bounds__(64) void k_local_dq(BwdDev a, const int32_t* nb, int W, int D, float scale) {
-    __shared__ float qs[128], dos[128], dss[128];
-    __shared__ int ids[128];
-    const int lane = threadIdx.x;
-    const int64_t item = blockIdx.x;
-    const int64_t row = item % a.N, bh = item / a.N;
-    const int b = (int)(bh / a.H), h = (int)(bh % a.H), kvh = h / (a.H / a.G);
-    const T* q = tp<T>(a.q) + b * a.qsb + h * a.qsh + row * a.qsn;
-    const T* dol = tp<T>(a.dol) + (bh * a.N + row) * D;
-    for (int c = lane; c < D; c += 64) {
-        qs[c] = to_f32(q[c]);
-        dos[c] = to_f32(dol[c]);
-    }
-    const float lse = a.lse_l[bh * a.N + row], delta = a.dl[bh * a.N + row];
-    int idx[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int w = lane + 64 * j;
-        idx[j] = w < W ? nb[row * W + w] : -1;
-        ids[w] = idx[j];
-    }
-    __syncthreads();
-    const T* K = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
-    const T* V = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        float ds = 0.f;
-        if (idx[j] >= 0 && lse != -INFINITY) {
-            const T* k = K + idx[j] * a.ksn;
-            const T* v = V + idx[j] * a.vsn;
-            float s = 0.f, dp = 0.f;
-            for (int c = 0; c < D; ++c) {
-                s += qs[c] * to_f32(k[c]);
-                dp += dos[c] * to_f32(v[c]);
-            }
-            ds = expf(s * scale - lse) * (dp - delta) * scale;
-        }
-        dss[lane + 64 * j] = ds;
-    }
-    __syncthreads();
-    float* dq = a.dq_l + (bh * a.N + row) * D;
-    for (int c = lane; c < D; c += 64) {
-        float acc = 0.f;
-        for (int w = 0; w < W; ++w) {
-            const int t = ids[w];
-            if (t >= 0) acc += dss[w] * to_f32(K[t * a.ksn + c]);
-        }
-        dq[c] = acc;
-    }
-}
-
-// Local dK, dV for one (batch, kv head, key row j): the queries that list j
-// come from the reverse adjacency; every query head of the kv group
-// contributes (kernels.py:154-181).
-template <typename T>
-__global__ __launch_bounds__(64) void k_local_dkv(BwdDev a, const int32_t* rev, int RW, int D, float scale) {
-    __shared__ float ks[128], vs[128], ps[128], dss[128];
-    __shared__ int ids[128];
-    const int lane = threadIdx.x;
-    const int64_t item = blockIdx.x;
-    const int64_t row = item % a.N, bg = item / a.N;
-    const int b = (int)(bg / a.G), g = (int)(bg % a.G), rep = a.H / a.G;
-    const T* k = tp<T>(a.kl) + b * a.ksb + g * a.ksh + row * a.ksn;
-    const T* v = tp<T>(a.vl) + b * a.vsb + g * a.vsh + row * a.vsn;
-    for (int c = lane; c < D; c += 64) {
-        ks[c] = to_f32(k[c]);
-        vs[c] = to_f32(v[c]);
-    }
-    int idx[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int w = lane + 64 * j;
-        idx[j] = w < RW ? rev[row * RW + w] : -1;
-        ids[w] = idx[j];
-    }
-    float dk[2] = {0.f, 0.f}, dv[2] = {0.f, 0.f};
-    for (int hh = 0; hh < rep; ++hh) {
-        const int h = g * rep + hh;
-        const int64_t bh = (int64_t)b * a.H + h;
-        const T* Q = tp<T>(a.q) + b * a.qsb + h * a.qsh;
-        const T* DO = tp<T>(a.dol) + bh * a.N * D;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float p = 0.f, ds = 0.f;
-            const int i = idx[j];
-            if (i >= 0) {
-                const float lse = a.lse_l[bh * a.N + i];
-                if (lse != -INFINITY) {
-                    float s = 0.f, dp = 0.f;
-                    for (int c = 0; c < D; ++c) {
-                        s += to_f32(Q[i * a.qsn + c]) * ks[c];
-                        dp += to_f32(DO[(int64_t)i * D + c]) * vs[c];
-                    }
-                    p = expf(s * scale - lse);
-                    ds = p * (dp - a.dl[bh * a.N + i]) * scale;
-                }
-            }
-            ps[lane + 64 * j] = p;
-            dss[lane + 64 * j] = ds;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const int c = lane + 64 * cc;
-            if (c >= D) continue;
-            for (int w = 0; w < RW; ++w) {
-                const int i = ids[w];
-                if (i >= 0) {
-                    dk[cc] += dss[w] * to_f32(Q[i * a.qsn + c]);
-                    dv[cc] += ps[w] * to_f32(DO[(int64_t)i * D + c]);
-                }
-            }
-        }
-    }
-    float* dko = a.dk_l + (bg * a.N + row) * D;
-    T* dvo = reinterpret_cast<T*>(a.dv_l) + (bg / a.G) * a.dvsb + (bg % a.G) * a.dvsh + row * a.dvsn;
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
-        const int c = lane + 64 * cc;
-        if (c < D) {
-            dko[c] = dk[cc];
-            dvo[c] = from_f32<T>(dv[cc]);
-        }
-    }
-}
 
 // ------------------------------------------------------------ summaries
 // sv rows [B,G,Mp,D] from svt, and skt [B,G,Mp/32,D,32] from sk (both the
@@ -886,36 +754,6 @@ extern "C" int p3d_mix_bwd(const p3d_bwd_args* args, void* stream) {
     return check_launch("p3d_mix_bwd");
 }
 
-extern "C" int p3d_local_bwd_indexed(const p3d_bwd_args* args, const int32_t* neighbors, int32_t width,
-                                     const int32_t* reverse, int32_t rwidth, void* stream) {
-    P3D_REQUIRE(args, "null args");
-    BwdDev d;
-    if (int rc = fill_bwd(*args, d)) return rc;
-    P3D_REQUIRE(neighbors && reverse && width >= 1 && width <= 128 && rwidth >= 1 && rwidth <= 128,
-                "neighbour tables must have 1..128 columns");
-    P3D_REQUIRE(args->dol && args->lse_local && args->delta_local && args->dq_local && args->dk_local &&
-                    view_ok(args->dv_local, dtype_size(args->dtype)),
-                "null pointer argument or misaligned dv_local");
-    const float scale = 1.f / sqrtf((float)args->head_dim);
-    const unsigned qitems = (unsigned)((int64_t)d.B * d.H * d.N);
-    const unsigned kitems = (unsigned)((int64_t)d.B * d.G * d.N);
-    hipStream_t s = as_stream(stream);
-    switch (args->dtype) {
-        case P3D_F32:
-            k_local_dq<float><<<qitems, 64, 0, s>>>(d, neighbors, width, args->head_dim, scale);
-            k_local_dkv<float><<<kitems, 64, 0, s>>>(d, reverse, rwidth, args->head_dim, scale);
-            break;
-        case P3D_F16:
-            k_local_dq<_Float16><<<qitems, 64, 0, s>>>(d, neighbors, width, args->head_dim, scale);
-            k_local_dkv<_Float16><<<kitems, 64, 0, s>>>(d, reverse, rwidth, args->head_dim, scale);
-            break;
-        default:
-            k_local_dq<__bf16><<<qitems, 64, 0, s>>>(d, neighbors, width, args->head_dim, scale);
-            k_local_dkv<__bf16><<<kitems, 64, 0, s>>>(d, reverse, rwidth, args->head_dim, scale);
-            break;
-    }
-    return check_launch("p3d_local_bwd_indexed");
-}
 
 extern "C" int p3d_global_bwd(const p3d_bwd_args* args, void* stream) {
     P3D_REQUIRE(args, "null args");

@@ -14,7 +14,8 @@
 //      64 and scored on MFMA with a second online-softmax state.
 //   4. Epilogue: y = sl * o_L + gate * sg * o_G, stored in the storage type.
 // Rows kernel (any validated geometry): the same global pathway and epilogue
-// for 64 packed rows per wave, with the local branch read from a buffer.
+// for 64 packed rows per wave, with the local branch read from y (written by
+// the indexed local kernel) or from an fp32 buffer.
 #include "attn_common.hpp"
 
 namespace p3d {
@@ -306,7 +307,8 @@ __device__ __forceinline__ void finish_local(const AttnDev& a, int b, int h, int
 }
 
 // y = sl * o_L + gate * sg * o_G.  The local term comes from y itself (grid
-// kernel, written by finish_local) or from o_local_in (rows kernel).
+// kernel, written by finish_local; rows kernel after p3d_local_fwd_indexed)
+// or from o_local_in (rows kernel).
 template <typename C, bool LOCAL_FROM_Y>
 __device__ __forceinline__ void epilogue(const AttnDev& a, int b, int h, int64_t row, bool valid, int g,
                                          const Soft<C::MB>& st) {
@@ -616,65 +618,13 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_rows(AttnDev a) {
     st[0].reset();
     st[1].reset();
     global_pass<C>(a, bg, lds, qf, st, lane);
+    if (a.o_local_in) {
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) epilogue<C, false>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
-}
-
-// Indexed local attention on VALU: one wave per (batch, head, query row);
-// lanes own neighbour columns for the scores and channels for the output.
-template <typename T>
-__global__ __launch_bounds__(64) void k_local_indexed(AttnDev a, const int32_t* nb, int W, int D,
-                                                     float* out, float scale) {
-    __shared__ float qs[128];
-    __shared__ float ps[128];
-    __shared__ int ids[128];
-    const int lane = threadIdx.x;
-    const int64_t item = blockIdx.x;
-    const int64_t row = item % a.N;
-    const int64_t bh = item / a.N;
-    const int b = (int)(bh / a.H), h = (int)(bh % a.H), kvh = h / (a.H / a.G);
-    const T* q = tp<T>(a.q) + b * a.qsb + h * a.qsh + row * a.qsn;
-    for (int c = lane; c < D; c += 64) qs[c] = to_f32(q[c]);
-    float s[2];
-    int idx[2];
+        for (int nb = 0; nb < 2; ++nb) epilogue<C, false>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
+    } else {  // y already holds sl * o_L (p3d_local_fwd_indexed)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int w = lane + 64 * j;
-        idx[j] = w < W ? nb[row * W + w] : -1;
-        ids[w] = idx[j];
+        for (int nb = 0; nb < 2; ++nb) epilogue<C, true>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
     }
-    __syncthreads();
-    const T* K = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        s[j] = -INFINITY;
-        if (idx[j] >= 0) {
-            const T* k = K + idx[j] * a.ksn;
-            float dot = 0.f;
-            for (int c = 0; c < D; ++c) dot += qs[c] * to_f32(k[c]);
-            s[j] = dot * scale;
-        }
-    }
-    const float mx = wave_max(fmaxf(s[0], s[1]));
-    const bool any = mx != -INFINITY;
-    float e[2], tot;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) e[j] = idx[j] >= 0 ? expf(s[j] - mx) : 0.f;
-    tot = wave_sum(e[0] + e[1]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) ps[lane + 64 * j] = any ? e[j] / tot : 0.f;
-    __syncthreads();
-    const T* V = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
-    float* o = out + (bh * a.N + row) * D;
-    for (int c = lane; c < D; c += 64) {
-        float acc = 0.f;
-        for (int w = 0; w < W; ++w) {
-            const int t = ids[w];
-            if (t >= 0) acc += ps[w] * to_f32(V[t * a.vsn + c]);
-        }
-        o[c] = acc;
-    }
-    if (a.lse_l && lane == 0) a.lse_l[bh * a.N + row] = any ? mx + __logf(tot) : -INFINITY;
 }
 
 int fill_dev(const p3d_attn_args& x, AttnDev& d) {
@@ -780,7 +730,6 @@ extern "C" int p3d_attn_fwd_rows(const p3d_attn_args* args, void* stream) {
     AttnDev d;
     int rc = fill_dev(*args, d);
     if (rc) return rc;
-    P3D_REQUIRE(args->o_local_in, "rows kernel needs o_local_in");
     P3D_REQUIRE((int64_t)d.B * d.H < 65536, "launch grid too large");
     dim3 grid((unsigned)cdiv(d.N, 64 * kWaves), (unsigned)(d.B * d.H));
     hipStream_t s = as_stream(stream);
@@ -793,22 +742,3 @@ extern "C" int p3d_attn_fwd_rows(const p3d_attn_args* args, void* stream) {
     }
 }
 
-extern "C" int p3d_local_fwd_indexed(const p3d_attn_args* args, const int32_t* neighbors, int32_t width,
-                                     float* o_local, void* stream) {
-    P3D_REQUIRE(args && neighbors && o_local, "null argument");
-    AttnDev d;
-    int rc = fill_dev(*args, d);
-    if (rc) return rc;
-    P3D_REQUIRE(width >= 1 && width <= 128, "width must be in [1, 128]");
-    P3D_REQUIRE(args->head_dim <= 128, "head_dim must be <= 128");
-    const int64_t items = (int64_t)d.B * d.H * d.N;
-    P3D_REQUIRE(items < (1LL << 31), "too many rows");
-    const float scale = 1.f / sqrtf((float)args->head_dim);
-    hipStream_t s = as_stream(stream);
-    switch (args->dtype) {
-        case P3D_F32: k_local_indexed<float><<<(unsigned)items, 64, 0, s>>>(d, neighbors, width, args->head_dim, o_local, scale); break;
-        case P3D_F16: k_local_indexed<_Float16><<<(unsigned)items, 64, 0, s>>>(d, neighbors, width, args->head_dim, o_local, scale); break;
-        default: k_local_indexed<__bf16><<<(unsigned)items, 64, 0, s>>>(d, neighbors, width, args->head_dim, o_local, scale); break;
-    }
-    return check_launch("p3d_local_fwd_indexed");
-}

@@ -368,3 +368,29 @@ def test_pool_norm_slots_first_and_repeated_call(gpu):
     exp = torch.zeros(norms.shape[0], norms.shape[1], 64, device=gpu)
     exp.scatter_reduce_(2, (torch.arange(m, device=gpu) % 64).expand_as(norms), norms, reduce="amax")
     assert torch.allclose(first.view_as(exp), exp, rtol=1e-5, atol=0), (first.view_as(exp) - exp).abs().max()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_pool_32_over_64_slots(gpu, dtype):
+    """Summary pool 32 over 64-slot fine blocks at head_dim 64: the reference
+    rejects pool_tile * slot_tile * head_dim > 32768 (_validation.py:21-24), a
+    register budget of its Triton pooling kernel; this pooling walks the fine
+    blocks one at a time and takes it.  Forward and every gradient against the
+    oracle, with random pooling weights and a padded last coarse group."""
+    print(f"pool 32 x 64 slots {dtype}", flush=True)
+    shape, d = (8, 16, 40), 64
+    n = math.prod(shape)
+    lay_h = p3d.build_layout(shape, (4, 4, 4), radius=1, pool_size=32, layout="native_block_morton")
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=1, pool_size=32, layout="native_block_morton")
+    assert lay_h.geometry.blocks.shape == (n // 64, 64) and (n // 64) % 32 != 0
+    inputs = random_core_inputs(1, 4, 2, n, d, 64, dtype, seed=32)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    rs = [t.detach().clone().requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, lay_h.geometry, temperature=0.6)
+    e = ref.pack3d_reference(*rs, lay_r.geometry, temperature=0.6)
+    _check(y, e, dtype, "y")
+    up = torch.randn(e.shape, generator=torch.Generator().manual_seed(6)).to(dtype)
+    got = torch.autograd.grad(y, xs, up.to(gpu))
+    exp = torch.autograd.grad(e, rs, up)
+    for a, b in zip(got, exp):
+        assert rel_l2(a.float(), b.float()) < REL[dtype]

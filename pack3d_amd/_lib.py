@@ -10,7 +10,9 @@ import threading
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpack3d_hip.so")
+# The in-tree build; PACK3D_HIP_LIB may name another build of the same ABI.
+LIB_PATH = os.environ.get("PACK3D_HIP_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                             "libpack3d_hip.so")
 
 c_int32, c_int64, c_float, c_void_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 

@@ -156,8 +156,10 @@ def cpu_baseline(shape, threads, repeats=3):
             times.append(time.perf_counter() - t0)
     med = sorted(times)[len(times) // 2]
     return {"value": round(1000.0 * med, 1), "unit": "ms/layer", "cores": threads, "kind": "port",
-            "sample": (f"the whole c2 layer forward (all {n} tokens and query rows) through the oracle in fp32; "
-                       f"median of {repeats} runs ({', '.join(f'{t:.2f}' for t in times)} s)")}
+            "host_cpus": os.cpu_count(),
+            "sample": (f"the whole c2 layer forward (all {n} tokens and query rows) through the oracle in fp32 "
+                       f"on {threads} threads (the one-GPU box's CPU share; the host reports {os.cpu_count()} "
+                       f"CPUs); median of {repeats} runs ({', '.join(f'{t:.2f}' for t in times)} s)")}
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_c2.md")

@@ -221,6 +221,181 @@ __device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typen
     }
 }
 
+// The bounded sweep, software-pipelined across tiles so that every stretch
+// of exponentials has independent MFMAs beside it.  With s0 / s1 the score
+// tiles of the wave's two column blocks, tile t runs as two phases:
+//   A(t): exponentials of s0(t)  |  MFMAs: scores s1(t), products of block 1 for t - 1
+//   B(t): exponentials of s1(t)  |  MFMAs: scores s0(t + 1), products of block 0 for t
+// so each phase holds 16 exponentials, 8 converts and 7 independent MFMAs
+// (head_dim 48), which the SIMD co-issues.  Stages rotate through three LDS
+// buffers: while stage s is consumed, stage s + 1 (already in LDS) feeds the
+// look-ahead score tile and stage s + 2 is fetched, so one barrier per stage
+// suffices.  Used for bf16 with head_dim <= 48 (fp16 takes the running max).
+template <typename C>
+constexpr bool kPiped = std::is_same<typename C::T_, __bf16>::value && C::D <= 48;
+
+template <typename C>
+__device__ __forceinline__ void probs_to_frags(const f32x16& s, typename C::Frag* pf, float& l) {
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = __builtin_amdgcn_exp2f(s[r]);
+    if constexpr (!C::ONES) {
+        float psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) psum += p[r];
+        l += psum;
+    }
+#pragma unroll
+    for (int ks = 0; ks < C::KSTEPS; ++ks) pf[ks] = frag_from_p<typename C::T_>(p, ks);
+}
+
+template <typename C>
+__device__ __forceinline__ void accumulate_frags(Soft<C::MB>& st, const typename C::Frag* vf,
+                                                 const typename C::Frag* pf) {
+#pragma unroll
+    for (int ks = 0; ks < C::KSTEPS; ++ks)
+#pragma unroll
+        for (int b = 0; b < C::MB; ++b) st.acc[b] = C::M::mfma(vf[b * C::KSTEPS + ks], pf[ks], st.acc[b]);
+}
+
+// Scores of keys at or beyond M (the partial last tile) -> -inf.
+template <typename C>
+__device__ __forceinline__ void mask_tail(const AttnDev& a, int first, f32x16& s, int g) {
+    if (first + 32 > a.M) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            if (first + kperm<C::E, C::KS>(acc_row(r, g)) >= a.M) s[r] = -INFINITY;
+    }
+}
+
+// One phase of the pipelined sweep: the exponentials of `sx` (column block
+// X) -> pfx, beside the score MFMAs sq = negm + K Q_Y^T of the other column
+// block Y and the products accY += V pfy of block Y's previous tile.  They
+// are written interleaved, each MFMA followed by its share of the
+// exponentials and converts, with scheduling barriers between the groups,
+// so that every exponential has an independent MFMA in flight beside it.
+// With LOADS, once the score MFMAs have read kf the next tile's keys are
+// loaded into it (this lane's key row at knext), and once the products have
+// read vf the values of the tile at vnext (a transposed stage buffer) are.
+template <typename C, bool LOADS>
+__device__ __forceinline__ void pipe_phase(const f32x16& sx, typename C::Frag* pfx, float& lx,
+                                           const typename C::Frag* qy, const f32x16& negm, f32x16& sq,
+                                           Soft<C::MB>& sty, const typename C::Frag* pfy, typename C::Frag* kf,
+                                           const typename C::T_* knext, typename C::Frag* vf,
+                                           const typename C::T_* vnext, int lane) {
+    constexpr int NQ = C::NT, NM = C::NT + C::MB * C::KSTEPS;
+    float p[16];
+#pragma unroll
+    for (int j = 0; j < NM; ++j) {
+        if (j < NQ) {
+            sq = C::M::mfma(kf[j], qy[j], j == 0 ? negm : sq);
+        } else {
+            const int i = j - NQ, ks = i / C::MB, b = i % C::MB;
+            sty.acc[b] = C::M::mfma(vf[b * C::KSTEPS + ks], pfy[ks], sty.acc[b]);
+        }
+#pragma unroll
+        for (int r = 16 * j / NM; r < 16 * (j + 1) / NM; ++r) {
+            p[r] = __builtin_amdgcn_exp2f(sx[r]);
+            if (r % 8 == 7) pfx[r / 8] = frag_from_p<typename C::T_>(p, r / 8);
+        }
+        if (LOADS && j == NQ - 1) load_kfrags<C>(knext, kf);
+        if (LOADS && j == NM - 1) load_vfrags<C, true>(vnext, 64 + Piece<typename C::T_>::N, 0, lane, vf);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (!C::ONES) {
+        float psum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) psum += p[r];
+        lx += psum;
+    }
+}
+
+// One tile t of the pipelined sweep: phases A(t) and B(t).  On entry s0
+// holds the block-0 scores and kf the keys of tile t, pf1 / vf the block-1
+// probabilities and the values of tile t - 1; on exit s0 and kf belong to
+// tile t + 1 (keys at knext), pf1 / vf to tile t (values at vcur).  negm is
+// the wave's common reference point.  MASK masks keys at or beyond M (the
+// partial last tile).
+template <typename C, bool MASK>
+__device__ __forceinline__ void pipe_tile(const AttnDev& a, const typename C::T_* vcur, int first,
+                                          const typename C::T_* knext, const typename C::Frag (*qf)[C::NT],
+                                          Soft<C::MB>* st, const f32x16& negm, f32x16& s0,
+                                          typename C::Frag* kf, typename C::Frag* pf1, typename C::Frag* vf,
+                                          int lane) {
+    const int g = lane >> 5;
+    typename C::Frag pf0[C::KSTEPS];
+    f32x16 s1;
+    if constexpr (MASK) mask_tail<C>(a, first, s0, g);
+    // A(t): exponentials of s0(t) | scores s1(t), block 1's products of t - 1;
+    // then the keys of t + 1 and the values of t are loaded
+    pipe_phase<C, true>(s0, pf0, st[0].l, qf[1], negm, s1, st[1], pf1, kf, knext, vf, vcur, lane);
+    if constexpr (MASK) mask_tail<C>(a, first, s1, g);
+    // B(t): exponentials of s1(t) | scores s0(t + 1), block 0's products of t
+    pipe_phase<C, false>(s1, pf1, st[1].l, qf[0], negm, s0, st[0], pf0, kf, nullptr, vf, nullptr, lane);
+}
+
+template <typename C>
+__device__ __forceinline__ void global_sweep_piped(const AttnDev& a, int64_t bg, typename C::T_* lds,
+                                                   const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st,
+                                                   int lane) {
+    typedef typename C::T_ T;
+    typedef typename C::Frag Frag;
+    const int g = lane >> 5, qi = lane & 31;
+    f32x16 negm;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) negm[r] = -st[0].m;
+    constexpr int EP = Piece<T>::N;
+    constexpr int VGS = 64 + EP;
+    constexpr int STAGE = 64 * C::KSTR + 32 * C::MB * VGS;
+#pragma unroll
+    for (int b = 0; b < 3; ++b) init_v_padding<C>(lds + b * STAGE + 64 * C::KSTR, VGS, 64);
+    const int stages = (a.M + 63) / 64, full = a.M / 64;
+    StageRegs<C> regs;
+    regs.load(a, bg, 0);
+    regs.store(lds);
+    if (stages > 1) {
+        regs.load(a, bg, 64);
+        regs.store(lds + STAGE);
+    }
+    __syncthreads();
+
+    const int krow = kperm<C::E, C::KS>(qi) * C::KSTR + C::E * g;
+    Frag kf[C::NT], vf[C::MB * C::KSTEPS], pf1[C::KSTEPS];
+#pragma unroll
+    for (int i = 0; i < C::MB * C::KSTEPS; ++i) vf[i] = frag_fill<T>(0.f);
+#pragma unroll
+    for (int i = 0; i < C::KSTEPS; ++i) pf1[i] = frag_fill<T>(0.f);
+    load_kfrags<C>(lds + krow, kf);
+    f32x16 s0 = score_tile<C>(kf, qf[0], negm);
+
+    // Stages whose 64 keys are all present: no masks.
+    int cur = 0;  // buffer of stage `stage`
+    for (int stage = 0; stage < full; ++stage) {
+        const bool fetch = stage + 2 < stages;
+        if (fetch) regs.load(a, bg, 64 * (stage + 2));
+        const int nxt = cur == 2 ? 0 : cur + 1;
+        const T* Ks = lds + cur * STAGE;
+        pipe_tile<C, false>(a, Ks + 64 * C::KSTR, 0, Ks + 32 * C::KSTR + krow, qf, st, negm, s0, kf, pf1, vf, lane);
+        pipe_tile<C, false>(a, Ks + 64 * C::KSTR + 32, 0, lds + nxt * STAGE + krow, qf, st, negm, s0, kf, pf1, vf,
+                            lane);
+        if (fetch) regs.store(lds + (nxt == 2 ? 0 : nxt + 1) * STAGE);
+        __syncthreads();
+        cur = nxt;
+    }
+    // The last, partial stage (its rows past M are zero in LDS).
+    if (full < stages) {
+        const T* Ks = lds + cur * STAGE;
+        const int base = 64 * full;
+        pipe_tile<C, true>(a, Ks + 64 * C::KSTR, base, Ks + 32 * C::KSTR + krow, qf, st, negm, s0, kf, pf1, vf,
+                           lane);
+        if (base + 32 < a.M)
+            pipe_tile<C, true>(a, Ks + 64 * C::KSTR + 32, base + 32, Ks + krow, qf, st, negm, s0, kf, pf1, vf,
+                               lane);
+        __syncthreads();
+    }
+    accumulate_frags<C>(st[1], vf, pf1);
+}
+
 // The summary pathway for this workgroup.  Summary keys are stored scaled by
 // log2(e)/sqrt(d), so scores are in the exp2 domain.  Every score of a query
 // is bounded by |q| max_j |sk_j| (Cauchy-Schwarz); that bound is the fixed
@@ -250,7 +425,14 @@ __device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typena
         st[nb].reset();
         st[nb].m = q_norm<C>(qf[nb]) * kmax;
     }
-    global_sweep<C, true>(a, bg, lds, qf, st, lane);
+    if constexpr (kPiped<C>) {
+        // One reference point for the wave's 64 queries (their largest bound),
+        // so both column blocks share one initial accumulator.
+        const float m = wave_max(fmaxf(st[0].m, st[1].m));
+        st[0].m = st[1].m = m;
+        global_sweep_piped<C>(a, bg, lds, qf, st, lane);
+    } else
+        global_sweep<C, true>(a, bg, lds, qf, st, lane);
     bool weak = false;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) weak = weak || !(soft_denominator<C>(st[nb], lane >> 5) > 0x1p-60f);
@@ -664,7 +846,7 @@ size_t lds_grid() {
     typedef Cfg<T, D> C;
     constexpr int ep = Piece<T>::N;
     const size_t plane = (size_t)kPlaneKeys * C::KSTR + (size_t)32 * C::MB * (kPlaneKeys + ep);
-    const size_t stages = 2 * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep));
+    const size_t stages = (kPiped<C> ? 3 : 2) * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep));
     return kRopeWindowBytes + (plane > stages ? plane : stages) * sizeof(T);
 }
 
@@ -672,7 +854,7 @@ template <typename T, int D>
 size_t lds_rows() {
     typedef Cfg<T, D> C;
     constexpr int ep = Piece<T>::N;
-    return 2 * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(T);
+    return (kPiped<C> ? 3 : 2) * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(T);
 }
 
 template <int D>

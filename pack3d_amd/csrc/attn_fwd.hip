@@ -21,7 +21,8 @@
 namespace p3d {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;      // brick kernel: one 4 x 8 x 8 brick per workgroup
+constexpr int kRowsWaves = 4;  // rows kernel: 256 query rows per workgroup (8 waves measured slower)
 constexpr int kPlane = 12;                 // plane side for radius <= 2 and an 8 x 8 brick face
 constexpr int kPlaneKeys = kPlane * kPlane;
 // LDS bytes of the rotation window: (cos, sin) for 64 pairs x 12 positions, then 64 axis ids.
@@ -96,28 +97,28 @@ __device__ __forceinline__ void load_q(const typename C::T_* row, bool valid, Ro
 // A stage is one contiguous block of sk ([64][D]) and one of svt
 // ([2][D][32]), so a thread's piece p sits at element offset p * EP in both;
 // the LDS offsets of its pieces are fixed and computed once.
-template <typename C>
+template <typename C, int WG>
 struct StageRegs {
     typedef typename C::T_ T;
     static constexpr int EP = Piece<T>::N;
     static constexpr int VGS = 64 + EP;
     static constexpr int KPIECES = 64 * (C::D / EP);
     static constexpr int VPIECES = C::D * (64 / EP);
-    static constexpr int KI = (KPIECES + 64 * kWaves - 1) / (64 * kWaves);
-    static constexpr int VI = (VPIECES + 64 * kWaves - 1) / (64 * kWaves);
+    static constexpr int KI = (KPIECES + WG - 1) / (WG);
+    static constexpr int VI = (VPIECES + WG - 1) / (WG);
     uint4 k[KI], v[VI];
     int klds[KI], vlds[VI];
 
     __device__ __forceinline__ StageRegs() {
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
+            const int p = threadIdx.x + i * WG;
             const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
             klds[i] = r * C::KSTR + c;
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
+            const int p = threadIdx.x + i * WG;
             const int tt = p / (C::D * (32 / EP));
             const int rem = p - tt * C::D * (32 / EP);
             const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
@@ -132,24 +133,54 @@ struct StageRegs {
         const T* svt = tp<T>(a.svt) + ((int64_t)bg * a.Mp + base) * C::D;
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
-            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
+            const int off = (threadIdx.x + i * WG) * EP;
             k[i] = off < limit ? *reinterpret_cast<const uint4*>(sk + off) : uint4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < VI; ++i) {
-            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
+            const int off = (threadIdx.x + i * WG) * EP;
             v[i] = off < limit ? *reinterpret_cast<const uint4*>(svt + off) : uint4{0, 0, 0, 0};
         }
+    }
+
+    // Branch-free forms for the pipelined sweep, whose stage loop must stay
+    // one basic block.  Every thread loads from a valid address: offsets are
+    // clamped into the stage's present rows, so a piece past them repeats
+    // one of this (b, g)'s summary rows (finite; its keys are masked or
+    // skipped by the sweep).  Pieces beyond the stage's count are stored into
+    // row padding that no fragment read touches (K columns [D, KSTR), V^T
+    // columns [64, VGS)).
+    __device__ __forceinline__ void load_clamped(const AttnDev& a, int64_t bg, int base) {
+        const int last = min(64, a.Mp - base) * C::D - EP;
+        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
+        const T* svt = tp<T>(a.svt) + ((int64_t)bg * a.Mp + base) * C::D;
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            k[i] = *reinterpret_cast<const uint4*>(sk + min((int)(threadIdx.x + i * WG) * EP, last));
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+            v[i] = *reinterpret_cast<const uint4*>(svt + min((int)(threadIdx.x + i * WG) * EP, last));
+    }
+    __device__ __forceinline__ void store_all(T* stage) const {
+        static_assert(C::KSTR - C::D >= EP && VGS - 64 >= EP, "no row padding for the spare pieces");
+        const int spare_k = (threadIdx.x % 64) * C::KSTR + C::D;
+        const int spare_v = 64 * C::KSTR + (threadIdx.x % C::D) * VGS + 64;
+#pragma unroll
+        for (int i = 0; i < KI; ++i)
+            *reinterpret_cast<uint4*>(stage + (threadIdx.x + i * WG < KPIECES ? klds[i] : spare_k)) = k[i];
+#pragma unroll
+        for (int i = 0; i < VI; ++i)
+            *reinterpret_cast<uint4*>(stage + (threadIdx.x + i * WG < VPIECES ? vlds[i] : spare_v)) = v[i];
     }
 
     // Write the staged pieces into a stage buffer (K rows then V rows).
     __device__ __forceinline__ void store(T* stage) const {
 #pragma unroll
         for (int i = 0; i < KI; ++i)
-            if (threadIdx.x + i * 64 * kWaves < KPIECES) *reinterpret_cast<uint4*>(stage + klds[i]) = k[i];
+            if (threadIdx.x + i * WG < KPIECES) *reinterpret_cast<uint4*>(stage + klds[i]) = k[i];
 #pragma unroll
         for (int i = 0; i < VI; ++i)
-            if (threadIdx.x + i * 64 * kWaves < VPIECES) *reinterpret_cast<uint4*>(stage + vlds[i]) = v[i];
+            if (threadIdx.x + i * WG < VPIECES) *reinterpret_cast<uint4*>(stage + vlds[i]) = v[i];
     }
 };
 
@@ -191,7 +222,7 @@ __device__ __forceinline__ void global_stage(const AttnDev& a, int base, const t
 }
 
 // All M summaries streamed through a double-buffered LDS region at `lds`.
-template <typename C, bool BOUND>
+template <typename C, bool BOUND, int WG>
 __device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typename C::T_* lds,
                                              const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
     f32x16 negm[2];
@@ -205,7 +236,7 @@ __device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typen
     constexpr int STAGE = 64 * C::KSTR + 32 * C::MB * VGS;
     init_v_padding<C>(lds + 64 * C::KSTR, VGS, 64);
     init_v_padding<C>(lds + STAGE + 64 * C::KSTR, VGS, 64);
-    StageRegs<C> regs;
+    StageRegs<C, WG> regs;
     regs.load(a, bg, 0);
     regs.store(lds);
     __syncthreads();
@@ -334,7 +365,7 @@ __device__ __forceinline__ void pipe_tile(const AttnDev& a, const typename C::T_
     pipe_phase<C, false>(s1, pf1, st[1].l, qf[0], negm, s0, st[0], pf0, kf, nullptr, vf, nullptr, lane);
 }
 
-template <typename C>
+template <typename C, int WG>
 __device__ __forceinline__ void global_sweep_piped(const AttnDev& a, int64_t bg, typename C::T_* lds,
                                                    const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st,
                                                    int lane) {
@@ -350,7 +381,7 @@ __device__ __forceinline__ void global_sweep_piped(const AttnDev& a, int64_t bg,
 #pragma unroll
     for (int b = 0; b < 3; ++b) init_v_padding<C>(lds + b * STAGE + 64 * C::KSTR, VGS, 64);
     const int stages = (a.M + 63) / 64, full = a.M / 64;
-    StageRegs<C> regs;
+    StageRegs<C, WG> regs;
     regs.load(a, bg, 0);
     regs.store(lds);
     if (stages > 1) {
@@ -370,15 +401,18 @@ __device__ __forceinline__ void global_sweep_piped(const AttnDev& a, int64_t bg,
 
     // Stages whose 64 keys are all present: no masks.
     int cur = 0;  // buffer of stage `stage`
+    // The loop body is one basic block (a branch would let the compiler sink
+    // a phase's exponentials away from their MFMAs): stage s + 2 is always
+    // fetched, past the last stage as a repeat of it into the buffer no one
+    // reads any more.
     for (int stage = 0; stage < full; ++stage) {
-        const bool fetch = stage + 2 < stages;
-        if (fetch) regs.load(a, bg, 64 * (stage + 2));
+        regs.load_clamped(a, bg, 64 * min(stage + 2, stages - 1));
         const int nxt = cur == 2 ? 0 : cur + 1;
         const T* Ks = lds + cur * STAGE;
         pipe_tile<C, false>(a, Ks + 64 * C::KSTR, 0, Ks + 32 * C::KSTR + krow, qf, st, negm, s0, kf, pf1, vf, lane);
         pipe_tile<C, false>(a, Ks + 64 * C::KSTR + 32, 0, lds + nxt * STAGE + krow, qf, st, negm, s0, kf, pf1, vf,
                             lane);
-        if (fetch) regs.store(lds + (nxt == 2 ? 0 : nxt + 1) * STAGE);
+        regs.store_all(lds + (nxt == 2 ? 0 : nxt + 1) * STAGE);
         __syncthreads();
         cur = nxt;
     }
@@ -410,13 +444,13 @@ __device__ __forceinline__ void global_sweep_piped(const AttnDev& a, int64_t bg,
 // bits, so a bound 14-24 log2 units above the true maximum would degrade
 // every probability of the query.  fp16 therefore takes the running max,
 // which keeps the largest probability of each query in [1, 2^8].
-template <typename C>
+template <typename C, int WG>
 __device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typename C::T_* lds,
                                             const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st, int lane) {
     if constexpr (std::is_same<typename C::T_, _Float16>::value) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) st[nb].reset();
-        global_sweep<C, false>(a, bg, lds, qf, st, lane);
+        global_sweep<C, false, WG>(a, bg, lds, qf, st, lane);
         return;
     }
     const float kmax = wave_max(a.sk_norm_max[bg * 64 + lane]);
@@ -430,16 +464,16 @@ __device__ __forceinline__ void global_pass(const AttnDev& a, int64_t bg, typena
         // so both column blocks share one initial accumulator.
         const float m = wave_max(fmaxf(st[0].m, st[1].m));
         st[0].m = st[1].m = m;
-        global_sweep_piped<C>(a, bg, lds, qf, st, lane);
+        global_sweep_piped<C, WG>(a, bg, lds, qf, st, lane);
     } else
-        global_sweep<C, true>(a, bg, lds, qf, st, lane);
+        global_sweep<C, true, WG>(a, bg, lds, qf, st, lane);
     bool weak = false;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) weak = weak || !(soft_denominator<C>(st[nb], lane >> 5) > 0x1p-60f);
     if (__syncthreads_or(weak)) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) st[nb].reset();
-        global_sweep<C, false>(a, bg, lds, qf, st, lane);
+        global_sweep<C, false, WG>(a, bg, lds, qf, st, lane);
     }
 }
 
@@ -768,13 +802,13 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     __syncthreads();  // the summary stages reuse the plane buffer
 
     // ---- global pathway (the rotation window is no longer needed)
-    global_pass<C>(a, bg, Kp, qf, st, lane);
+    global_pass<C, 64 * kWaves>(a, bg, Kp, qf, st, lane);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) epilogue<C, true>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
 }
 
 template <typename T, int D>
-__global__ __launch_bounds__(64 * kWaves, 2) void k_attn_rows(AttnDev a) {
+__global__ __launch_bounds__(64 * kRowsWaves, 2) void k_attn_rows(AttnDev a) {
     typedef Cfg<T, D> C;
     extern __shared__ __align__(16) unsigned char smem[];
     T* lds = reinterpret_cast<T*>(smem);
@@ -788,7 +822,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_rows(AttnDev a) {
     bool qok[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        const int64_t row = (int64_t)blockIdx.x * 64 * kWaves + 64 * wave + 32 * nb + qi;
+        const int64_t row = (int64_t)blockIdx.x * 64 * kRowsWaves + 64 * wave + 32 * nb + qi;
         qok[nb] = row < a.N;
         qrow[nb] = qok[nb] ? row : 0;
         int64_t pos[3];
@@ -799,7 +833,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_rows(AttnDev a) {
     Soft<C::MB> st[2];
     st[0].reset();
     st[1].reset();
-    global_pass<C>(a, bg, lds, qf, st, lane);
+    global_pass<C, 64 * kRowsWaves>(a, bg, lds, qf, st, lane);
     if (a.o_local_in) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) epilogue<C, false>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
@@ -870,9 +904,9 @@ int launch_grid(const AttnDev& d, int dtype, dim3 grid, hipStream_t s) {
 template <int D>
 int launch_rows(const AttnDev& d, int dtype, dim3 grid, hipStream_t s) {
     switch (dtype) {
-        case P3D_F32: k_attn_rows<float, D><<<grid, 64 * kWaves, lds_rows<float, D>(), s>>>(d); break;
-        case P3D_F16: k_attn_rows<_Float16, D><<<grid, 64 * kWaves, lds_rows<_Float16, D>(), s>>>(d); break;
-        default: k_attn_rows<__bf16, D><<<grid, 64 * kWaves, lds_rows<__bf16, D>(), s>>>(d); break;
+        case P3D_F32: k_attn_rows<float, D><<<grid, 64 * kRowsWaves, lds_rows<float, D>(), s>>>(d); break;
+        case P3D_F16: k_attn_rows<_Float16, D><<<grid, 64 * kRowsWaves, lds_rows<_Float16, D>(), s>>>(d); break;
+        default: k_attn_rows<__bf16, D><<<grid, 64 * kRowsWaves, lds_rows<__bf16, D>(), s>>>(d); break;
     }
     return check_launch("p3d_attn_fwd_rows");
 }
@@ -913,7 +947,7 @@ extern "C" int p3d_attn_fwd_rows(const p3d_attn_args* args, void* stream) {
     int rc = fill_dev(*args, d);
     if (rc) return rc;
     P3D_REQUIRE((int64_t)d.B * d.H < 65536, "launch grid too large");
-    dim3 grid((unsigned)cdiv(d.N, 64 * kWaves), (unsigned)(d.B * d.H));
+    dim3 grid((unsigned)cdiv(d.N, 64 * kRowsWaves), (unsigned)(d.B * d.H));
     hipStream_t s = as_stream(stream);
     switch (args->head_dim) {
 #define CASE(DD) \

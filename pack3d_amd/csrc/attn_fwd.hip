@@ -492,18 +492,19 @@ __device__ __forceinline__ void load_quad(const T* src, float* v) {
     for (int i = 0; i < 4; ++i) v[i] = to_f32(src[i]);
 }
 
-// Finish the local state: y <- sl * o_L (storage type; the epilogue adds the
-// global branch), optionally saving o_L and its log-sum-exp.
+// Finish the local state: sl * o_L (storage type; the epilogue adds the
+// global branch) goes to y, or with a park buffer into LDS (slot
+// 4 mb + q of this lane, quads of 4 channels, lane-fastest), optionally
+// saving o_L and its log-sum-exp.
 template <typename C>
 __device__ __forceinline__ void finish_local(const AttnDev& a, int b, int h, int64_t row, bool valid, int g,
-                                             const Soft<C::MB>& st) {
+                                             const Soft<C::MB>& st, typename C::T_* park, int lane) {
     typedef typename C::T_ T;
     const float den = soft_denominator<C>(st, g);
-    if (!valid) return;
     const float inv = den > 0.f ? 1.f / den : 0.f;  // an all-masked row gives 0
     const int64_t bh = (int64_t)b * a.H + h;
     T* y = reinterpret_cast<T*>(a.y) + b * a.ysb + h * a.ysh + row * a.ysn;
-    T* ol = a.o_l ? reinterpret_cast<T*>(a.o_l) + (bh * a.N + row) * C::D : nullptr;
+    T* ol = a.o_l && valid ? reinterpret_cast<T*>(a.o_l) + (bh * a.N + row) * C::D : nullptr;
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
@@ -516,18 +517,25 @@ __device__ __forceinline__ void finish_local(const AttnDev& a, int b, int h, int
                 o[i] = st.acc[mb][4 * q + i] * inv;
                 yl[i] = a.sl[ch0 + i] * o[i];
             }
-            store_quad<T>(y + ch0, yl);
+            if (park)
+                store_quad<T>(park + ((4 * mb + q) * 64 + lane) * 4, yl);
+            else if (valid)
+                store_quad<T>(y + ch0, yl);
             if (ol) store_quad<T>(ol + ch0, o);
         }
-    if (a.lse_l) a.lse_l[bh * a.N + row] = den > 0.f ? st.m * kLn2 + __logf(den) : -INFINITY;
+    if (a.lse_l && valid) a.lse_l[bh * a.N + row] = den > 0.f ? st.m * kLn2 + __logf(den) : -INFINITY;
 }
 
-// y = sl * o_L + gate * sg * o_G.  The local term comes from y itself (grid
-// kernel, written by finish_local; rows kernel after p3d_local_fwd_indexed)
-// or from o_local_in (rows kernel).
-template <typename C, bool LOCAL_FROM_Y>
+// y = sl * o_L + gate * sg * o_G.  The local term comes from y itself
+// (LOCAL_Y: written by finish_local, or by p3d_local_fwd_indexed before the
+// rows kernel), from o_local_in (LOCAL_IN, rows kernel) or from the LDS
+// park buffer finish_local filled (LOCAL_PARK, brick kernel).
+enum LocalSource { LOCAL_Y, LOCAL_IN, LOCAL_PARK };
+
+template <typename C, int SRC>
 __device__ __forceinline__ void epilogue(const AttnDev& a, int b, int h, int64_t row, bool valid, int g,
-                                         const Soft<C::MB>& st) {
+                                         const Soft<C::MB>& st, const typename C::T_* park = nullptr,
+                                         int lane = 0) {
     typedef typename C::T_ T;
     const float den = soft_denominator<C>(st, g);
     if (!valid) return;
@@ -536,7 +544,7 @@ __device__ __forceinline__ void epilogue(const AttnDev& a, int b, int h, int64_t
     const float gate = load_any(a.gate, b * a.gsb + h * a.gsh + row * a.gsn, a.gate_dtype);
     T* y = reinterpret_cast<T*>(a.y) + b * a.ysb + h * a.ysh + row * a.ysn;
     T* og = a.o_g ? reinterpret_cast<T*>(a.o_g) + (bh * a.N + row) * C::D : nullptr;
-    const float* oli = LOCAL_FROM_Y ? nullptr : a.o_local_in + (bh * a.N + row) * C::D;
+    const float* oli = SRC == LOCAL_IN ? a.o_local_in + (bh * a.N + row) * C::D : nullptr;
 #pragma unroll
     for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
@@ -544,8 +552,10 @@ __device__ __forceinline__ void epilogue(const AttnDev& a, int b, int h, int64_t
             if (32 * mb + 8 * q >= C::D) continue;
             const int ch0 = acc_channel(mb, 4 * q, g);
             float yl[4], out[4], o[4];
-            if constexpr (LOCAL_FROM_Y) {
+            if constexpr (SRC == LOCAL_Y) {
                 load_quad<T>(y + ch0, yl);
+            } else if constexpr (SRC == LOCAL_PARK) {
+                load_quad<T>(park + ((4 * mb + q) * 64 + lane) * 4, yl);
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) yl[i] = a.sl[ch0 + i] * oli[ch0 + i];
@@ -693,6 +703,25 @@ __device__ __forceinline__ uint32_t stencil_mask(const AttnDev& a, int c, int g,
     return m;
 }
 
+// LDS of the brick kernel: the rotation window, then the plane buffer or
+// the summary stages (whichever is larger), then -- when it still leaves room
+// for two workgroups per CU -- the park buffer of sl * o_L (4 waves x 2
+// column blocks x D / 8 quads x 64 lanes x 4 values), which saves y a write
+// and a re-read.
+template <typename C>
+constexpr size_t grid_main_bytes() {
+    constexpr size_t ep = Piece<typename C::T_>::N;
+    constexpr size_t plane = (size_t)kPlaneKeys * C::KSTR + (size_t)32 * C::MB * (kPlaneKeys + ep);
+    constexpr size_t stages = (kPiped<C> ? 3 : 2) * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep));
+    return kRopeWindowBytes + (plane > stages ? plane : stages) * sizeof(typename C::T_);
+}
+template <typename C>
+constexpr size_t grid_park_bytes() {
+    return (size_t)kWaves * 2 * (C::D / 8) * 64 * 4 * sizeof(typename C::T_);
+}
+template <typename C>
+constexpr bool kPark = grid_main_bytes<C>() + grid_park_bytes<C>() <= 80 * 1024;
+
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     typedef Cfg<T, D> C;
@@ -794,9 +823,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
             }
         }
     }
+    T* park = kPark<C> ? reinterpret_cast<T*>(smem + grid_main_bytes<C>()) : nullptr;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        finish_local<C>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
+        finish_local<C>(a, b, h, qrow[nb], qok[nb], g, st[nb],
+                        park ? park + (wave * 2 + nb) * (C::D / 8) * 64 * 4 : nullptr, lane);
         st[nb].reset();
     }
     __syncthreads();  // the summary stages reuse the plane buffer
@@ -804,7 +835,13 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     // ---- global pathway (the rotation window is no longer needed)
     global_pass<C, 64 * kWaves>(a, bg, Kp, qf, st, lane);
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) epilogue<C, true>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
+    for (int nb = 0; nb < 2; ++nb) {
+        if constexpr (kPark<C>)
+            epilogue<C, LOCAL_PARK>(a, b, h, qrow[nb], qok[nb], g, st[nb],
+                                    park + (wave * 2 + nb) * (C::D / 8) * 64 * 4, lane);
+        else
+            epilogue<C, LOCAL_Y>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
+    }
 }
 
 template <typename T, int D>
@@ -836,10 +873,10 @@ __global__ __launch_bounds__(64 * kRowsWaves, 2) void k_attn_rows(AttnDev a) {
     global_pass<C, 64 * kRowsWaves>(a, bg, lds, qf, st, lane);
     if (a.o_local_in) {
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) epilogue<C, false>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
+        for (int nb = 0; nb < 2; ++nb) epilogue<C, LOCAL_IN>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
     } else {  // y already holds sl * o_L (p3d_local_fwd_indexed)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) epilogue<C, true>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
+        for (int nb = 0; nb < 2; ++nb) epilogue<C, LOCAL_Y>(a, b, h, qrow[nb], qok[nb], g, st[nb]);
     }
 }
 
@@ -878,10 +915,7 @@ int fill_dev(const p3d_attn_args& x, AttnDev& d) {
 template <typename T, int D>
 size_t lds_grid() {
     typedef Cfg<T, D> C;
-    constexpr int ep = Piece<T>::N;
-    const size_t plane = (size_t)kPlaneKeys * C::KSTR + (size_t)32 * C::MB * (kPlaneKeys + ep);
-    const size_t stages = (kPiped<C> ? 3 : 2) * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep));
-    return kRopeWindowBytes + (plane > stages ? plane : stages) * sizeof(T);
+    return grid_main_bytes<C>() + (kPark<C> ? grid_park_bytes<C>() : 0);
 }
 
 template <typename T, int D>

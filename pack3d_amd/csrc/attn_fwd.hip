@@ -740,12 +740,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     const int bh = work % (a.B * a.H), brick = work / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.G);
     const int64_t bg = (int64_t)b * a.G + kvh;
-    // Bricks run z-fastest: consecutive bricks of an XCD share 2 rz of their
-    // 4 + 2 rz halo planes, which the XCD's L2 still holds.
-    const int bricks_z = (a.Z + 3) / 4;
-    const int Z0 = 4 * (brick % bricks_z);
-    const int Y0 = 8 * ((brick / bricks_z) / a.bricks_x);
-    const int X0 = 8 * ((brick / bricks_z) % a.bricks_x);
+    const int Z0 = 4 * (brick / (a.bricks_y * a.bricks_x));
+    const int Y0 = 8 * ((brick / a.bricks_x) % a.bricks_y);
+    const int X0 = 8 * (brick % a.bricks_x);
     const int wy = wave >> 1, wx = wave & 1;
     const int qy = (qi >> 2) & 3, qx = qi & 3;  // within the wave footprint
 

@@ -50,8 +50,11 @@ __device__ __forceinline__ void store4(T* dst, const float (&v)[4]) {
     *reinterpret_cast<T4*>(dst) = o;
 }
 
+// Waves per SIMD: 4 up to dim 128, 3 at dim 192 (the 168 registers that
+// leaves hold the GEMM without spilling; at 4 it spilled 16), else 2.
 template <typename T, int KS>
-__global__ __launch_bounds__(64 * kProjWaves) __attribute__((amdgpu_waves_per_eu(KS <= 12 ? 4 : 2))) void k_project(ProjDev a) {
+__global__ __launch_bounds__(64 * kProjWaves)
+__attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_project(ProjDev a) {
     typedef Mma<T> M;
     typedef typename M::Frag Frag;
     constexpr int DIM = 16 * KS;

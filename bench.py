@@ -29,10 +29,11 @@ if ROOT not in sys.path:
 METRIC = "ms per PACK3D layer fwd @262,144 tokens bf16; % of MFMA/HBM roofline"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-# v_exp_f32 issue rate of the whole chip, two waves per SIMD, measured by
-# `bench.py --probe-rates` (profiles/issue_rates.md): the transcendental
-# rate that bounds the softmax of the summary pathway.
-PEAK_EXP_PER_S = 11.81e12
+# v_exp_f32 rate of the whole chip, 16 independent chains per wave at four
+# waves per SIMD, measured by `bench.py --probe-rates`
+# (profiles/issue_rates.md): the transcendental rate of the summary
+# pathway's softmax.
+PEAK_EXP_PER_S = 16.53e12
 
 SHAPE = (64, 64, 64)
 DIM, HEADS, KV_HEADS, HEAD_DIM, BLOCK, RADIUS = 192, 4, 4, 48, (4, 4, 4), 2
@@ -263,36 +264,43 @@ def bench_c4(steps, warmup):
 
 
 def probe_rates():
-    """Issue rates the summary pathway is bound by, with two waves per SIMD on
-    every CU, timed with HIP events: v_exp_f32 and v_fma_f32 per second, the
-    bf16 32x32x16 MFMA in TFLOP/s, and both rates when every wave issues 4
-    MFMAs and 16 exponentials per iteration, independent of each other."""
+    """Issue rates and co-issue of the units the summary pathway uses
+    (p3d_probe_issue_rates), every operand in registers, at 1, 2 and 4 waves
+    per SIMD on every CU: SIMD cycles per wave-iteration (time x the run's
+    shader clock / iterations per SIMD) and, for the single kinds, rates per
+    second.  The clock comes from the waves' own shader-clock and 100 MHz
+    wall-clock counters."""
     from pack3d_amd import _lib
 
     dev = torch.device("cuda:0")
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    blocks, iters = 2 * cus, 4096
-    waves = blocks * 4
-    cycles = torch.zeros(waves, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream(dev)
-    res = {}
-    for kind, name in ((0, "exp"), (1, "fma"), (2, "mfma"), (3, "mix")):
-        _lib.call("p3d_probe_issue_rates", kind, 64, blocks, cycles.data_ptr(), stream.cuda_stream)
-        ms = time_events(lambda: _lib.call("p3d_probe_issue_rates", kind, iters, blocks, cycles.data_ptr(),
-                                           stream.cuda_stream), 3, stream)
-        sec = ms * 1e-3
-        lanes = waves * 64 * iters * 16
-        mfma_flops = waves * iters * 4 * 32 * 32 * 16 * 2
-        if name == "exp":
-            res["exp_per_s"] = lanes / sec
-        elif name == "fma":
-            res["fma_per_s"] = lanes / sec
-        elif name == "mfma":
-            res["mfma_tflops"] = mfma_flops / sec / 1e12
-        else:
-            res["mix_mfma_tflops"] = mfma_flops / sec / 1e12
-            res["mix_exp_per_s"] = lanes / sec
-    return {k: float(f"{v:.4g}") for k, v in res.items()} | {"cus": cus, "waves_per_simd": 2}
+    iters = 4096
+    kinds = {0: "16 exp", 1: "16 fma", 2: "4 mfma", 3: "16 exp + 4 mfma",
+             4: "summary tile pattern (2 tiles x 2 blocks: 14 mfma, 32 exp, 16 cvt)"}
+    res = {"cus": cus, "iters": iters, "runs": []}
+    for wps in (1, 2, 4):
+        blocks = wps * cus
+        waves = blocks * 4
+        cycles = torch.zeros(2 * waves, dtype=torch.int64, device=dev)
+        for kind, name in kinds.items():
+            if kind == 4 and wps > 2:
+                continue  # its registers allow at most 3 waves per SIMD
+            run = lambda: _lib.call("p3d_probe_issue_rates", kind, iters, blocks, cycles.data_ptr(),
+                                    stream.cuda_stream)
+            _lib.call("p3d_probe_issue_rates", kind, 64, blocks, cycles.data_ptr(), stream.cuda_stream)
+            ms = time_events(run, 3, stream)
+            c = cycles.view(-1, 2).double().sum(0).tolist()
+            ghz = c[0] / c[1] * 0.1  # shader cycles per 10 ns tick -> GHz
+            per_simd = waves * iters / (4 * cus)
+            line = {"kind": name, "waves_per_simd": wps, "ms": round(ms, 4), "ghz": round(ghz, 3),
+                    "simd_cycles_per_wave_iter": round(ms * 1e-3 * ghz * 1e9 / per_simd, 1)}
+            if kind in (0, 1):
+                line["lanes_per_s"] = float(f"{waves * 64 * iters * 16 / (ms * 1e-3):.4g}")
+            if kind == 2:
+                line["mfma_tflops"] = round(waves * iters * 4 * 32 * 32 * 16 * 2 / (ms * 1e-3) / 1e12, 1)
+            res["runs"].append(line)
+    return res
 
 
 def main():

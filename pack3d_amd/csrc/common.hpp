@@ -82,6 +82,12 @@ struct Mma<__bf16> {
     __device__ __forceinline__ static f32x16 mfma(Frag a, Frag b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
     }
+    // v_mfma_f32_16x16x32: D[16x16] = A[16x32] B[32x16] + C; lane l holds A
+    // row / B column l % 16 and k = 8 (l / 16) + j; register r of lane l
+    // holds D[4 (l / 16) + r][l % 16].
+    __device__ __forceinline__ static f32x4 mfma16(Frag a, Frag b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
 };
 
 template <>
@@ -91,6 +97,9 @@ struct Mma<_Float16> {
     typedef f16x8 Frag;
     __device__ __forceinline__ static f32x16 mfma(Frag a, Frag b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    __device__ __forceinline__ static f32x4 mfma16(Frag a, Frag b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
     }
 };
 

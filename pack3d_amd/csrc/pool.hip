@@ -12,6 +12,7 @@
 // forms its column sums with one lane per column dword (column_sums_w).  The
 // coarse mean divides by the number of non-empty fine blocks.
 #include <algorithm>
+#include <type_traits>
 
 #include "rope.hpp"
 
@@ -177,26 +178,31 @@ __device__ __forceinline__ uint4 round_piece<_Float16, 8>(float (&x)[8]) {
 
 // ------------------------------------------------------------------ forward
 //
-// One wave pools one (batch, kv head, summary) item at a time.  The K and V
-// rows of a fine block are loaded with 16 bytes per lane and consecutive
-// lanes on consecutive pieces of a row, so one load instruction covers whole
-// row spans, and are written to the wave's LDS buffer as rows.  The loads of
-// the wave's next fine block are issued into the same registers right after
-// that, before any arithmetic: the HBM latency of one step hides behind the
-// arithmetic of the step before it.  Each lane then takes its own slot's
-// rows (lane = slot): rotate the key, round it to the storage type, form the
-// slot logit, and take the slot softmax as a wave reduction.
+// One wave pools one (batch, kv head, summary) item at a time, one fine block
+// (a "step") after the other.  Each lane holds one slot (lane = slot).
 //
-// The weighted sums over the 64 slots, sum_s a_s k_s and sum_s a_s v_s, are
-// a matrix-vector product.  For 2-byte types each lane writes its rotated,
-// rounded K row back over its staged row (the V rows stay as staged), and
-// the MFMA computes W X with W = [hi(a); lo(a)] (the weights split into two
-// storage-type parts, hi = round(a), lo = round(a - hi)) and X the staged
-// [64 slots x (K | V)] rows.  Its B operand needs 8 consecutive slots of one
-// channel per lane, read straight out of the row-major rows with
+// The K and V rows of a step are loaded with 16 bytes per lane and
+// consecutive lanes on consecutive pieces of a row, so one load instruction
+// covers whole row spans, and are written to the wave's LDS buffer as rows.
+// (Loading each lane's own K row instead, 64 rows per load instruction, was
+// measured slower.)  The loads of the wave's next step are issued into the
+// prefetch registers early in a step, so their HBM latency hides behind that
+// step's arithmetic.  Each lane reads its own slot's K row back, rotates it,
+// rounds it to the storage type (the reference pools rotated keys stored in
+// that type), forms the slot logit, and the slot softmax is a wave
+// reduction.
+//
+// 2-byte types: the rotated, rounded K row is written back over its staged
+// row, and the weighted sums over the 64 slots, sum_s a_s k_s and
+// sum_s a_s v_s, run on MFMA: D = W X with W = [hi(a); lo(a)] (the weights
+// split into two storage-type parts, hi = round(a), lo = round(a - hi)) and X
+// the staged [64 slots x (K | V)] rows.  Its B operand needs 8 consecutive
+// slots of one channel per lane, read straight out of the row-major rows with
 // ds_read_b64_tr_b16 (two per fragment).  Each product of two storage-type
 // values is exact in fp32 and the sum carries a with 16 significant bits.
-// fp32 rows are summed across lanes by a reduce-scatter butterfly instead.
+//
+// fp32: each lane also reads its own V row, and the sums are taken across
+// lanes by a reduce-scatter butterfly.
 
 template <typename T, int D>
 struct PoolRowCfg {
@@ -206,11 +212,11 @@ struct PoolRowCfg {
     static constexpr int PFN = (PPR + 3) & ~3;       // run flags, padded to 16 bytes
     static constexpr int RB = D * (int)sizeof(T);    // row bytes
     static constexpr int ROWS_BYTES = 2 * 64 * RB;   // K rows, then V rows
-    // MFMA path: the rows, then the weight rows hi, lo and a zero row (64 slots each).
-    static constexpr int WAVE_BYTES = MF ? ROWS_BYTES + 3 * 64 * 2 : ROWS_BYTES;
+    // MFMA path: the rows, then the weight rows hi and lo (64 slots each).
+    static constexpr int WAVE_BYTES = MF ? ROWS_BYTES + 2 * 64 * 2 : ROWS_BYTES;
     static constexpr int MAX_WAVES = (159 * 1024) / WAVE_BYTES < 8 ? (159 * 1024) / WAVE_BYTES : 8;
     static constexpr int VOFF = 64 * RB;             // where the V rows are staged
-    static constexpr int NT = 2 * D / 32;            // 32-channel MFMA tiles of [k; v]
+    static constexpr int NT = 2 * D / 16;            // 16-channel MFMA tiles of [k; v]
     static constexpr int NCH = D / 16;               // 16-channel chunks of the butterfly
     static constexpr int PPC = 16 / EP;              // pieces per chunk
     static constexpr int NACC = MF ? NT : NCH;       // per-lane partial sums
@@ -270,8 +276,8 @@ __device__ __forceinline__ void unpack_piece(const u32x4& raw, float (&x)[EP]) {
 }
 
 // Store the summary of (batch * kv head bg, summary m) from the lane's sums
-// acc (over the fine blocks of the summary).  MFMA layout: lanes 0..31 hold
-// channel 32 t + l of [k; v] in acc[t].  Butterfly layout: lane l holds
+// acc (over the fine blocks of the summary).  MFMA layout: lanes 0..15 hold
+// channel 16 t + l of [k; v] in acc[t].  Butterfly layout: lane l holds
 // channel 16 k + 8 b4 + 4 b3 + 2 b2 + b1 of tensor b5 in acc[k] (even lanes
 // store).  The coarse stage divides the group sum by the count of non-empty
 // fine blocks (compression.py:42-43); keys are stored times key_scale.
@@ -287,16 +293,17 @@ __device__ __forceinline__ void store_summary(const PoolDev& a, int bg, int m, i
         int c;
         bool is_v, writer;
         if constexpr (C::MF) {
-            const int cc = 32 * k + lane;
+            const int cc = 16 * k + lane;
             is_v = cc >= D;
             c = is_v ? cc - D : cc;
-            writer = lane < 32;
+            writer = lane < 16;
         } else {
             c = 16 * k + 8 * ((lane >> 4) & 1) + 4 * ((lane >> 3) & 1) + 2 * ((lane >> 2) & 1) + ((lane >> 1) & 1);
             is_v = lane & 32;
             writer = !(lane & 1);
         }
-        const float mean = count ? acc[k] / (float)count : 0.f;
+        // count is wave-uniform: one fine block (pool_size 1) takes no division.
+        const float mean = count == 1 ? acc[k] : (count ? acc[k] / (float)count : 0.f);
         if (writer && !is_v) {
             const T x = from_f32<T>(mean * a.key_scale);
             sk[c] = x;
@@ -334,23 +341,23 @@ __device__ __forceinline__ void pool_fetch(const PoolDev& a, unsigned i, int idx
     }
 }
 
-// MFMA B operand for k-step ks and 32-channel tile t of [K | V] (2-byte
-// types): lane L holds channel 32 t + L % 32 for slots 16 ks + 8 (L / 32) ..
-// + 8, read from the row-major staged rows by two ds_read_b64_tr_b16.  Within
-// a 16-lane block, lane B + 4a + e receives element e of the 8-byte windows
-// addressed by lanes B + a + 4j (j = 0..3), so lane L addresses slot
-// 16 ks + 8 (L / 32) + (L % 16) / 4 (four slots further for the second read)
-// at channel 32 t + 16 ((L / 16) % 2) + 4 (L % 4) of K or, past D, of V.
-// D is a multiple of 16, so no 4-channel window straddles K and V.
+// MFMA B operand (16x16x32) for k-step ks and 16-channel tile t of [K | V]
+// (2-byte types): lane L holds channel 16 t + L % 16 for slots
+// 32 ks + 8 (L / 16) .. + 8, read from the row-major staged rows by two
+// ds_read_b64_tr_b16.  Within a 16-lane block, lane B + 4a + e receives
+// element e of the 8-byte windows addressed by lanes B + a + 4j (j = 0..3),
+// so lane L addresses slot 32 ks + 8 (L / 16) + (L % 16) / 4 (four slots
+// further for the second read) at channel 16 t + 4 (L % 4) of K or, past D,
+// of V.  D is a multiple of 16, so no tile straddles K and V.
 template <typename T, int D>
 __device__ __forceinline__ typename Mma<T>::Frag pool_frag_tr(const unsigned char* rows, int ks, int t, int lane) {
     typedef PoolRowCfg<T, D> C;
     typedef short v4s __attribute__((ext_vector_type(4)));
     typedef short v8s __attribute__((ext_vector_type(8)));
     typedef __attribute__((address_space(3))) v4s* lds_v4s;
-    const int slot = 16 * ks + 8 * (lane >> 5) + ((lane & 15) >> 2);
-    const int ch = 32 * t + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    const unsigned char* base = ch < D ? rows + ch * 2 : rows + C::VOFF + (ch - D) * 2;
+    const int slot = 32 * ks + 8 * (lane >> 4) + ((lane & 15) >> 2);
+    const int ch = 16 * t + 4 * (lane & 3);
+    const unsigned char* base = 16 * t < D ? rows + ch * 2 : rows + C::VOFF + (ch - D) * 2;
     const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + slot * C::RB));
     const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + (slot + 4) * C::RB));
     const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -380,7 +387,7 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
     const int tab_dw = TAB_LDS ? ((a.table_entries * 2 + 3) & ~3) : 0;
     unsigned char* rows = reinterpret_cast<unsigned char*>(reinterpret_cast<uint32_t*>(ltab) + tab_dw) +
                           (size_t)wave * C::WAVE_BYTES;
-    T* wrows = reinterpret_cast<T*>(rows + C::ROWS_BYTES);  // MFMA path: weight rows hi, lo, 0
+    T* wrows = reinterpret_cast<T*>(rows + C::ROWS_BYTES);  // MFMA path: weight rows hi, lo
     for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(a.rope.pairs, j);
     // Piece p is a table run when its pairs read consecutive entries with one
     // stride vector: entry(j0 + t) = entry(j0) + t for every position.
@@ -407,8 +414,8 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
     // item arithmetic is 32-bit scalar code.
     const unsigned total = (unsigned)a.B * a.G * a.Mp;
     const unsigned stride = gridDim.x * waves;
-    unsigned it = blockIdx.x * waves + wave;
-    if (it >= total) return;
+    const unsigned it0 = blockIdx.x * waves + wave;
+    if (it0 >= total) return;
 
     // Waves walk the items from the last one down (item = total - 1 - i for
     // the i-th of the walk): the projections that write kg / vg just before
@@ -435,165 +442,194 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
                      __builtin_amdgcn_readfirstlane(m0.z), __builtin_amdgcn_readfirstlane(m0.w)};
         runs |= (unsigned)(__builtin_amdgcn_readfirstlane(prun[p]) != 0) << p;
     }
-    u32x4 pk[PPR], pv[PPR];
-    // MFMA path: lane l supplies weight row min(l % 32, 2) of the A operand.
-    const T* wsrc = wrows + 64 * min(lane & 31, 2);
-    if constexpr (C::MF) wrows[128 + lane] = from_f32<T>(0.f);
+    if constexpr (C::MF) wrows[lane] = from_f32<T>(0.f);  // weight rows before the first step's sync
 
-    int fl = 0, ns = steps_of(it);
-    int idx = row_of(it, 0);
-    int pos[3];
-    rope_position32(a.rope, max(idx, 0), pos);
-    pool_fetch<T, D>(a, item_of(it), idx, lane, pk, pv);
-    unsigned it1 = ns > 1 ? it : it + stride;
-    int fl1 = ns > 1 ? 1 : 0;
-    int idx1 = it1 < total ? row_of(it1, fl1) : -1;
-    float acc[C::NACC];
+    // For 2-byte types the loop is compiled twice: once for tables whose
+    // pieces are all runs (every (cos, sin) entry of a piece at e0 + t, no
+    // per-pair metadata and no branch, so all the table reads of a step issue
+    // together), once for the general pair order.
+    auto pool_loop = [&](auto all_runs_tag) __attribute__((always_inline)) {
+        constexpr bool ALL_RUNS = decltype(all_runs_tag)::value;
+        u32x4 pk[PPR], pv[PPR];
+        unsigned it = it0;
+        int fl = 0, ns = steps_of(it);
+        int idx = row_of(it, 0);
+        int pos[3];
+        rope_position32(a.rope, max(idx, 0), pos);
+        pool_fetch<T, D>(a, item_of(it), idx, lane, pk, pv);
+        unsigned it1 = ns > 1 ? it : it + stride;
+        int fl1 = ns > 1 ? 1 : 0;
+        int idx1 = it1 < total ? row_of(it1, fl1) : -1;
+        float acc[C::NACC];
 #pragma unroll
-    for (int k = 0; k < C::NACC; ++k) acc[k] = 0.f;
-    int count = 0;
-    // The summary of a finished item is stored in the next step, after that
-    // step's rows are staged and before the loads of the step after it are
-    // issued, so the wait for those loads never waits on the stores.
-    bool pending = false;
-    int pend_bg = 0, pend_m = 0, pend_count = 0;
-    float pend[C::NACC];
-    for (;;) {
-        // Stage this step's pieces as rows (slot s at s * RB).
+        for (int k = 0; k < C::NACC; ++k) acc[k] = 0.f;
+        int count = 0;
+        // The summary of a finished item is stored in the next step, after that
+        // step's rows are staged and before the loads of the step after it are
+        // issued, so the wait for those loads never waits on the stores.
+        bool pending = false;
+        int pend_bg = 0, pend_m = 0, pend_count = 0;
+        float pend[C::NACC];
+        for (;;) {
+            // Stage this step's pieces as rows (slot s at s * RB).
 #pragma unroll
-        for (int r = 0; r < PPR; ++r) {
-            const int q = r * 64 + lane;
-            *reinterpret_cast<u32x4*>(rows + q * 16) = pk[r];
-            *reinterpret_cast<u32x4*>(rows + C::VOFF + q * 16) = pv[r];
-        }
-        wave_lds_sync();
-        if (pending) {
-            store_summary<T, D>(a, pend_bg, pend_m, lane, pend_count, pend);
-            pending = false;
-        }
-        // The lane's own K row (and V row for the fp32 butterfly).
-        u32x4 kr[PPR], vr[PPR];
-#pragma unroll
-        for (int p = 0; p < PPR; ++p) {
-            kr[p] = *reinterpret_cast<const u32x4*>(rows + lane * RB + p * 16);
-            if constexpr (!C::MF) vr[p] = *reinterpret_cast<const u32x4*>(rows + C::VOFF + lane * RB + p * 16);
-        }
-        // Next step's coordinates, the block-table row after it, then the next
-        // step's rows.  The load counter completes in issue order, and the
-        // coordinates and table row are carried into the next iteration (a
-        // register copy that must wait for them): issued before the rows,
-        // that wait leaves the row loads in flight under this step's
-        // arithmetic instead of draining them at the end of the step.
-        const bool more = it1 < total;
-        int ns1 = 1, pos1[3] = {0, 0, 0}, idx2 = -1;
-        unsigned it2 = total;
-        int fl2 = 0;
-        if (more) {
-            ns1 = steps_of(it1);
-            rope_position32(a.rope, max(idx1, 0), pos1);
-            it2 = fl1 + 1 < ns1 ? it1 : it1 + stride;
-            fl2 = fl1 + 1 < ns1 ? fl1 + 1 : 0;
-            if (it2 < total) idx2 = row_of(it2, fl2);
-            pool_fetch<T, D>(a, item_of(it1), idx1, lane, pk, pv);
-        }
-
-        if (__ballot(idx >= 0) != 0) {  // empty fine block: no mass, no count
-            ++count;
-            // Rotate the slot's key, round it to the storage type, and form its
-            // logit (compression.py:31-35): (k . w) / tau + bias_s.
-            float dot = 0.f;
+            for (int r = 0; r < PPR; ++r) {
+                const int q = r * 64 + lane;
+                *reinterpret_cast<u32x4*>(rows + q * 16) = pk[r];
+                *reinterpret_cast<u32x4*>(rows + C::VOFF + q * 16) = pv[r];
+            }
+            wave_lds_sync();
+            if (pending) {
+                store_summary<T, D>(a, pend_bg, pend_m, lane, pend_count, pend);
+                pending = false;
+            }
+            // The lane's own K row (and V row for the fp32 butterfly).
+            u32x4 kr[PPR], vr[PPR];
 #pragma unroll
             for (int p = 0; p < PPR; ++p) {
-                float kx[EP];
-                unpack_piece<T, EP>(kr[p], kx);
-                const int e0 = pm[p].x + mul_u24(pm[p].y, pos[0]) + mul_u24(pm[p].z, pos[1]) +
-                               mul_u24(pm[p].w, pos[2]);
-                float2 cs[EP / 2];
-                if (runs >> p & 1) {
+                kr[p] = *reinterpret_cast<const u32x4*>(rows + lane * RB + p * 16);
+                if constexpr (!C::MF) vr[p] = *reinterpret_cast<const u32x4*>(rows + C::VOFF + lane * RB + p * 16);
+            }
+            // Next step's coordinates, the block-table row after it, then the
+            // next step's rows.  The load counter completes in issue order, and
+            // the coordinates and table row are carried into the next iteration
+            // (a register copy that must wait for them): issued before the rows,
+            // that wait leaves the row loads in flight under this step's
+            // arithmetic instead of draining them at the end of the step.
+            const bool more = it1 < total;
+            int ns1 = 1, pos1[3] = {0, 0, 0}, idx2 = -1;
+            unsigned it2 = total;
+            int fl2 = 0;
+            if (more) {
+                ns1 = steps_of(it1);
+                rope_position32(a.rope, max(idx1, 0), pos1);
+                it2 = fl1 + 1 < ns1 ? it1 : it1 + stride;
+                fl2 = fl1 + 1 < ns1 ? fl1 + 1 : 0;
+                if (it2 < total) idx2 = row_of(it2, fl2);
+                pool_fetch<T, D>(a, item_of(it1), idx1, lane, pk, pv);
+            }
+
+            if (__ballot(idx >= 0) != 0) {  // empty fine block: no mass, no count
+                ++count;
+                // Rotate the slot's key, round it to the storage type, and form
+                // its logit (compression.py:31-35): (k . w) / tau + bias_s.
+                // 2-byte types read every (cos, sin) entry of the step first (one
+                // batch of LDS reads); fp32 rows, twice as many pieces, read them
+                // piece by piece.
+                float2 cs[C::MF ? PPR : 1][EP / 2];
+                auto table_piece = [&](int p, float2(&c)[EP / 2]) __attribute__((always_inline)) {
+                    const int e0 = pm[p].x + mul_u24(pm[p].y, pos[0]) + mul_u24(pm[p].z, pos[1]) +
+                                   mul_u24(pm[p].w, pos[2]);
+                    if (ALL_RUNS || (runs >> p & 1)) {
 #pragma unroll
-                    for (int t = 0; t < EP / 2; ++t) cs[t] = tab[e0 + t];
+                        for (int t = 0; t < EP / 2; ++t) c[t] = tab[e0 + t];
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < EP / 2; ++t) c[t] = pair_cs(meta[p * EP / 2 + t], tab, pos);
+                    }
+                };
+                if constexpr (C::MF) {
+#pragma unroll
+                    for (int p = 0; p < PPR; ++p) table_piece(p, cs[p]);
+                }
+                float dot = 0.f;
+#pragma unroll
+                for (int p = 0; p < PPR; ++p) {
+                    float2(&c)[EP / 2] = cs[C::MF ? p : 0];
+                    if constexpr (!C::MF) table_piece(p, c);
+                    float kx[EP];
+                    unpack_piece<T, EP>(kr[p], kx);
+#pragma unroll
+                    for (int t = 0; t < EP / 2; ++t) rotate_pair(kx[2 * t], kx[2 * t + 1], c[t].x, c[t].y);
+                    kr[p] = __builtin_bit_cast(u32x4, round_piece<T, EP>(kx));
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) dot += kx[e] * lweight[p * EP + e];
+                }
+                const float logit = idx >= 0 ? dot * a.inv_tau + lbias[lane] : -INFINITY;
+                const float mx = wave_max(logit);
+                const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
+                const float wgt = ex / wave_sum(ex);
+                if constexpr (C::MF) {
+                    typedef typename Mma<T>::Frag Frag;
+                    // The rotated, rounded key over the lane's own staged row (only
+                    // this lane has read it).
+#pragma unroll
+                    for (int p = 0; p < PPR; ++p) *reinterpret_cast<u32x4*>(rows + lane * RB + p * 16) = kr[p];
+                    const T hi = from_f32<T>(wgt);
+                    wrows[lane] = hi;
+                    wrows[64 + lane] = from_f32<T>(wgt - to_f32(hi));
+                    wave_lds_sync();
+                    // D[w][c] = sum_s W[w][s] X[s][c] for the weight rows w = 0
+                    // (hi), 1 (lo), over 32 slots per instruction: lane l holds
+                    // slots 8 (l / 16) + j of channel l % 16 (B) and, for
+                    // l % 16 < 2, of weight row l % 16 (A); rows 0 and 1 of D
+                    // are registers 0 and 1 of lanes 0..15.
+                    const int wr = lane & 15;
+                    Frag wa[2];
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const u32x4 w = *reinterpret_cast<const u32x4*>(wrows + 64 * (wr & 1) + 32 * ks + 8 * (lane >> 4));
+                        wa[ks] = __builtin_bit_cast(Frag, wr < 2 ? w : u32x4{0u, 0u, 0u, 0u});
+                    }
+                    Frag xb[2][C::NT];
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                        for (int t = 0; t < C::NT; ++t) xb[ks][t] = pool_frag_tr<T, D>(rows, ks, t, lane);
+#pragma unroll
+                    for (int t = 0; t < C::NT; ++t) {
+                        f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) d = Mma<T>::mfma16(wa[ks], xb[ks][t], d);
+                        acc[t] += d[0] + d[1];
+                    }
                 } else {
 #pragma unroll
-                    for (int t = 0; t < EP / 2; ++t) cs[t] = pair_cs(meta[p * EP / 2 + t], tab, pos);
-                }
+                    for (int k = 0; k < NCH; ++k) {
+                        float kv[16], vv[16];
 #pragma unroll
-                for (int t = 0; t < EP / 2; ++t) rotate_pair(kx[2 * t], kx[2 * t + 1], cs[t].x, cs[t].y);
-                kr[p] = __builtin_bit_cast(u32x4, round_piece<T, EP>(kx));
+                        for (int t = 0; t < PPC; ++t) {
+                            float xk[EP], xv[EP];
+                            unpack_piece<T, EP>(kr[k * PPC + t], xk);
+                            unpack_piece<T, EP>(vr[k * PPC + t], xv);
 #pragma unroll
-                for (int e = 0; e < EP; ++e) dot += kx[e] * lweight[p * EP + e];
-            }
-            const float logit = idx >= 0 ? dot * a.inv_tau + lbias[lane] : -INFINITY;
-            const float mx = wave_max(logit);
-            const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
-            const float wgt = ex / wave_sum(ex);
-            if constexpr (C::MF) {
-                typedef typename Mma<T>::Frag Frag;
-                // The rotated, rounded key over the lane's own staged row (only
-                // this lane has read it).
-#pragma unroll
-                for (int p = 0; p < PPR; ++p) *reinterpret_cast<u32x4*>(rows + lane * RB + p * 16) = kr[p];
-                const T hi = from_f32<T>(wgt);
-                wrows[lane] = hi;
-                wrows[64 + lane] = from_f32<T>(wgt - to_f32(hi));
-                wave_lds_sync();
-                // D[w][c] = sum_s W[w][s] X[s][c] for the weight rows w = 0
-                // (hi), 1 (lo), over 16 slots per instruction: lane l holds
-                // slots 8 (l / 32) + j of channel l % 32 (B) and, for l % 32 <
-                // 2, of weight row l % 32 (A); rows 0 and 1 of D are
-                // registers 0 and 1 of lanes 0..31.
-                const int g = lane >> 5;
-                f32x16 d[C::NT];
-#pragma unroll
-                for (int t = 0; t < C::NT; ++t)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) d[t][r] = 0.f;
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const Frag wa = __builtin_bit_cast(Frag, *reinterpret_cast<const u32x4*>(wsrc + 16 * ks + 8 * g));
-#pragma unroll
-                    for (int t = 0; t < C::NT; ++t) d[t] = Mma<T>::mfma(wa, pool_frag_tr<T, D>(rows, ks, t, lane), d[t]);
-                }
-#pragma unroll
-                for (int t = 0; t < C::NT; ++t) acc[t] += d[t][0] + d[t][1];
-            } else {
-#pragma unroll
-                for (int k = 0; k < NCH; ++k) {
-                    float kv[16], vv[16];
-#pragma unroll
-                    for (int t = 0; t < PPC; ++t) {
-                        float xk[EP], xv[EP];
-                        unpack_piece<T, EP>(kr[k * PPC + t], xk);
-                        unpack_piece<T, EP>(vr[k * PPC + t], xv);
-#pragma unroll
-                        for (int e = 0; e < EP; ++e) {
-                            kv[t * EP + e] = wgt * xk[e];
-                            vv[t * EP + e] = wgt * xv[e];
+                            for (int e = 0; e < EP; ++e) {
+                                kv[t * EP + e] = wgt * xk[e];
+                                vv[t * EP + e] = wgt * xv[e];
+                            }
                         }
+                        acc[k] += butterfly_sum(kv, vv, lane);
                     }
-                    acc[k] += butterfly_sum(kv, vv, lane);
                 }
             }
-        }
-        if (fl + 1 == ns) {
-            const unsigned bm = item_of(it) / a.G;
-            pending = true;
-            pend_bg = (int)(bm / a.Mp) * a.G + (int)(item_of(it) % a.G);
-            pend_m = (int)(bm % a.Mp);
-            pend_count = count;
+            if (fl + 1 == ns) {
+                const unsigned bm = item_of(it) / a.G;
+                pending = true;
+                pend_bg = (int)(bm / a.Mp) * a.G + (int)(item_of(it) % a.G);
+                pend_m = (int)(bm % a.Mp);
+                pend_count = count;
 #pragma unroll
-            for (int k = 0; k < C::NACC; ++k) {
-                pend[k] = acc[k];
-                acc[k] = 0.f;
+                for (int k = 0; k < C::NACC; ++k) {
+                    pend[k] = acc[k];
+                    acc[k] = 0.f;
+                }
+                count = 0;
             }
-            count = 0;
+            if (!more) break;
+            wave_lds_sync();  // the next step's staging overwrites the rows
+            it = it1, fl = fl1, ns = ns1, idx = idx1;
+            pos[0] = pos1[0], pos[1] = pos1[1], pos[2] = pos1[2];
+            it1 = it2, fl1 = fl2, idx1 = idx2;
         }
-        if (!more) break;
-        wave_lds_sync();  // the next step's staging overwrites the rows
-        it = it1, fl = fl1, ns = ns1, idx = idx1;
-        pos[0] = pos1[0], pos[1] = pos1[1], pos[2] = pos1[2];
-        it1 = it2, fl1 = fl2, idx1 = idx2;
+        if (pending) store_summary<T, D>(a, pend_bg, pend_m, lane, pend_count, pend);
+    };
+    if constexpr (C::MF) {
+        if (runs == (1u << PPR) - 1u) {
+            pool_loop(std::true_type{});
+            return;
+        }
     }
-    if (pending) store_summary<T, D>(a, pend_bg, pend_m, lane, pend_count, pend);
+    pool_loop(std::false_type{});
 }
 
 // Pooling backward (the VJP of compression.py:28-44; kernels.py:240-270 of

@@ -71,37 +71,101 @@ def time_events(fn, iters, stream):
     return start.elapsed_time(end) / iters
 
 
-def kernel_times_in_layer(layer, x, layout, steps, stream):
-    """Mean durations (ms) of the pool and attention launches within layer steps."""
+class _TimedLib:
+    """The loaded library with HIP events on the launch stream around the
+    named entry points."""
+
+    def __init__(self, real, names, mark):
+        self._real, self._names, self._mark = real, names, mark
+
+    def __getattr__(self, name):
+        fn = getattr(self._real, name)
+        if name not in self._names:
+            return fn
+
+        def timed(*args):
+            self._mark(name)
+            rc = fn(*args)
+            self._mark(name)
+            return rc
+        return timed
+
+
+def kernel_times_in_layer(layer, x, layout, steps, stream, fused=True):
+    """Mean durations (ms) of the layer's launches within layer steps, by
+    name: "p3d_project_pool" (projections with the pooling fused in) or
+    "p3d_project" and "pool" (the unfused path, fused=False), and "attention"."""
+    import pack3d_amd.attention as attention
+    from pack3d_amd import _lib
     from pack3d_amd.core import ForwardPlan
 
-    marks = []
-    orig_pool, orig_attn = ForwardPlan.pool, ForwardPlan.attention
+    marks = {}
 
-    def mark():
+    def mark(name):
         ev = torch.cuda.Event(enable_timing=True)
         ev.record(stream)
-        marks.append(ev)
+        marks.setdefault(name, []).append(ev)
+
+    orig = ForwardPlan.pool, ForwardPlan.attention, _lib.lib, attention.pooled_core
 
     def pool(self):
-        mark()
-        orig_pool(self)
-        mark()
+        mark("pool")
+        orig[0](self)
+        mark("pool")
 
-    def attention(self):
-        mark()
-        orig_attn(self)
-        mark()
+    def attn(self):
+        mark("attention")
+        orig[1](self)
+        mark("attention")
 
-    ForwardPlan.pool, ForwardPlan.attention = pool, attention
+    timed = _TimedLib(orig[2](), ("p3d_project_pool", "p3d_project"), mark)
+    ForwardPlan.pool, ForwardPlan.attention, _lib.lib = pool, attn, lambda: timed
+    if not fused:
+        attention.pooled_core = lambda *args: None
     try:
         for _ in range(steps):
             layer(x, layout)
     finally:
-        ForwardPlan.pool, ForwardPlan.attention = orig_pool, orig_attn
+        ForwardPlan.pool, ForwardPlan.attention, _lib.lib, attention.pooled_core = orig
     torch.cuda.synchronize()
-    spans = [marks[i].elapsed_time(marks[i + 1]) for i in range(0, len(marks), 2)]
-    return sum(spans[0::2]) / steps, sum(spans[1::2]) / steps
+    return {name: sum(ev[i].elapsed_time(ev[i + 1]) for i in range(0, len(ev), 2)) / steps
+            for name, ev in marks.items()}
+
+
+def layer_ms_unfused(layer, x, layout, steps):
+    """The layer step with the projection pooling switched off (p3d_project,
+    then p3d_pool_fwd and the attention), for comparison."""
+    import pack3d_amd.attention as attention
+
+    real = attention.pooled_core
+    attention.pooled_core = lambda *args: None
+    try:
+        for _ in range(5):
+            layer(x, layout)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            layer(x, layout)
+        torch.cuda.synchronize()
+        return 1000.0 * (time.perf_counter() - t0) / steps
+    finally:
+        attention.pooled_core = real
+
+
+def pool_alone_cold_ms(plan, reps, stream, device):
+    """k_pool_fwd alone, each launch after a 1 GiB fill that evicts the
+    caches (none of kg / vg is in the last-level cache when it starts)."""
+    flush = torch.empty(256 * 2 ** 20, dtype=torch.float32, device=device)
+    total = 0.0
+    for _ in range(reps):
+        flush.fill_(0.0)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        plan.pool()
+        end.record(stream)
+        end.synchronize()
+        total += start.elapsed_time(end)
+    return total / reps
 
 
 def summary_pathway_ms(plan, steps, stream):
@@ -358,15 +422,21 @@ def main():
         ms_layer = 1000.0 * (time.perf_counter() - t0) / a.steps
 
         # Per-kernel durations inside the same layer steps: HIP events on the
-        # launch stream around the pool and attention launches of each step
-        # (a second pass over the steps, so the first one runs without them).
-        ms_pool, ms_attn = kernel_times_in_layer(layer, x, layout, a.steps, stream)
+        # launch stream around the layer's launches (a second pass over the
+        # steps, so the first one runs without them); then the layer step with
+        # the projection pooling switched off, for comparison.
+        fused = kernel_times_in_layer(layer, x, layout, a.steps, stream)
+        if "p3d_project_pool" not in fused:
+            raise RuntimeError("the benchmark layer did not take the fused projection pooling")
+        ms_proj_pool, ms_attn = fused["p3d_project_pool"], fused["attention"]
+        ms_layer_unfused = layer_ms_unfused(layer, x, layout, a.steps)
         q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, layout)
         plan = ForwardPlan(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate, layer.local_scale,
                            layer.global_scale, layout.geometry, layer.temperature, rope, rope)
         plan.run()
         ms_core = time_events(plan.run, max(5, a.steps), stream)
         ms_summary = summary_pathway_ms(plan, a.steps, stream)
+        ms_pool_cold = pool_alone_cold_ms(plan, 20, stream, dev)
 
     m = layout.geometry.num_summaries
     edges = valid_edges(SHAPE, RADIUS)
@@ -376,7 +446,12 @@ def main():
     exps = HEADS * n * m + HEADS * edges  # one exponential per (query, summary) and per valid edge
     exp_rate = exps / (ms_attn * 1e-3)
     pool_bytes = 2 * KV_HEADS * n * HEAD_DIM * 2 + 2 * KV_HEADS * m * HEAD_DIM * 2
-    pool_gbs = pool_bytes / (ms_pool * 1e-3) / 1e9
+    pool_gbs = pool_bytes / (ms_pool_cold * 1e-3) / 1e9
+    # The fused projection kernel's compulsory HBM bytes: x read; q, kl, vl,
+    # the gate and the summaries written (the weights are a few hundred KB).
+    proj_pool_bytes = (n * DIM + n * HEADS * HEAD_DIM + 2 * n * KV_HEADS * HEAD_DIM + n * HEADS
+                       + 2 * KV_HEADS * m * HEAD_DIM) * 2
+    proj_pool_gbs = proj_pool_bytes / (ms_proj_pool * 1e-3) / 1e9
     cpu = None if a.no_cpu_baseline else cpu_baseline(SHAPE, a.cpu_threads)
     traffic = load_traffic()
     out = {
@@ -387,8 +462,10 @@ def main():
                    "dim": DIM, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM, "radius": RADIUS,
                    "block": list(BLOCK), "pool_size": 1, "summaries": m, "valid_edges": edges,
                    "tokens_per_s": round(n / (ms_layer * 1e-3)), "ms_layer": round(ms_layer, 4),
-                   "ms_core": round(ms_core, 4), "ms_pool_kernel": round(ms_pool, 4),
+                   "ms_core": round(ms_core, 4), "ms_project_pool_kernel": round(ms_proj_pool, 4),
                    "ms_attn_kernel": round(ms_attn, 4), "ms_summary_pathway": round(ms_summary, 4),
+                   "ms_layer_unfused": round(ms_layer_unfused, 4),
+                   "ms_pool_kernel_alone_cold": round(ms_pool_cold, 4),
                    "parallelism": "single GPU"},
         "roofline": {"kernel": "k_attn_grid (fused local+global forward)", "bound": "mfma",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
@@ -402,10 +479,17 @@ def main():
                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(flops_summary / (ms_summary * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                              "algorithmic_flops": flops_summary},
-        "roofline_pool": {"kernel": "k_pool_fwd", "bound": "hbm", "achieved": round(pool_gbs, 1),
+        "roofline_pool": {"kernel": "k_pool_fwd (the unfused pooling: training, other layouts), alone after a "
+                                    "1 GiB cache flush", "bound": "hbm", "achieved": round(pool_gbs, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(pool_gbs / PEAK_HBM_GBS, 4),
                           "traffic": traffic.get("pool_bytes_per_launch"),
                           "algorithmic_bytes": pool_bytes},
+        "roofline_project_pool": {"kernel": "k_project_pool (LayerNorm, projections, gate and summary pooling, "
+                                            "in the layer)", "bound": "hbm", "achieved": round(proj_pool_gbs, 1),
+                                  "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                  "frac": round(proj_pool_gbs / PEAK_HBM_GBS, 4),
+                                  "traffic": traffic.get("project_pool_bytes_per_launch"),
+                                  "algorithmic_bytes": proj_pool_bytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

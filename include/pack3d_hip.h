@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 11
+#define P3D_ABI_VERSION 12
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -284,6 +284,23 @@ typedef struct p3d_project_args {
 } p3d_project_args;
 
 int p3d_project(const p3d_project_args* args, void* stream);
+
+/* The projections of p3d_project with the summary pooling (compression.py:
+ * 28-44, the pooling p3d_pool_fwd performs) fused in, for the no-grad
+ * forward: writes q, kl, vl (the first 2 * kv_heads * head_dim columns of
+ * each kv row) and gate, and the summaries sk, svt and the key-norm slots of
+ * `pool`, from the kg and vg values it computes; the kg and vg columns of kv
+ * are left unwritten.  Replaces, in the layer's no-grad forward
+ * (attention.py:64-67 followed by the core's pooling, reference.py:13-14),
+ * the projections and the pooling pass over kg / vg.  Contract: the layout's
+ * fine block f of each batch is rows [64 f, 64 f + 64) of that batch (the
+ * blocks of this package's build_layout), pool_size 1, 64 slots; pool->kg,
+ * pool->vg and pool->blocks are not read.  Returns P3D_EUNSUPPORTED, before
+ * launching anything, for shapes outside head_dim 16/32/48/64, kv_heads *
+ * head_dim <= 192, tokens a multiple of 64 and dim 64/96/128/192/256 (the
+ * caller then runs p3d_project and p3d_pool_fwd); P3D_EINVAL for arguments
+ * either would reject. */
+int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, void* stream);
 
 /* Output projection with the residual (attention.py:89): out = x + y Wo^T for
  * y [rows, k] (the core's output, heads concatenated), Wo [dim, k] and x,

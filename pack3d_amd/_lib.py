@@ -17,6 +17,7 @@ LIB_PATH = os.environ.get("PACK3D_HIP_LIB") or os.path.join(os.path.dirname(os.p
 c_int32, c_int64, c_float, c_void_p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
 
 P3D_F32, P3D_F16, P3D_BF16 = 0, 1, 2
+P3D_EUNSUPPORTED = 3  # enum p3d_status
 DTYPES = {torch.float32: P3D_F32, torch.float16: P3D_F16, torch.bfloat16: P3D_BF16}
 
 
@@ -24,7 +25,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 11  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 12  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -99,6 +100,7 @@ SIGNATURES = {
                    c_int32),
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
     "p3d_project": ([ctypes.POINTER(ProjectArgs), _P], c_int32),
+    "p3d_project_pool": ([ctypes.POINTER(ProjectArgs), ctypes.POINTER(PoolArgs), _P], c_int32),
     "p3d_out_residual": ([_P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_layer_norm_train": ([_P, _P, _P, c_int32, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_float,
                               _P], c_int32),

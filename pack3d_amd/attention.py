@@ -4,7 +4,10 @@ Same constructor, parameters (names, shapes, initialisation order) and
 forward as ``PACK3DAttention`` of amilworks/Pack3D (``src/pack3d/attention.py``),
 with ``backend="hip"``.  In the no-grad forward (fp16 / bf16) LayerNorm,
 to_q, to_kv, the gate map and its softmax run as one kernel
-(``p3d_project``); with autograd active in fp16 / bf16 the linear maps are
+(``p3d_project``); on layouts whose fine blocks are consecutive 64-token runs
+with pool_size 1 (this package's ``build_layout``) that kernel also pools the
+summaries from the kg / vg values it computes (``p3d_project_pool``), and kg /
+vg never reach memory; with autograd active in fp16 / bf16 the linear maps are
 ``linear.InputProjections`` / ``linear.OutputResidual`` (torch GEMMs forward,
 weight gradients from ``p3d_weight_grad``); for fp32 models they are the
 torch modules (LayerNorm on the HIP kernel when no gradient is needed).  The
@@ -22,9 +25,9 @@ import torch
 from torch import nn
 
 from . import _lib
-from .core import SUPPORTED_HEAD_DIMS, pack3d_hip_projections
+from .core import SUPPORTED_HEAD_DIMS, ForwardPlan, _projection_views, _validate_inputs, pack3d_hip_projections
 from .linear import InputProjections, LayerNormTrain, OutputResidual, compute_dtype, layer_norm_train_supported
-from .geometry import TokenLayout
+from .geometry import TokenLayout, blocks_consecutive
 from .rope import axial_rope, balanced_pairs, packed_rope
 
 
@@ -55,12 +58,10 @@ def layer_norm(norm: nn.LayerNorm, x):
 PROJECT_DIMS = (64, 96, 128, 192, 256, 384, 512)
 
 
-def fused_projections(layer, x):
-    """(q [B,N,H*d], kv [B,N,4*G*d], gate [B,N,H]) of the no-grad forward from
-    one kernel (``p3d_project``): LayerNorm, to_q, to_kv, the gate map and its
-    pair softmax.  None when it does not apply (autograd active, fp32 or mixed
-    dtypes, a model width the kernel does not take); the caller then runs the
-    separate ops, which compute the same values."""
+def _project_buffers(layer, x):
+    """(argument block, q [B,N,H*d], kv [B,N,4*G*d], gate [B,N,H]) for the
+    fused projection kernels, or None when they do not apply (autograd
+    active, fp32 or mixed dtypes, a model width the kernels do not take)."""
     norm, lin = layer.norm, (layer.to_q, layer.to_kv, layer.gate)
     dt = x.dtype
     params = [norm.weight, norm.bias, *(m.weight for m in lin), layer.gate.bias]
@@ -84,8 +85,69 @@ def fused_projections(layer, x):
                             layer.gate.bias.data_ptr(), q.data_ptr(), kv.data_ptr(), gate.data_ptr(), b * n, layer.dim,
                             h * d, 4 * g * d, h, _lib.DTYPES[dt], _lib.DTYPES[norm.weight.dtype],
                             _lib.DTYPES[layer.gate.bias.dtype], float(norm.eps))
+    args._keep = xc
+    return args, q, kv, gate
+
+
+def fused_projections(layer, x):
+    """(q [B,N,H*d], kv [B,N,4*G*d], gate [B,N,H]) of the no-grad forward from
+    one kernel (``p3d_project``): LayerNorm, to_q, to_kv, the gate map and its
+    pair softmax.  None when it does not apply (autograd active, fp32 or mixed
+    dtypes, a model width the kernel does not take); the caller then runs the
+    separate ops, which compute the same values."""
+    made = _project_buffers(layer, x)
+    if made is None:
+        return None
+    args, q, kv, gate = made
     _lib.call("p3d_project", args, _lib.stream_of(x.device))
     return q, kv, gate
+
+
+POOLED_HEAD_DIMS = (16, 32, 48, 64)
+POOLED_DIMS = (64, 96, 128, 192, 256)
+
+
+def pooled_core(layer, x, layout):
+    """The core's output [B, H, N, d] (a transposed view of a [B, N, H, d]
+    buffer) of the no-grad forward with the summary pooling fused into the
+    projections (``p3d_project_pool``): q, kl, vl, the gate and the summaries
+    come from one kernel, kg and vg are never written, and the attention
+    kernels follow.  The same values as the projections, ``p3d_pool_fwd``
+    and the attention, up to the order of fp32 sums in the pooling.  None
+    when it does not apply: autograd active, fp32, pool_size other than 1,
+    fine blocks that are not the consecutive 64-token runs of
+    ``build_layout``, or shapes the kernel does not take; the caller then runs
+    the projections and the core separately."""
+    geometry = layout.geometry
+    h, g, d = layer.heads, layer.kv_heads, layer.head_dim
+    pool_params = (layer.pool_weight, layer.slot_bias, layer.local_scale, layer.global_scale)
+    if torch.is_grad_enabled() and any(p.requires_grad for p in pool_params):
+        return None
+    if (geometry.pool_size != 1 or d not in POOLED_HEAD_DIMS or g * d > 192 or layer.dim not in POOLED_DIMS
+            or not x.is_cuda or x.dtype not in (torch.float16, torch.bfloat16) or x.shape[1] % 64):
+        return None
+    made = _project_buffers(layer, x)
+    if made is None or not blocks_consecutive(geometry):
+        return None
+    args, qp, kvp, gp = made
+    q, kl, vl, kg, vg = _projection_views(qp, kvp, h, g)
+    inputs = (q, kl, vl, kg, vg, *pool_params[:2], gp.transpose(1, 2), *pool_params[2:])
+    _validate_inputs(*inputs, geometry, layer.temperature)
+    rope = layer._rope(x, layout)
+    plan = ForwardPlan(*inputs, geometry, layer.temperature, rope, rope)
+    m = geometry.num_summaries
+    if m % 32:
+        # Padding summaries up to the next multiple of 32: zero, as
+        # p3d_pool_fwd writes them (the fused kernel writes real ones only).
+        plan.sk[:, :, m:].zero_()
+        plan.svt[:, :, -1, :, m % 32:].zero_()
+    rc = _lib.lib().p3d_project_pool(args, plan.pool_args, _lib.stream_of(x.device))
+    if rc == _lib.P3D_EUNSUPPORTED:
+        return None
+    if rc != 0:
+        raise RuntimeError(f"p3d_project_pool failed ({rc}): {_lib.lib().p3d_last_error().decode()}")
+    plan.attention()
+    return plan.y
 
 
 def fused_out_residual(layer, x, y):
@@ -196,10 +258,12 @@ class PACK3DAttention(nn.Module):
         if self.backend != "hip":
             raise ValueError("unknown backend; implicit fallback is disabled")
         b, n = x.shape[0], x.shape[1]
-        qp, kvp, gate, res = self._projections(x)
-        out = pack3d_hip_projections(qp, kvp, self.heads, self.kv_heads, self.pool_weight, self.slot_bias, gate,
-                                     self.local_scale, self.global_scale, layout.geometry, self._rope(x, layout),
-                                     temperature=self.temperature)
+        out, res = pooled_core(self, x, layout), None
+        if out is None:
+            qp, kvp, gate, res = self._projections(x)
+            out = pack3d_hip_projections(qp, kvp, self.heads, self.kv_heads, self.pool_weight, self.slot_bias,
+                                         gate, self.local_scale, self.global_scale, layout.geometry,
+                                         self._rope(x, layout), temperature=self.temperature)
         # x + to_out(out): one kernel in the no-grad forward, else one GEMM with the
         # residual as its C operand (to_out has no bias), with a HIP weight gradient
         # in 16-bit training.

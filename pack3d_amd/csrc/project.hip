@@ -21,7 +21,9 @@
 // fragments of 32 different rows.  Outputs are rounded to the storage type,
 // as the linear maps' outputs are; the gate bias is added before that
 // rounding and the pair softmax runs in fp32 on the rounded logits.
-#include "common.hpp"
+#include <type_traits>
+
+#include "rope.hpp"
 
 namespace p3d {
 namespace {
@@ -48,6 +50,52 @@ __device__ __forceinline__ void store4(T* dst, const float (&v)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = from_f32<T>(v[i]);
     *reinterpret_cast<T4*>(dst) = o;
+}
+
+// LayerNorm of a wave's 32 tokens into the B fragments of the projection
+// GEMM: lane l holds token l % 32 and, for every 16-channel k-step ks,
+// channels 16 ks + 8 (l / 32) .. +8, normalised in fp32 (statistics shared
+// with lane l ^ 32, which holds the other half of the row) and rounded to
+// the storage type as torch's LayerNorm output is.  lw / lb: the affine
+// parameters in LDS as fp32.
+template <typename T, int KS>
+__device__ __forceinline__ void layer_norm_frags(const ProjDev& a, const float* lw, const float* lb, int64_t tok,
+                                                 bool live, int g, typename Mma<T>::Frag (&xf)[KS]) {
+    constexpr int DIM = 16 * KS;
+    const T* xr = reinterpret_cast<const T*>(a.x) + (live ? tok : 0) * DIM + 8 * g;
+    u32x4 raw[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(xr + 16 * ks);
+    float sum = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const T* v = reinterpret_cast<const T*>(&raw[ks]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum += to_f32(v[j]);
+    }
+    const float mean = (sum + lane_xor32(sum)) / (float)DIM;
+    float sq = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const T* v = reinterpret_cast<const T*>(&raw[ks]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float c = to_f32(v[j]) - mean;
+            sq = fmaf(c, c, sq);
+        }
+    }
+    const float rstd = 1.f / sqrtf((sq + lane_xor32(sq)) / (float)DIM + a.eps);
+    // Explicit fused multiply-adds: every kernel that normalises through here
+    // rounds the same way, whatever the compiler contracts elsewhere.
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        const T* v = reinterpret_cast<const T*>(&raw[ks]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int c = 16 * ks + 8 * g + j;
+            xf[ks][j] = from_f32<T>(fmaf((to_f32(v[j]) - mean) * rstd, lw[c], lb[c]));
+        }
+    }
 }
 
 // Waves per SIMD: 4 up to dim 128, 3 at dim 192 (the 168 registers that
@@ -102,41 +150,10 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + (threadIdx.x >> 6)) * 32, tok = tok0 + t;
     T* tile = otile[threadIdx.x >> 6];
     const bool live = tok < a.rows;
-    const T* xr = reinterpret_cast<const T*>(a.x) + (live ? tok : 0) * DIM + 8 * g;
 
     // ---- LayerNorm of the lane's half row (channels 16 ks + 8 g + j)
-    u32x4 raw[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(xr + 16 * ks);
-    float sum = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const T* v = reinterpret_cast<const T*>(&raw[ks]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sum += to_f32(v[j]);
-    }
-    const float mean = (sum + lane_xor32(sum)) / (float)DIM;
-    float sq = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const T* v = reinterpret_cast<const T*>(&raw[ks]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float c = to_f32(v[j]) - mean;
-            sq += c * c;
-        }
-    }
-    const float rstd = 1.f / sqrtf((sq + lane_xor32(sq)) / (float)DIM + a.eps);
     Frag xf[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const T* v = reinterpret_cast<const T*>(&raw[ks]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int c = 16 * ks + 8 * g + j;
-            xf[ks][j] = from_f32<T>((to_f32(v[j]) - mean) * rstd * lw[c] + lb[c]);
-        }
-    }
+    layer_norm_frags<T, KS>(a, lw, lb, tok, live, g, xf);
 
     // ---- D = W X^T, 32 outputs at a time
     T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
@@ -197,6 +214,381 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
             if (ob + 2 < nblocks) fetch(ob + 2);
         }
         __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- pooled
+// k_project with the summary pooling of compression.py:28-44 fused in, for
+// the no-grad forward on layouts whose fine block f of a batch is rows
+// [64 f, 64 f + 64) (the blocks of build_layout), pool_size 1 and 64 slots.
+// The kg / vg columns of kv are not written: in that forward their only
+// reader is the pooling, which happens here on the values in the kernel.
+//
+// The waves 2k and 2k + 1 of a workgroup hold the two halves of one fine
+// block.  The output blocks run in the order q | kl | vl | kg | vg | gate:
+//   q, kl, vl   written as in k_project;
+//   kg          each key rounded to the storage type (the value kv would
+//               hold), rotated and rounded again (the reference pools rotated
+//               keys stored in that type), into the wave's LDS rows;
+//   (after the last kg block) the slot logits (k . w) / tau + bias_s from
+//               those rows, the slot softmax over the fine block's 64 tokens
+//               with the maxima and then the sums exchanged between the two
+//               waves through LDS at workgroup barriers, and the weighted kg
+//               sums over the wave's 32 tokens on MFMA: weights split into
+//               two storage-type rows hi = round(a), lo = round(a - hi), so
+//               every product is exact in fp32, as in k_pool_fwd;
+//   vg          each block rounded through the wave's output tile and summed
+//               the same way;
+//   gate        as in k_project.
+// At the end the even wave adds its partner's sums and stores the summary
+// (keys times key_scale), its transposed value column and the key-norm slot
+// as k_pool_fwd stores them.
+struct PoolFuseDev {
+    int G, D, GD, Mp;
+    int tokens;       // per batch, a multiple of 64
+    int kg0;          // output row of kg's first channel: q_out + 2 G D
+    float inv_tau, key_scale;
+    const float* weight;  // pooling weight [D], fp32
+    const float* bias;    // slot bias [64], fp32
+    RopeDev rope;
+    char *sk, *svt;
+    float* norm;          // [B, G, 64] key-norm slots, zero on entry
+};
+
+constexpr int kPoolFuseMaxCh = 192;  // G * D: the kg rows of 8 waves fill most of the LDS
+
+// Dynamic LDS of k_project_pool (bytes), with KGS = G D + 8:
+//   rows  [waves][32][KGS] T   each wave's rotated, rounded kg rows; after
+//                              the kg sums, its fp32 sums [2][G D] (kg, vg)
+//                              and key squares [G D]
+//   wts   [waves][G][2][32] T  slot weights hi, lo of the wave's tokens
+//   xch   [waves][16] float    softmax maxima [8] and sums [8] per head
+//   meta  [D / 2] int4         rotary pair metadata
+//   lwp   [D] float, lbias [64] float
+inline size_t pool_fuse_lds_bytes(int G, int D) {
+    return (size_t)kProjWaves * 32 * (G * D + 8) * 2 + (size_t)kProjWaves * G * 64 * 2 + (size_t)kProjWaves * 16 * 4 +
+           (size_t)(D / 2) * 16 + (size_t)D * 4 + 64 * 4;
+}
+
+// Static LDS of k_project / k_project_pool at model width DIM (bytes).
+inline size_t project_static_lds_bytes(int dim) {
+    return (size_t)2 * dim * 4 + (size_t)2 * 32 * (dim + 8) * 2 + (size_t)kProjWaves * 32 * 40 * 2;
+}
+
+// sum_t (hi_t + lo_t) X[t][c0 + l] over a wave's 32 tokens, in lanes l < 16:
+// one 16x16x32 MFMA with A = the weight rows hi, lo (w: [2][32]) and B =
+// 16 channels of the row-major rows X (token t at x + t * stride, channel c0
+// at x), read with two ds_read_b64_tr_b16: within a 16-lane block, lane
+// B + 4a + e receives element e of the 8-byte windows addressed by lanes
+// B + a + 4j (j = 0..3), so lane L addresses token 8 (L / 16) + (L % 16) / 4
+// (four tokens further for the second read) at channel 4 (L % 4).
+template <typename T>
+__device__ __forceinline__ float slot_sum(const T* w, const T* x, int stride, int lane) {
+    typedef typename Mma<T>::Frag Frag;
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) v4s* lds_v4s;
+    const int r = lane & 15;
+    u32x4 wv = u32x4{0u, 0u, 0u, 0u};
+    if (r < 2) wv = *reinterpret_cast<const u32x4*>(w + 32 * r + 8 * (lane >> 4));
+    const int tk = 8 * (lane >> 4) + (r >> 2);
+    const unsigned char* base = reinterpret_cast<const unsigned char*>(x + 4 * (lane & 3));
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + tk * stride * 2));
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(base + (tk + 4) * stride * 2));
+    const v8s b = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const f32x4 d = Mma<T>::mfma16(__builtin_bit_cast(Frag, wv), __builtin_bit_cast(Frag, b), f32x4{0.f, 0.f, 0.f, 0.f});
+    return d[0] + d[1];
+}
+
+// v0 for x < c1, v1 for x < c2, v2 for x < c3, else v3 (c1 <= c2 <= c3), as
+// selects of values.
+__device__ __forceinline__ int pick4(int x, int c1, int c2, int c3, int v0, int v1, int v2, int v3) {
+    const int lo = x < c1 ? v0 : v1, hi = x < c3 ? v2 : v3;
+    return x < c2 ? lo : hi;
+}
+
+template <typename T, int KS>
+__global__ __launch_bounds__(64 * kProjWaves)
+__attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseDev p) {
+    typedef Mma<T> M;
+    typedef typename M::Frag Frag;
+    constexpr int DIM = 16 * KS;
+    constexpr int WS = DIM + 8;
+    constexpr int PIECES = 32 * DIM / 8;
+    constexpr int PPT = (PIECES + 64 * kProjWaves - 1) / (64 * kProjWaves);
+    constexpr int OS = 32 + 8;
+    __shared__ __align__(16) float lw[DIM], lb[DIM];
+    __shared__ __align__(16) T wbuf[2][32 * WS];
+    __shared__ __align__(16) T otile[kProjWaves][32 * OS];
+    extern __shared__ __align__(16) unsigned char pool_lds[];
+    const int G = p.G, D = p.D, GD = p.GD, KGS = GD + 8;
+    T* rows_all = reinterpret_cast<T*>(pool_lds);
+    T* wts_all = rows_all + kProjWaves * 32 * KGS;
+    float* xch_all = reinterpret_cast<float*>(wts_all + kProjWaves * G * 64);
+    int4* meta = reinterpret_cast<int4*>(xch_all + kProjWaves * 16);
+    float* lwp = reinterpret_cast<float*>(meta + D / 2);
+    float* lbias = lwp + D;
+    for (int c = threadIdx.x; c < DIM; c += blockDim.x) {
+        lw[c] = load_any(a.ln_w, c, a.ln_dtype);
+        lb[c] = load_any(a.ln_b, c, a.ln_dtype);
+    }
+    for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(p.rope.pairs, j);
+    for (int c = threadIdx.x; c < D; c += blockDim.x) lwp[c] = p.weight[c];
+    for (int c = threadIdx.x; c < 64; c += blockDim.x) lbias[c] = p.bias[c];
+    const int kg0 = p.kg0, vg0 = kg0 + GD, gbase = a.q_out + a.kv_out, nout = gbase + 2 * a.heads;
+    // Blocks of 32 output rows over [0, kg0), [kg0, vg0), [vg0, gbase) and [gbase, nout).
+    const int c1 = (kg0 + 31) / 32, c2 = c1 + (GD + 31) / 32, c3 = c2 + (GD + 31) / 32;
+    const int nblocks = c3 + (2 * a.heads + 31) / 32;
+    // Values through selects (pick4), not conditionals over captured
+    // variables, which the compiler turns into loads from the closure in
+    // scratch memory.
+    auto start_of = [=](int ob) __attribute__((always_inline)) -> int {
+        return pick4(ob, c1, c2, c3, 32 * ob, kg0 + 32 * (ob - c1), vg0 + 32 * (ob - c2), gbase + 32 * (ob - c3));
+    };
+    auto end_of = [=](int ob) __attribute__((always_inline)) -> int {
+        return pick4(ob, c1, c2, c3, kg0, vg0, gbase, nout);
+    };
+    // Weight row o of the concatenation [Wq; Wkv; Wg].
+    auto wrow = [&](int o) __attribute__((always_inline)) -> const T* {
+        return o < a.q_out ? reinterpret_cast<const T*>(a.wq) + (int64_t)o * DIM
+               : o < gbase ? reinterpret_cast<const T*>(a.wkv) + (int64_t)(o - a.q_out) * DIM
+                           : reinterpret_cast<const T*>(a.wg) + (int64_t)(o - gbase) * DIM;
+    };
+    u32x4 wreg[PPT];
+    auto fetch = [&](int ob) __attribute__((always_inline)) {
+        const int o0 = start_of(ob), oe = end_of(ob);
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (DIM / 8), c = (pc % (DIM / 8)) * 8;
+            const int o = o0 + r;
+            wreg[i] = (pc < PIECES && o < oe) ? *reinterpret_cast<const u32x4*>(wrow(o) + c) : u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (DIM / 8), c = (pc % (DIM / 8)) * 8;
+            if (pc < PIECES) *reinterpret_cast<u32x4*>(&wbuf[buf][r * WS + c]) = wreg[i];
+        }
+    };
+    fetch(0);
+    stage(0);
+    if (nblocks > 1) fetch(1);
+    __syncthreads();
+
+    // Wave-uniform quantities in scalar registers: the batch and token of the
+    // wave's first row (rows < 2^31, and a wave's 32 rows never straddle a
+    // batch since tokens is a multiple of 64).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
+    const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + wave) * 32, tok = tok0 + t;
+    const int bw = (int)tok0 / p.tokens, n0 = (int)tok0 - bw * p.tokens;
+    T* tile = otile[wave];
+    // rows is a multiple of 64: a wave, and the pair that holds its fine block,
+    // is wholly live or not.
+    const bool live = tok0 < a.rows;
+    T* krows = rows_all + wave * 32 * KGS;
+    float* sums = reinterpret_cast<float*>(krows);  // after the kg sums: kg sums, vg sums, key squares
+    T* wts = wts_all + wave * G * 64;
+    float* xch = xch_all + wave * 16;
+    const float* xch_pair = xch_all + (wave ^ 1) * 16;
+
+    Frag xf[KS];
+    layer_norm_frags<T, KS>(a, lw, lb, tok, live, g, xf);
+    int pos[3];
+    {
+        // rope_position32 without its branch (a branch here doubled the
+        // kernel's registers): a packed rotation reads three words of the
+        // pair table, always valid, and discards them.
+        const int n = live ? n0 + t : 0;
+        const int* c = p.rope.packed ? p.rope.pairs : reinterpret_cast<const int*>(p.rope.coords) + 6 * n;
+        const int c0 = c[0], c1 = c[2], c2 = c[4];
+        pos[0] = p.rope.packed ? n : c0;
+        pos[1] = p.rope.packed ? 0 : c1;
+        pos[2] = p.rope.packed ? 0 : c2;
+    }
+
+    T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
+    // One output block: the GEMM, then the range's epilogue; PRE: q, kl, vl
+    // and kg blocks, else vg and gate blocks.  The block loop runs in two
+    // parts around the slot softmax, so no value of that phase is hoisted
+    // into a loop and held across it.
+    auto run_block = [&](int ob, auto pre_tag) __attribute__((always_inline)) {
+        constexpr bool PRE = decltype(pre_tag)::value;
+        const int o_first = start_of(ob), o_end = end_of(ob);
+        const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
+        f32x16 d;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) d[r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) d = M::mfma(*reinterpret_cast<const Frag*>(wb + 16 * ks), xf[ks], d);
+        if (PRE && ob < c1) {
+            // q / kl / vl through the tile as coalesced 16-byte row pieces (as k_project).
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const float v[4] = {d[4 * qd], d[4 * qd + 1], d[4 * qd + 2], d[4 * qd + 3]};
+                store4<T>(tile + t * OS + acc_row(4 * qd, g), v);
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int tt = 16 * i + (lane >> 2), pp = lane & 3, o0 = o_first + 8 * pp;
+                const int64_t tk = tok0 + tt;
+                if (tk < a.rows && o0 < o_end) {
+                    const u32x4 piece = *reinterpret_cast<const u32x4*>(tile + tt * OS + 8 * pp);
+                    T* dst = o0 < a.q_out ? reinterpret_cast<T*>(a.q) + tk * a.q_out + o0
+                                          : reinterpret_cast<T*>(a.kv) + tk * a.kv_out + (o0 - a.q_out);
+                    *reinterpret_cast<u32x4*>(dst) = piece;
+                }
+            }
+            wave_lds_sync();  // the next block's tile writes follow these reads
+        } else if (PRE) {
+            // kg: lane (t, g) holds channels c .. c + 3 of token t for c =
+            // o_first - kg0 + 8 qd + 4 g, two rotary pairs of one head (4 | D).
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const int c = o_first - kg0 + 8 * qd + 4 * g;
+                if (c < GD) {
+                    const int cc = c % D;
+                    float x[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) x[i] = to_f32(from_f32<T>(d[4 * qd + i]));
+#pragma unroll
+                    for (int pp = 0; pp < 2; ++pp) {
+                        const int4 m = meta[(cc >> 1) + pp];
+                        const float2 cs = p.rope.table[m.x + m.y * pos[0] + m.z * pos[1] + m.w * pos[2]];
+                        rotate_pair(x[2 * pp], x[2 * pp + 1], cs.x, cs.y);
+                    }
+                    store4<T>(krows + t * KGS + c, x);
+                }
+            }
+        } else if (ob < c3) {
+            // vg: the rounded block through the tile, then the weighted sums of
+            // its 16-channel tiles over the wave's tokens.
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const float v[4] = {d[4 * qd], d[4 * qd + 1], d[4 * qd + 2], d[4 * qd + 3]};
+                store4<T>(tile + t * OS + acc_row(4 * qd, g), v);
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int c = o_first - vg0 + 16 * j;
+                if (c < GD) {
+                    const float s = slot_sum<T>(wts + (c / D) * 64, tile + 16 * j, OS, lane);
+                    if (lane < 16) sums[GD + c + lane] = s;
+                }
+            }
+            wave_lds_sync();  // the next block's tile writes follow these reads
+        } else if (live && o_first + 32 > gbase) {
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                const int o0 = o_first + acc_row(4 * qd, g);  // outputs o0 .. o0 + 3
+                float v[4] = {d[4 * qd], d[4 * qd + 1], d[4 * qd + 2], d[4 * qd + 3]};
+                if (o0 >= gbase && o0 < nout) {
+                    // Logit pairs (2h, 2h + 1) of heads h = (o0 - gbase) / 2 + {0, 1}.
+#pragma unroll
+                    for (int q2 = 0; q2 < 2; ++q2) {
+                        const int j = o0 - gbase + 2 * q2;
+                        if (j + 1 >= 2 * a.heads) break;
+                        const float l0 =
+                            to_f32(from_f32<T>(v[2 * q2] + load_any(a.gate_bias, j, a.gate_bias_dtype)));
+                        const float l1 =
+                            to_f32(from_f32<T>(v[2 * q2 + 1] + load_any(a.gate_bias, j + 1, a.gate_bias_dtype)));
+                        const float m = fmaxf(l0, l1);
+                        const float e0 = expf(l0 - m), e1 = expf(l1 - m);
+                        go[j / 2] = from_f32<T>(e1 / (e0 + e1));
+                    }
+                }
+            }
+        }
+        if (ob + 1 < nblocks) {
+            stage((ob + 1) & 1);
+            if (ob + 2 < nblocks) fetch(ob + 2);
+        }
+        __syncthreads();
+    };
+    for (int ob = 0; ob < c2; ++ob) run_block(ob, std::true_type{});
+    {
+        // Slot logits of the wave's 32 tokens for every head: lane (t, g)
+        // takes half g of each head's channels, lane t ^ 32 the other.
+        const int slot = 32 * (wave & 1) + t;
+        float logit[8];
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            if (h >= G) break;
+            const T* row = krows + t * KGS + h * D + g * (D / 2);
+            float dot = 0.f;
+            for (int i = 0; i < D / 2; i += 8) {
+                const u32x4 piece = *reinterpret_cast<const u32x4*>(row + i);
+                const T* v = reinterpret_cast<const T*>(&piece);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dot += to_f32(v[e]) * lwp[g * (D / 2) + i + e];
+            }
+            dot += lane_xor32(dot);
+            logit[h] = dot * p.inv_tau + lbias[slot];
+            const float mx = wave_max(logit[h]);
+            if (lane == 0) xch[h] = mx;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            if (h >= G) break;
+            logit[h] = expf(logit[h] - fmaxf(xch[h], xch_pair[h]));
+            const float s = wave_sum(g ? 0.f : logit[h]);
+            if (lane == 0) xch[8 + h] = s;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            if (h >= G) break;
+            const float wgt = logit[h] / (xch[8 + h] + xch_pair[8 + h]);
+            if (g == 0) {
+                const T hi = from_f32<T>(wgt);
+                wts[h * 64 + t] = hi;
+                wts[h * 64 + 32 + t] = from_f32<T>(wgt - to_f32(hi));
+            }
+        }
+        wave_lds_sync();
+        // The kg sums, one 16-channel tile at a time (each tile's reads
+        // kept next to its MFMA), parked in the wave's idle output tile and
+        // then moved over the rows, which are no longer needed.
+        float* park = reinterpret_cast<float*>(tile);
+        for (int j = 0; 16 * j < GD; ++j) {
+            const float s = slot_sum<T>(wts + (16 * j / D) * 64, krows + 16 * j, KGS, lane);
+            if (lane < 16) park[16 * j + lane] = s;
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        wave_lds_sync();
+        for (int c = lane; c < GD; c += 64) sums[c] = park[c];
+        wave_lds_sync();  // the next block's tile writes follow these reads
+    }
+    for (int ob = c2; ob < nblocks; ++ob) run_block(ob, std::false_type{});
+
+    // The fine block's summaries: the even wave adds its partner's sums (the
+    // last block's barrier orders them).
+    if (!live || (wave & 1)) return;
+    const int b = bw, m = n0 / 64;
+    const float* pair = reinterpret_cast<const float*>(krows + 32 * KGS);
+    float* nsq = sums + 2 * GD;
+    for (int c = lane; c < GD; c += 64) {
+        const int h = c / D, cc = c - h * D;
+        const int64_t bg = (int64_t)b * G + h;
+        const T kx = from_f32<T>((sums[c] + pair[c]) * p.key_scale);
+        const T vx = from_f32<T>(sums[GD + c] + pair[GD + c]);
+        reinterpret_cast<T*>(p.sk)[(bg * p.Mp + m) * D + cc] = kx;
+        reinterpret_cast<T*>(p.svt)[((bg * (p.Mp / 32) + m / 32) * D + cc) * 32 + (m & 31)] = vx;
+        nsq[c] = to_f32(kx) * to_f32(kx);
+    }
+    wave_lds_sync();
+    if (lane < G) {
+        float sq = 0.f;
+        for (int c = 0; c < D; ++c) sq += nsq[lane * D + c];
+        // Norm of the stored (rounded) summary key; non-negative floats order
+        // like their bit patterns, so an integer max is an exact float max.
+        const float norm = sqrtf(sq) * (1.f + 1e-6f);
+        atomicMax(reinterpret_cast<int*>(p.norm) + ((int64_t)b * G + lane) * 64 + (m % 64), __float_as_int(norm));
     }
 }
 
@@ -323,6 +715,27 @@ int launch_out_residual(const void* y, const void* wo, const void* x, void* out,
     return check_launch("p3d_out_residual");
 }
 
+template <typename T>
+int launch_project_pool(const ProjDev& d, const PoolFuseDev& p, hipStream_t s) {
+    const unsigned blocks = (unsigned)cdiv(cdiv(d.rows, 32), kProjWaves);
+    const size_t smem = pool_fuse_lds_bytes(p.G, p.D);
+    switch (d.dim) {
+#define CASE(DIM)                                                                     \
+    case DIM:                                                                         \
+        k_project_pool<T, DIM / 16><<<blocks, 64 * kProjWaves, smem, s>>>(d, p);      \
+        break;
+        CASE(64) CASE(96) CASE(128) CASE(192) CASE(256)
+#undef CASE
+        default: return fail(P3D_EUNSUPPORTED, "pooled projections: dim must be one of 64, 96, 128, 192, 256");
+    }
+    return check_launch("p3d_project_pool");
+}
+
+__global__ void k_zero_norm_slots(float* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
 }  // namespace
 }  // namespace p3d
 
@@ -341,9 +754,10 @@ extern "C" int p3d_out_residual(const void* y, const void* wo, const void* x, vo
                             : launch_out_residual<__bf16>(y, wo, x, out, rows, k, dim, s);
 }
 
-extern "C" int p3d_project(const p3d_project_args* args, void* stream) {
-    P3D_REQUIRE(args, "null args");
-    const p3d_project_args& a = *args;
+namespace {
+
+// Validates the projection arguments and fills the kernels' argument block.
+int project_dev(const p3d_project_args& a, ProjDev& d) {
     P3D_REQUIRE(a.dtype == P3D_F16 || a.dtype == P3D_BF16, "dtype must be fp16 or bf16");
     P3D_REQUIRE(a.ln_dtype >= P3D_F32 && a.ln_dtype <= P3D_BF16 && a.gate_bias_dtype >= P3D_F32 &&
                     a.gate_bias_dtype <= P3D_BF16,
@@ -358,7 +772,6 @@ extern "C" int p3d_project(const p3d_project_args* args, void* stream) {
                 "x and the weights must be 16-byte aligned");
     P3D_REQUIRE(aligned16(a.q) && aligned16(a.kv), "q and kv must be 16-byte aligned");
     P3D_REQUIRE(cdiv(a.rows, 32 * kProjWaves) < (1LL << 31), "too many rows");
-    ProjDev d;
     d.x = (const char*)a.x;
     d.ln_w = a.ln_weight;
     d.ln_b = a.ln_bias;
@@ -377,6 +790,65 @@ extern "C" int p3d_project(const p3d_project_args* args, void* stream) {
     d.ln_dtype = a.ln_dtype;
     d.gate_bias_dtype = a.gate_bias_dtype;
     d.eps = a.eps;
+    return P3D_OK;
+}
+
+}  // namespace
+
+extern "C" int p3d_project(const p3d_project_args* args, void* stream) {
+    P3D_REQUIRE(args, "null args");
+    ProjDev d;
+    if (int rc = project_dev(*args, d)) return rc;
     hipStream_t s = as_stream(stream);
-    return a.dtype == P3D_F16 ? launch_project<_Float16>(d, s) : launch_project<__bf16>(d, s);
+    return args->dtype == P3D_F16 ? launch_project<_Float16>(d, s) : launch_project<__bf16>(d, s);
+}
+
+extern "C" int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, void* stream) {
+    P3D_REQUIRE(args && pool, "null args");
+    ProjDev d;
+    int rc = project_dev(*args, d);
+    if (rc) return rc;
+    const p3d_pool_args& q = *pool;
+    P3D_REQUIRE(q.dtype == args->dtype, "pooling and projections disagree on the dtype");
+    P3D_REQUIRE(q.weight && q.bias && q.sk && q.svt && q.sk_norm_max && q.rope.table && q.rope.pairs &&
+                    (q.rope.packed || q.rope.coords),
+                "null pointer argument");
+    P3D_REQUIRE(q.temperature > 0.f, "temperature must be positive");
+    P3D_REQUIRE(q.kv_heads >= 1 && q.head_dim >= 16 && args->kv_out == 4 * q.kv_heads * q.head_dim,
+                "kv_out must be 4 * kv_heads * head_dim");
+    P3D_REQUIRE(q.tokens >= 64 && (int64_t)q.batch * q.tokens == args->rows,
+                "rows must be batch * tokens");
+    // Shapes the fused kernel does not take (the caller runs p3d_project and
+    // p3d_pool_fwd instead); nothing has been launched.
+    if (!(q.head_dim == 16 || q.head_dim == 32 || q.head_dim == 48 || q.head_dim == 64) || q.kv_heads > 8 ||
+        q.kv_heads * q.head_dim > kPoolFuseMaxCh || q.slots != 64 || q.pool_size != 1 || q.tokens % 64 ||
+        q.fine_blocks != q.tokens / 64 || q.summaries != q.fine_blocks ||
+        !(args->dim == 64 || args->dim == 96 || args->dim == 128 || args->dim == 192 || args->dim == 256) ||
+        project_static_lds_bytes(args->dim) + pool_fuse_lds_bytes(q.kv_heads, q.head_dim) > 160 * 1024)
+        return fail(P3D_EUNSUPPORTED,
+                    "pooled projections need head_dim 16/32/48/64, kv_heads * head_dim <= 192, 64-slot fine "
+                    "blocks of pool_size 1 over tokens a multiple of 64, and dim 64/96/128/192/256 within the LDS");
+    PoolFuseDev p;
+    p.G = q.kv_heads;
+    p.D = q.head_dim;
+    p.GD = q.kv_heads * q.head_dim;
+    p.Mp = (int)cdiv(q.summaries, 32) * 32;
+    p.tokens = q.tokens;
+    p.kg0 = args->q_out + 2 * p.GD;
+    p.inv_tau = 1.f / q.temperature;
+    p.key_scale = q.key_scale;
+    p.weight = q.weight;
+    p.bias = q.bias;
+    p.rope = rope_dev(q.rope);
+    p.sk = (char*)q.sk;
+    p.svt = (char*)q.svt;
+    p.norm = q.sk_norm_max;
+    hipStream_t s = as_stream(stream);
+    if (!q.norms_cleared) {
+        const int n = q.batch * q.kv_heads * 64;
+        k_zero_norm_slots<<<(unsigned)cdiv(n, 256), 256, 0, s>>>(q.sk_norm_max, n);
+        rc = check_launch("p3d_project_pool (norm slots)");
+        if (rc) return rc;
+    }
+    return args->dtype == P3D_F16 ? launch_project_pool<_Float16>(d, p, s) : launch_project_pool<__bf16>(d, p, s);
 }

@@ -360,6 +360,32 @@ def _remember(geometry, tag):
     _TAGS[key] = (ref, _versions_of(geometry.tensors), tag)
 
 
+_CONSECUTIVE = {}
+
+
+def blocks_consecutive(geometry):
+    """Whether fine block f of ``geometry`` is rows 64 f .. 64 f + 63 in slot
+    order, 64 slots each (the blocks of this package's ``build_layout``):
+    checked once per geometry object on its device (one comparison and a
+    synchronisation), then cached while its tables are unchanged."""
+    blocks = geometry.blocks
+    if blocks.ndim != 2 or blocks.shape[1] != 64 or blocks.shape[0] * 64 != geometry.num_tokens:
+        return False
+    key = id(geometry)
+    versions = _versions_of(geometry.tensors)
+    hit = _CONSECUTIVE.get(key)
+    if hit is not None and hit[0]() is geometry and hit[1] == versions:
+        return hit[2]
+    flat = blocks.reshape(-1)
+    ok = bool(torch.equal(flat, torch.arange(flat.numel(), device=flat.device, dtype=flat.dtype)))
+    try:
+        ref = weakref.ref(geometry, lambda _r, key=key: _CONSECUTIVE.pop(key, None))
+    except TypeError:
+        return ok
+    _CONSECUTIVE[key] = (ref, versions, ok)
+    return ok
+
+
 def _map_for(mapping, like):
     """A raster->packed map as a contiguous int32 tensor on ``like``'s device."""
     if mapping is None:

@@ -179,3 +179,61 @@ def test_core_rejects_geometry_tables_that_are_not_int32():
     wide = RefGeometry(g.neighbors.long(), g.reverse_neighbors, g.blocks, g.pool_size, g.num_tokens)
     with pytest.raises(ValueError, match="int32"):
         pack3d_hip(*inputs, wide)
+
+
+def test_blocks_consecutive_recognises_build_layout_blocks():
+    """The fused projection pooling takes geometries whose fine block f is
+    rows 64 f .. 64 f + 63 in slot order; any other table (rows swapped,
+    other slot counts, an in-place change after a first check) does not."""
+    import types
+
+    import oracle.pack3d_oracle as ref
+    from pack3d_amd.geometry import blocks_consecutive
+    from tests._refobjects import reference_layout
+
+    def geom(blocks):
+        g = types.SimpleNamespace(blocks=blocks, num_tokens=blocks.numel())
+        g.tensors = (blocks,)
+        return g
+
+    lay = reference_layout(ref.build_layout((4, 8, 8), (4, 4, 4), radius=1, pool_size=1))
+    assert blocks_consecutive(lay.geometry)
+    blocks = torch.arange(4 * 64, dtype=torch.int32).view(4, 64)
+    g = geom(blocks.clone())
+    assert blocks_consecutive(g) and blocks_consecutive(g)
+    g.blocks[0, :2] = g.blocks[0, :2].flip(0)      # in place: the cached answer is dropped
+    assert not blocks_consecutive(g)
+    swapped = blocks.clone()
+    swapped[[1, 2]] = swapped[[2, 1]]
+    assert not blocks_consecutive(geom(swapped))
+    assert not blocks_consecutive(geom(torch.arange(4 * 8, dtype=torch.int32).view(4, 8)))
+
+
+def test_project_pool_answers_unsupported_before_launch():
+    """p3d_project_pool refuses shapes it does not take with P3D_EUNSUPPORTED
+    and malformed arguments with P3D_EINVAL, before touching any pointer."""
+    from pack3d_amd import _lib
+    bf16 = _lib.DTYPES[torch.bfloat16]
+    fake = 1 << 20   # 16-byte aligned, never dereferenced
+    h, g, d, dim, n = 4, 4, 48, 192, 4096
+    args = _lib.ProjectArgs(fake, fake, fake, fake, fake, fake, fake, fake, fake, fake, n, dim, h * d, 4 * g * d,
+                            h, bf16, bf16, bf16, 1e-5)
+    pool = _lib.PoolArgs()
+    pool.batch, pool.kv_heads, pool.tokens, pool.head_dim, pool.dtype = 1, g, n, d, bf16
+    pool.fine_blocks, pool.slots, pool.pool_size, pool.summaries = n // 64, 64, 1, n // 64
+    pool.temperature, pool.key_scale = 1.0, 1.0
+    pool.weight = pool.bias = pool.sk = pool.svt = pool.sk_norm_max = fake
+    pool.rope.table = pool.rope.pairs = pool.rope.coords = fake
+    lib = _lib.lib()
+    for field, value in (("pool_size", 2), ("slots", 32)):
+        setattr(pool, field, value)
+        assert lib.p3d_project_pool(args, pool, None) == _lib.P3D_EUNSUPPORTED
+        setattr(pool, field, {"pool_size": 1, "slots": 64}[field])
+    pool.kv_heads = 2       # kv_out no longer 4 * kv_heads * head_dim
+    assert lib.p3d_project_pool(args, pool, None) == 1
+    assert b"kv_out" in lib.p3d_last_error()
+    pool.kv_heads = g
+    pool.dtype = _lib.DTYPES[torch.float16]
+    assert lib.p3d_project_pool(args, pool, None) == 1
+    with pytest.raises(RuntimeError, match="null args"):
+        _lib.call("p3d_project_pool", None, None, None)

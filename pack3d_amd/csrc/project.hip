@@ -409,6 +409,22 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     }
 
     T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
+    // (cos, sin) of the lane's rotary pairs in kg block ob (channels
+    // c .. c + 3 for c = ob's first kg channel + 8 qd + 4 g, pairs of one head
+    // since 4 | D), loaded one block ahead so that the table reads' latency
+    // hides behind a block's GEMM.
+    float2 csn[8];
+    auto load_cs = [&](int ob) __attribute__((always_inline)) {
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+            const int c = min(kg0 + 32 * (ob - c1) - kg0 + 8 * qd + 4 * g, GD - 4), cc = c % D;
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                const int4 m = meta[(cc >> 1) + pp];
+                csn[2 * qd + pp] = p.rope.table[m.x + m.y * pos[0] + m.z * pos[1] + m.w * pos[2]];
+            }
+        }
+    };
     // One output block: the GEMM, then the range's epilogue; PRE: q, kl, vl
     // and kg blocks, else vg and gate blocks.  The block loop runs in two
     // parts around the slot softmax, so no value of that phase is hoisted
@@ -445,20 +461,19 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
         } else if (PRE) {
             // kg: lane (t, g) holds channels c .. c + 3 of token t for c =
             // o_first - kg0 + 8 qd + 4 g, two rotary pairs of one head (4 | D).
+            float2 cs[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cs[k] = csn[k];
+            if (ob + 1 < c2) load_cs(ob + 1);
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
                 const int c = o_first - kg0 + 8 * qd + 4 * g;
                 if (c < GD) {
-                    const int cc = c % D;
                     float x[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i) x[i] = to_f32(from_f32<T>(d[4 * qd + i]));
 #pragma unroll
-                    for (int pp = 0; pp < 2; ++pp) {
-                        const int4 m = meta[(cc >> 1) + pp];
-                        const float2 cs = p.rope.table[m.x + m.y * pos[0] + m.z * pos[1] + m.w * pos[2]];
-                        rotate_pair(x[2 * pp], x[2 * pp + 1], cs.x, cs.y);
-                    }
+                    for (int pp = 0; pp < 2; ++pp) rotate_pair(x[2 * pp], x[2 * pp + 1], cs[2 * qd + pp].x, cs[2 * qd + pp].y);
                     store4<T>(krows + t * KGS + c, x);
                 }
             }
@@ -508,7 +523,11 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
         }
         __syncthreads();
     };
-    for (int ob = 0; ob < c2; ++ob) run_block(ob, std::true_type{});
+    for (int ob = 0; ob < c1; ++ob) {
+        if (ob == c1 - 1) load_cs(c1);
+        run_block(ob, std::true_type{});
+    }
+    for (int ob = c1; ob < c2; ++ob) run_block(ob, std::true_type{});
     {
         // Slot logits of the wave's 32 tokens for every head: lane (t, g)
         // takes half g of each head's channels, lane t ^ 32 the other.
@@ -529,7 +548,6 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
             logit[h] = dot * p.inv_tau + lbias[slot];
             const float mx = wave_max(logit[h]);
             if (lane == 0) xch[h] = mx;
-            __builtin_amdgcn_sched_barrier(0);
         }
         __syncthreads();
 #pragma unroll
@@ -551,14 +569,13 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
             }
         }
         wave_lds_sync();
-        // The kg sums, one 16-channel tile at a time (each tile's reads
-        // kept next to its MFMA), parked in the wave's idle output tile and
-        // then moved over the rows, which are no longer needed.
+        // The kg sums, 16 channels per MFMA, parked in the wave's idle output
+        // tile and then moved over the rows, which are no longer needed.
         float* park = reinterpret_cast<float*>(tile);
+#pragma unroll 4
         for (int j = 0; 16 * j < GD; ++j) {
             const float s = slot_sum<T>(wts + (16 * j / D) * 64, krows + 16 * j, KGS, lane);
             if (lane < 16) park[16 * j + lane] = s;
-            __builtin_amdgcn_sched_barrier(0);
         }
         wave_lds_sync();
         for (int c = lane; c < GD; c += 64) sums[c] = park[c];

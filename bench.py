@@ -93,8 +93,10 @@ class _TimedLib:
 
 def kernel_times_in_layer(layer, x, layout, steps, stream, fused=True):
     """Mean durations (ms) of the layer's launches within layer steps, by
-    name: "p3d_project_pool" (projections with the pooling fused in) or
-    "p3d_project" and "pool" (the unfused path, fused=False), and "attention"."""
+    name: "p3d_project_pool" (projections with the pooling fused in) and
+    "attention"; with fused=False the unfused path's "pool" and "attention"
+    (the projections are not wrapped there: every wrapped call adds host
+    time, and the pool's start event must not wait on the host)."""
     import pack3d_amd.attention as attention
     from pack3d_amd import _lib
     from pack3d_amd.core import ForwardPlan
@@ -118,9 +120,11 @@ def kernel_times_in_layer(layer, x, layout, steps, stream, fused=True):
         orig[1](self)
         mark("attention")
 
-    timed = _TimedLib(orig[2](), ("p3d_project_pool", "p3d_project"), mark)
-    ForwardPlan.pool, ForwardPlan.attention, _lib.lib = pool, attn, lambda: timed
-    if not fused:
+    ForwardPlan.pool, ForwardPlan.attention = pool, attn
+    if fused:
+        timed = _TimedLib(orig[2](), ("p3d_project_pool",), mark)
+        _lib.lib = lambda: timed
+    else:
         attention.pooled_core = lambda *args: None
     try:
         for _ in range(steps):
@@ -150,22 +154,6 @@ def layer_ms_unfused(layer, x, layout, steps):
         return 1000.0 * (time.perf_counter() - t0) / steps
     finally:
         attention.pooled_core = real
-
-
-def pool_alone_cold_ms(plan, reps, stream, device):
-    """k_pool_fwd alone, each launch after a 1 GiB fill that evicts the
-    caches (none of kg / vg is in the last-level cache when it starts)."""
-    flush = torch.empty(256 * 2 ** 20, dtype=torch.float32, device=device)
-    total = 0.0
-    for _ in range(reps):
-        flush.fill_(0.0)
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        plan.pool()
-        end.record(stream)
-        end.synchronize()
-        total += start.elapsed_time(end)
-    return total / reps
 
 
 def summary_pathway_ms(plan, steps, stream):
@@ -251,11 +239,14 @@ def traffic_probe():
     """Launch sequence profiled for HBM traffic (run under rocprofv3 --pmc).
 
     A 1 GiB fill evicts the caches, an elementwise add over 256 MiB gives the
-    counter calibration (268,435,456 bytes read and written), then the pool
-    and attention kernels of the c2 workload run three times each.
+    counter calibration (268,435,456 bytes read and written), then the fused
+    projection pooling, the pool and the attention kernels of the c2 workload
+    run three times each.
     """
     import pack3d_amd as p3d
-    from pack3d_amd.core import ForwardPlan
+    import pack3d_amd.attention as attention
+    from pack3d_amd import _lib
+    from pack3d_amd.core import ForwardPlan, _projection_views
 
     dev = torch.device("cuda:0")
     n = math.prod(SHAPE)
@@ -269,9 +260,17 @@ def traffic_probe():
         q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, layout)
         plan = ForwardPlan(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate, layer.local_scale,
                            layer.global_scale, layout.geometry, layer.temperature, rope, rope)
+        made = attention._project_buffers(layer, x)
+        fused = ForwardPlan(*_projection_views(made[1], made[2], HEADS, KV_HEADS), layer.pool_weight,
+                            layer.slot_bias, made[3].transpose(1, 2), layer.local_scale, layer.global_scale,
+                            layout.geometry, layer.temperature, rope, rope)
+        stream = _lib.stream_of(dev)
         for _ in range(3):
             flush.fill_(0.0)
             torch.add(src, 1.0, out=dst)
+            flush.fill_(0.0)
+            fused.pool_args.norms_cleared = 0
+            _lib.call("p3d_project_pool", made[0], fused.pool_args, stream)
             flush.fill_(0.0)
             plan.pool()
             plan.attention()
@@ -424,19 +423,20 @@ def main():
         # Per-kernel durations inside the same layer steps: HIP events on the
         # launch stream around the layer's launches (a second pass over the
         # steps, so the first one runs without them); then the layer step with
-        # the projection pooling switched off, for comparison.
+        # the projection pooling switched off (p3d_project, p3d_pool_fwd, the
+        # attention), for comparison, and its pooling launch.
         fused = kernel_times_in_layer(layer, x, layout, a.steps, stream)
         if "p3d_project_pool" not in fused:
             raise RuntimeError("the benchmark layer did not take the fused projection pooling")
         ms_proj_pool, ms_attn = fused["p3d_project_pool"], fused["attention"]
         ms_layer_unfused = layer_ms_unfused(layer, x, layout, a.steps)
+        ms_pool = kernel_times_in_layer(layer, x, layout, a.steps, stream, fused=False)["pool"]
         q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, layout)
         plan = ForwardPlan(q, kl, vl, kg, vg, layer.pool_weight, layer.slot_bias, gate, layer.local_scale,
                            layer.global_scale, layout.geometry, layer.temperature, rope, rope)
         plan.run()
         ms_core = time_events(plan.run, max(5, a.steps), stream)
         ms_summary = summary_pathway_ms(plan, a.steps, stream)
-        ms_pool_cold = pool_alone_cold_ms(plan, 20, stream, dev)
 
     m = layout.geometry.num_summaries
     edges = valid_edges(SHAPE, RADIUS)
@@ -446,7 +446,7 @@ def main():
     exps = HEADS * n * m + HEADS * edges  # one exponential per (query, summary) and per valid edge
     exp_rate = exps / (ms_attn * 1e-3)
     pool_bytes = 2 * KV_HEADS * n * HEAD_DIM * 2 + 2 * KV_HEADS * m * HEAD_DIM * 2
-    pool_gbs = pool_bytes / (ms_pool_cold * 1e-3) / 1e9
+    pool_gbs = pool_bytes / (ms_pool * 1e-3) / 1e9
     # The fused projection kernel's compulsory HBM bytes: x read; q, kl, vl,
     # the gate and the summaries written (the weights are a few hundred KB).
     proj_pool_bytes = (n * DIM + n * HEADS * HEAD_DIM + 2 * n * KV_HEADS * HEAD_DIM + n * HEADS
@@ -465,7 +465,7 @@ def main():
                    "ms_core": round(ms_core, 4), "ms_project_pool_kernel": round(ms_proj_pool, 4),
                    "ms_attn_kernel": round(ms_attn, 4), "ms_summary_pathway": round(ms_summary, 4),
                    "ms_layer_unfused": round(ms_layer_unfused, 4),
-                   "ms_pool_kernel_alone_cold": round(ms_pool_cold, 4),
+                   "ms_pool_kernel_unfused_layer": round(ms_pool, 4),
                    "parallelism": "single GPU"},
         "roofline": {"kernel": "k_attn_grid (fused local+global forward)", "bound": "mfma",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
@@ -479,8 +479,8 @@ def main():
                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(flops_summary / (ms_summary * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                              "algorithmic_flops": flops_summary},
-        "roofline_pool": {"kernel": "k_pool_fwd (the unfused pooling: training, other layouts), alone after a "
-                                    "1 GiB cache flush", "bound": "hbm", "achieved": round(pool_gbs, 1),
+        "roofline_pool": {"kernel": "k_pool_fwd (the unfused pooling: training, other layouts), inside the "
+                                    "unfused layer step", "bound": "hbm", "achieved": round(pool_gbs, 1),
                           "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(pool_gbs / PEAK_HBM_GBS, 4),
                           "traffic": traffic.get("pool_bytes_per_launch"),
                           "algorithmic_bytes": pool_bytes},

@@ -184,6 +184,85 @@ struct StageRegs {
     }
 };
 
+// LDS byte address of a pointer into the workgroup's shared memory.
+template <typename T>
+__device__ __forceinline__ uint32_t lds_address(const T* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
+}
+
+// Summary stages of the pipelined sweep, copied by the LDS DMA
+// (global_load_lds_dwordx4): the pieces go from L2 straight into LDS, with no
+// registers to hold them and no LDS store instructions.  One copy writes 64
+// consecutive 16-byte pieces of LDS, lane i the piece at M0 + 16 i, from a
+// global address of the lane's choosing.  The stage keeps the layout of
+// StageRegs (K rows of KSTR, V^T rows of VGS): a copy spans whole padded
+// rows, its lanes on padding slots fetch a piece of the same row (finite,
+// never read), and the last copy of each region starts 64 pieces before the
+// region's end, so it rewrites its predecessor's tail with the same data
+// instead of running into the V^T padding rows (the ones row and zeros,
+// written once).  Copies are split evenly over the waves; a wave with fewer
+// repeats the last copy, so every wave issues the same instructions.
+// Completion is tracked by the vector-memory counter (dma_wait).
+template <typename C, int WG>
+struct StageDma {
+    typedef typename C::T_ T;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int VGS = 64 + EP;
+    static constexpr int KROW = C::KSTR / EP, VROW = VGS / EP;  // pieces per padded row
+    static constexpr int KPIECES = 64 * KROW, VPIECES = C::D * VROW;
+    static constexpr int KCH = (KPIECES + 63) / 64, VCH = (VPIECES + 63) / 64;
+    static constexpr int CH = KCH + VCH, WAVES = WG / 64, PER = (CH + WAVES - 1) / WAVES;
+    static_assert(C::KSTR % EP == 0 && VGS % EP == 0 && KPIECES >= 64 && VPIECES >= 64, "stage layout");
+    uint32_t off[PER];  // byte offset of this lane's source piece in the stage's sk / svt block
+    int wave;
+
+    __device__ __forceinline__ static int chunk(int w, int i) { return min(w * PER + i, CH - 1); }
+    // First piece of copy c within its region (K rows, or the data rows of V^T).
+    __device__ __forceinline__ static int first_piece(int c) {
+        return c < KCH ? min(64 * c, KPIECES - 64) : min(64 * (c - KCH), VPIECES - 64);
+    }
+
+    __device__ __forceinline__ StageDma() {
+        wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = chunk(wave, i), slot = first_piece(c) + lane;
+            int e;
+            if (c < KCH) {
+                const int row = slot / KROW, p = slot % KROW;
+                e = row * C::D + (p < C::D / EP ? p : 0) * EP;
+            } else {
+                const int ch = slot / VROW, p = slot % VROW, dp = p < 64 / EP ? p : 0;
+                e = (dp / (32 / EP)) * C::D * 32 + ch * 32 + (dp % (32 / EP)) * EP;
+            }
+            off[i] = (uint32_t)e * sizeof(T);
+        }
+    }
+
+    // Copy stage [base, base + 64) into `stage`.  Source offsets are clamped
+    // into the rows present, so every lane reads this (b, g)'s summaries.
+    __device__ __forceinline__ void copy(const AttnDev& a, int64_t bg, int base, T* stage) const {
+        const uint32_t last = (uint32_t)(min(64, a.Mp - base) * C::D - EP) * sizeof(T);
+        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
+        const T* svt = tp<T>(a.svt) + ((int64_t)bg * a.Mp + base) * C::D;
+        const uint32_t lds0 = lds_address(stage);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = chunk(wave, i);
+            const uint32_t m0 = lds0 + (uint32_t)(c < KCH ? first_piece(c) : KPIECES + first_piece(c)) * 16u;
+            const T* src = c < KCH ? sk : svt;
+            asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(min(off[i], last)), "s"(src), "{m0}"(m0)
+                         : "memory");
+        }
+    }
+};
+
+// Wait for this wave's LDS DMA copies (they count as vector-memory loads) and
+// its LDS reads, before the barrier after which another wave's copy may
+// overwrite what they read.
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); }
+
 // One summary stage (two 32-key tiles) on this wave's two column blocks.
 template <typename C, bool BOUND>
 __device__ __forceinline__ void global_stage(const AttnDev& a, int base, const typename C::T_* Ks,
@@ -381,13 +460,10 @@ __device__ __forceinline__ void global_sweep_piped(const AttnDev& a, int64_t bg,
 #pragma unroll
     for (int b = 0; b < 3; ++b) init_v_padding<C>(lds + b * STAGE + 64 * C::KSTR, VGS, 64);
     const int stages = (a.M + 63) / 64, full = a.M / 64;
-    StageRegs<C, WG> regs;
-    regs.load(a, bg, 0);
-    regs.store(lds);
-    if (stages > 1) {
-        regs.load(a, bg, 64);
-        regs.store(lds + STAGE);
-    }
+    const StageDma<C, WG> dma;
+    dma.copy(a, bg, 0, lds);
+    dma.copy(a, bg, 64 * min(1, stages - 1), lds + STAGE);
+    dma_wait();
     __syncthreads();
 
     const int krow = kperm<C::E, C::KS>(qi) * C::KSTR + C::E * g;
@@ -406,13 +482,15 @@ __device__ __forceinline__ void global_sweep_piped(const AttnDev& a, int64_t bg,
     // fetched, past the last stage as a repeat of it into the buffer no one
     // reads any more.
     for (int stage = 0; stage < full; ++stage) {
-        regs.load_clamped(a, bg, 64 * min(stage + 2, stages - 1));
         const int nxt = cur == 2 ? 0 : cur + 1;
+        // Buffer cur + 2 held stage - 1, which every wave finished reading
+        // before the barrier that ended the previous iteration.
+        dma.copy(a, bg, 64 * min(stage + 2, stages - 1), lds + (nxt == 2 ? 0 : nxt + 1) * STAGE);
         const T* Ks = lds + cur * STAGE;
         pipe_tile<C, false>(a, Ks + 64 * C::KSTR, 0, Ks + 32 * C::KSTR + krow, qf, st, negm, s0, kf, pf1, vf, lane);
         pipe_tile<C, false>(a, Ks + 64 * C::KSTR + 32, 0, lds + nxt * STAGE + krow, qf, st, negm, s0, kf, pf1, vf,
                             lane);
-        regs.store_all(lds + (nxt == 2 ? 0 : nxt + 1) * STAGE);
+        dma_wait();
         __syncthreads();
         cur = nxt;
     }

@@ -270,7 +270,7 @@ def traffic_probe():
             torch.add(src, 1.0, out=dst)
             flush.fill_(0.0)
             fused.pool_args.norms_cleared = 0
-            _lib.call("p3d_project_pool", made[0], fused.pool_args, stream)
+            _lib.call("p3d_project_pool", made[0], fused.pool_args, 1, stream)
             flush.fill_(0.0)
             plan.pool()
             plan.attention()

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 12
+#define P3D_ABI_VERSION 13
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -185,6 +185,11 @@ typedef struct p3d_attn_args {
     float* lse_global;          /* [B,H,N] */
     void* o_local;              /* [B,H,N,D] dtype */
     void* o_global;             /* [B,H,N,D] dtype */
+    int32_t kl_rotated;         /* nonzero: kl already holds R(pos) kl rounded to
+                                   dtype (p3d_project_pool with rotate_kl, or
+                                   p3d_rotate); the grid kernel then rotates
+                                   only q.  The rows and indexed kernels always
+                                   take kl rotated. */
 } p3d_attn_args;
 int p3d_attn_fwd_grid(const p3d_attn_args* args, void* stream);
 int p3d_attn_fwd_rows(const p3d_attn_args* args, void* stream);
@@ -299,8 +304,10 @@ int p3d_project(const p3d_project_args* args, void* stream);
  * launching anything, for shapes outside head_dim 16/32/48/64, kv_heads *
  * head_dim <= 192, tokens a multiple of 64 and dim 64/96/128/192/256 (the
  * caller then runs p3d_project and p3d_pool_fwd); P3D_EINVAL for arguments
- * either would reject. */
-int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, void* stream);
+ * either would reject.  rotate_kl nonzero: kl is written rotated by
+ * pool->rope (rounded to dtype, rotated in fp32, rounded again -- the values
+ * the attention kernels rotate it to), for p3d_attn_args.kl_rotated. */
+int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, int32_t rotate_kl, void* stream);
 
 /* Output projection with the residual (attention.py:89): out = x + y Wo^T for
  * y [rows, k] (the core's output, heads concatenated), Wo [dim, k] and x,

@@ -25,7 +25,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 12  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 13  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -51,7 +51,7 @@ class AttnArgs(ctypes.Structure):
                 ("rope", Rope), ("grid", c_int32 * 3), ("radius", c_int32 * 3),
                 ("raster_to_packed", c_void_p), ("o_local_in", c_void_p), ("y", View),
                 ("lse_local", c_void_p), ("lse_global", c_void_p), ("o_local", c_void_p),
-                ("o_global", c_void_p)]
+                ("o_global", c_void_p), ("kl_rotated", c_int32)]
 
 
 class BwdArgs(ctypes.Structure):
@@ -100,7 +100,7 @@ SIGNATURES = {
                    c_int32),
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
     "p3d_project": ([ctypes.POINTER(ProjectArgs), _P], c_int32),
-    "p3d_project_pool": ([ctypes.POINTER(ProjectArgs), ctypes.POINTER(PoolArgs), _P], c_int32),
+    "p3d_project_pool": ([ctypes.POINTER(ProjectArgs), ctypes.POINTER(PoolArgs), c_int32, _P], c_int32),
     "p3d_out_residual": ([_P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_layer_norm_train": ([_P, _P, _P, c_int32, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_float,
                               _P], c_int32),

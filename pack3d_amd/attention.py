@@ -111,9 +111,10 @@ def pooled_core(layer, x, layout):
     """The core's output [B, H, N, d] (a transposed view of a [B, N, H, d]
     buffer) of the no-grad forward with the summary pooling fused into the
     projections (``p3d_project_pool``): q, kl, vl, the gate and the summaries
-    come from one kernel, kg and vg are never written, and the attention
-    kernels follow.  The same values as the projections, ``p3d_pool_fwd``
-    and the attention, up to the order of fp32 sums in the pooling.  None
+    come from one kernel, kg and vg are never written, kl is stored rotated
+    (the attention kernels then rotate only q), and the attention kernels
+    follow.  The same values as the projections, ``p3d_pool_fwd`` and the
+    attention, up to the order of fp32 sums in the pooling.  None
     when it does not apply: autograd active, fp32, pool_size other than 1,
     fine blocks that are not the consecutive 64-token runs of
     ``build_layout``, or shapes the kernel does not take; the caller then runs
@@ -134,14 +135,17 @@ def pooled_core(layer, x, layout):
     inputs = (q, kl, vl, kg, vg, *pool_params[:2], gp.transpose(1, 2), *pool_params[2:])
     _validate_inputs(*inputs, geometry, layer.temperature)
     rope = layer._rope(x, layout)
-    plan = ForwardPlan(*inputs, geometry, layer.temperature, rope, rope)
+    # kl is stored rotated by the projections, so the attention kernels do
+    # not rotate every halo key again for each brick that reads it.
+    rotate = not rope.identity
+    plan = ForwardPlan(*inputs, geometry, layer.temperature, rope, rope, kl_rotated=rotate)
     m = geometry.num_summaries
     if m % 32:
         # Padding summaries up to the next multiple of 32: zero, as
         # p3d_pool_fwd writes them (the fused kernel writes real ones only).
         plan.sk[:, :, m:].zero_()
         plan.svt[:, :, -1, :, m % 32:].zero_()
-    rc = _lib.lib().p3d_project_pool(args, plan.pool_args, _lib.stream_of(x.device))
+    rc = _lib.lib().p3d_project_pool(args, plan.pool_args, int(rotate), _lib.stream_of(x.device))
     if rc == _lib.P3D_EUNSUPPORTED:
         return None
     if rc != 0:

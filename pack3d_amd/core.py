@@ -107,11 +107,13 @@ class ForwardPlan:
     """Buffers and ctypes argument blocks of one forward; ``run()`` launches it.
 
     Splitting construction from launch lets callers time or replay the
-    pooling and attention kernels individually.
+    pooling and attention kernels individually.  ``kl_rotated``: kl already
+    holds the rotated keys (``p3d_project_pool`` with rotate_kl), so neither
+    the grid kernel nor the indexed path rotates it again.
     """
 
     def __init__(self, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature,
-                 rope: RopeSpec, pool_rope: RopeSpec, save_state=False):
+                 rope: RopeSpec, pool_rope: RopeSpec, save_state=False, kl_rotated=False):
         b, h, n, d = q.shape
         g = kl.shape[1]
         dev = q.device
@@ -159,6 +161,7 @@ class ForwardPlan:
         a.o_local = _lib.ptr(self.saved.get("o_local"))
         a.o_global = _lib.ptr(self.saved.get("o_global"))
         a.vl = _lib.view(vl)
+        a.kl_rotated = 1 if kl_rotated else 0
         self.attn_args = a
         tag = brick_tag(geometry)
         self.grid = tag is not None
@@ -177,7 +180,7 @@ class ForwardPlan:
             # gathered per edge); q rotates on load in both kernels.  The
             # indexed local kernel writes sl * o_L into y, and the rows kernel
             # adds the summary branch in its epilogue.
-            if not rope.identity:
+            if not rope.identity and not kl_rotated:
                 klr = torch.empty(kl.shape, dtype=kl.dtype, device=dev)
                 self.pre.append(("p3d_rotate", (_lib.view(kl), _lib.view(klr), b, g, n, d, dt, rope.struct(), 0)))
                 kl = klr

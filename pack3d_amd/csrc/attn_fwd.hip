@@ -48,6 +48,7 @@ struct AttnDev {
     float *lse_l, *lse_g;
     char *o_l, *o_g;
     float scale_log2;  // log2(e) / sqrt(D)
+    int kl_rotated;    // kl already rotated: the grid kernel rotates q only
 };
 
 template <typename T>
@@ -727,7 +728,10 @@ struct PlaneStager {
                         const int64_t row = a.map ? (int64_t)a.map[raster] : raster;
                         kraw[i] = *reinterpret_cast<const uint4*>(KL + row * a.ksn + piece * EP);
                         vraw[i] = *reinterpret_cast<const uint4*>(VL + row * a.vsn + piece * EP);
-                        if (a.rope.packed) {
+                        if (a.kl_rotated) {
+#pragma unroll
+                            for (int e = 0; e < EP / 2; ++e) cs[i][e] = float2{1.f, 0.f};  // not applied
+                        } else if (a.rope.packed) {
                             const int64_t pos[3] = {row, 0, 0};
 #pragma unroll
                             for (int e = 0; e < EP / 2; ++e) cs[i][e] = rope_cs(a.rope, piece * EP / 2 + e, pos);
@@ -744,7 +748,7 @@ struct PlaneStager {
 #pragma unroll
                     for (int e = 0; e < EP; e += 2) {
                         float x0 = to_f32(kv[e]), x1 = to_f32(kv[e + 1]);
-                        if (in[i]) rotate_pair(x0, x1, cs[i][e / 2].x, cs[i][e / 2].y);
+                        if (in[i] && !a.kl_rotated) rotate_pair(x0, x1, cs[i][e / 2].x, cs[i][e / 2].y);
                         kt[e] = from_f32<T>(x0);
                         kt[e + 1] = from_f32<T>(x1);
                     }
@@ -781,6 +785,119 @@ __device__ __forceinline__ uint32_t stencil_mask(const AttnDev& a, int c, int g,
     return m;
 }
 
+// Local-pathway plane staging by the LDS DMA (bf16, head_dim <= 48).  Each
+// halo plane is copied into one of two plane buffers while the previous plane
+// is scored, so no wave waits on global memory between planes.  A buffer holds
+// K and V in the same key-major layout (key row stride KSTR: D / 8 data slots
+// of 16 bytes and one spare, whose lanes fetch a piece of the same row).  K is
+// rotated in place once its copy has landed; the value fragments are read
+// with ds_read_b64_tr_b16, so V needs no transposing store.  The packed row
+// of every halo key of the brick is looked up once into a table in LDS; keys
+// outside the grid take the row of the nearest grid key (finite, and masked
+// by the stencil).
+template <typename C>
+constexpr bool kPlaneDma = kPiped<C>;
+
+template <typename C>
+struct PlaneDma {
+    typedef typename C::T_ T;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int KROW = C::KSTR / EP;           // 16-byte slots per key row
+    static constexpr int SLOTS = kPlaneKeys * KROW;      // slots of K (or V) of one plane
+    static constexpr int CH = (SLOTS + 63) / 64;         // copies per region
+    static constexpr int PER = (2 * CH + kWaves - 1) / kWaves;
+    static constexpr size_t REGION = (size_t)SLOTS * 16;
+    static constexpr size_t BUF = 2 * REGION;            // one plane: K region, then V region
+    static constexpr int kMaxPlanes = 8;                 // 4 + 2 rz with rz <= 2
+    static constexpr size_t ROWS = (size_t)kMaxPlanes * kPlaneKeys * sizeof(int);
+    static constexpr size_t BYTES = 2 * BUF + ROWS;      // two plane buffers and the row table
+    static_assert(C::KSTR % EP == 0 && C::KSTR > C::D, "key rows need a spare slot");
+
+    // Packed rows of the halo keys of planes [0, planes) (z from Z0 - rz).
+    __device__ __forceinline__ static void fill_rows(const AttnDev& a, int Z0, int Y0, int X0, int planes,
+                                                     int* rows) {
+        for (int i = threadIdx.x; i < planes * kPlaneKeys; i += blockDim.x) {
+            const int hz = i / kPlaneKeys, k = i - hz * kPlaneKeys, ky = k / kPlane, kx = k - ky * kPlane;
+            const int gz = min(max(Z0 - a.rz + hz, 0), a.Z - 1);
+            const int gy = min(max(Y0 - a.ry + ky, 0), a.Y - 1);
+            const int gx = min(max(X0 - a.rx + kx, 0), a.X - 1);
+            const int64_t raster = ((int64_t)gz * a.Y + gy) * a.X + gx;
+            rows[i] = a.map ? a.map[raster] : (int)raster;
+        }
+    }
+
+    // Issue the copies of one plane (its rows at `rows`) into `buf`.
+    __device__ __forceinline__ static void copy(const AttnDev& a, const T* KL, const T* VL, const int* rows,
+                                                unsigned char* buf, int wave, int lane) {
+        const uint32_t lds0 = lds_address(buf);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = min(wave * PER + i, 2 * CH - 1);  // wave-uniform
+            const bool v = c >= CH;
+            const int first = min(64 * (v ? c - CH : c), SLOTS - 64);
+            const int slot = first + lane, key = slot / KROW, s = slot - key * KROW;
+            const int64_t row = rows[key];
+            const int e = (s < C::D / EP ? s : 0) * EP;
+            const T* src = v ? VL + row * a.vsn + e : KL + row * a.ksn + e;
+            const uint32_t m0 = lds0 + (v ? (uint32_t)REGION : 0u) + (uint32_t)first * 16u;
+            asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+        }
+    }
+
+    // Rotate the K rows of plane hz in place (rows: that plane's row table).
+    __device__ __forceinline__ static void rotate(const AttnDev& a, T* K, const int* rows, int hz,
+                                                  const RopeWindow& win) {
+        constexpr int PPR = C::D / EP;
+        for (int i = threadIdx.x; i < kPlaneKeys * PPR; i += blockDim.x) {
+            const int key = i / PPR, piece = i - key * PPR, ky = key / kPlane, kx = key - ky * kPlane;
+            uint4* p = reinterpret_cast<uint4*>(K + key * C::KSTR + piece * EP);
+            const uint4 raw = *p;
+            const T* kv = reinterpret_cast<const T*>(&raw);
+            T kt[EP];
+#pragma unroll
+            for (int e = 0; e < EP; e += 2) {
+                const int j = piece * EP / 2 + e / 2;
+                float2 cs;
+                if (a.rope.packed) {
+                    const int64_t pos[3] = {rows[key], 0, 0};
+                    cs = rope_cs(a.rope, j, pos);
+                } else {
+                    cs = win.at(j, hz, ky, kx);
+                }
+                float x0 = to_f32(kv[e]), x1 = to_f32(kv[e + 1]);
+                rotate_pair(x0, x1, cs.x, cs.y);
+                kt[e] = from_f32<T>(x0);
+                kt[e + 1] = from_f32<T>(x1);
+            }
+            *p = *reinterpret_cast<const uint4*>(kt);
+        }
+    }
+
+    // Value fragment (A operand of O^T += V^T P^T) of block mb from the
+    // key-major V rows: lane l holds channel 32 mb + l % 32 of the 8 keys
+    // key0 .. key0 + 7 (plane key indices, consecutive in x).  Within a
+    // 16-lane block, lane B + 4a + e of ds_read_b64_tr_b16 receives element e
+    // of the 8-byte windows addressed by lanes B + a + 4j (j = 0..3), so lane
+    // l addresses key key0 + (l % 16) / 4 (four keys further for the second
+    // read) at channel 32 mb + 16 ((l / 16) % 2) + 4 (l % 4).  Blocks past D
+    // read channels of the last 16 and are replaced by the padding rows of
+    // O^T (the ones row at channel D, zeros).
+    __device__ __forceinline__ static typename C::Frag vfrag(const T* V, int key0, int mb, int lane) {
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        typedef __attribute__((address_space(3))) v4s* lds_v4s;
+        const int blk = 32 * mb + 16 * ((lane >> 4) & 1);
+        const T* p = V + (key0 + ((lane & 15) >> 2)) * C::KSTR + min(blk, C::D - 16) + 4 * (lane & 3);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)p);
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p + 4 * C::KSTR));
+        const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        typename C::Frag f = __builtin_bit_cast(typename C::Frag, v);
+        if (32 * mb + 16 >= C::D && blk >= C::D)
+            f = frag_fill<T>(C::ONES && 32 * mb + (lane & 31) == C::D ? 1.f : 0.f);
+        return f;
+    }
+};
+
 // LDS of the brick kernel: the rotation window, then the plane buffer or
 // the summary stages (whichever is larger), then -- when it still leaves room
 // for two workgroups per CU -- the park buffer of sl * o_L (4 waves x 2
@@ -798,7 +915,67 @@ constexpr size_t grid_park_bytes() {
     return (size_t)kWaves * 2 * (C::D / 8) * 64 * 4 * sizeof(typename C::T_);
 }
 template <typename C>
-constexpr bool kPark = grid_main_bytes<C>() + grid_park_bytes<C>() <= 80 * 1024;
+constexpr bool kPark = kPlaneDma<C> || grid_main_bytes<C>() + grid_park_bytes<C>() <= 80 * 1024;
+// With the plane DMA the regions after the rotation window are used twice:
+// in the local phase by the two plane buffers and the row table, in the
+// summary phase by the park buffer (over plane buffer 0, which the last
+// plane -- always of odd index -- does not use) and the summary stages.
+template <typename C>
+constexpr size_t grid_dma_bytes() {
+    constexpr size_t ep = Piece<typename C::T_>::N;
+    constexpr size_t stages = 3 * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(typename C::T_);
+    constexpr size_t summary = grid_park_bytes<C>() + stages;
+    return kRopeWindowBytes + (PlaneDma<C>::BYTES > summary ? PlaneDma<C>::BYTES : summary);
+}
+template <typename C>
+constexpr size_t grid_lds_bytes() {
+    if constexpr (kPlaneDma<C>) {
+        static_assert(grid_dma_bytes<C>() <= 80 * 1024, "two workgroups per CU");
+        static_assert(grid_park_bytes<C>() <= PlaneDma<C>::BUF, "park buffer within plane buffer 0");
+        return grid_dma_bytes<C>();
+    } else {
+        return grid_main_bytes<C>() + (kPark<C> ? grid_park_bytes<C>() : 0);
+    }
+}
+
+// Scores and products of one staged plane on this wave's two column blocks
+// (the chunks of its 8 x 8 key footprint).  Kb holds the plane's rotated K
+// rows; vfrag(c, mb, ks) returns the value fragment of chunk c.
+template <typename C, typename VFrag>
+__device__ __forceinline__ void plane_chunks(const AttnDev& a, const typename C::T_* Kb, VFrag vfrag, int hz,
+                                             int wy, int wx, int qi, int g, const uint32_t* kmask,
+                                             const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        if (4 * c >= 4 + 2 * a.ry) continue;
+        const int kap = kperm<C::E, C::KS>(qi);
+        typename C::Frag kf[C::NT], vf[C::MB * C::KSTEPS];
+        load_kfrags<C>(Kb + ((4 * wy + 4 * c + kap / 8) * kPlane + 4 * wx + kap % 8) * C::KSTR + C::E * g, kf);
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks) vf[mb * C::KSTEPS + ks] = vfrag(c, mb, ks);
+        f32x16 bias;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bias[r] = (kmask[c] >> r) & 1 ? 0.f : -INFINITY;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            // Column block nb holds query planes 2nb and 2nb + 1.
+            if (hz < 2 * nb || hz > 2 * nb + 1 + 2 * a.rz) continue;
+            f32x16 s = score_tile<C>(kf, qf[nb], bias);
+            if (hz == 2 * nb || hz == 2 * nb + 1 + 2 * a.rz) {  // only one of the two query planes reaches
+                const int qz = 2 * nb + (qi >> 4);
+                if ((unsigned)(hz - qz) > (unsigned)(2 * a.rz)) {
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[r] = -INFINITY;
+                }
+            }
+            float p[16];
+            soft_probs<C>(st[nb], s, a.scale_log2, p);
+            soft_accumulate<C>(st[nb], p, vf);
+        }
+    }
+}
 
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
@@ -824,8 +1001,19 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     const int wy = wave >> 1, wx = wave & 1;
     const int qy = (qi >> 2) & 3, qx = qi & 3;  // within the wave footprint
 
+    typedef PlaneDma<C> PD;
+    unsigned char* const planes_lds = smem + kRopeWindowBytes;  // plane DMA: two buffers, then the row table
+    int* const rowtab = reinterpret_cast<int*>(planes_lds + 2 * PD::BUF);
+    const int planes = 4 + 2 * a.rz;
+    const T* KL = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
+    const T* VL = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
     if (!a.rope.packed) build_rope_window(a, D, Z0 - a.rz, Y0 - a.ry, X0 - a.rx, win);
+    if constexpr (kPlaneDma<C>) PD::fill_rows(a, Z0, Y0, X0, planes, rowtab);
     __syncthreads();
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);
+    if constexpr (kPlaneDma<C>) {
+        if ((unsigned)(Z0 - a.rz) < (unsigned)a.Z) PD::copy(a, KL, VL, rowtab, planes_lds, uwave, lane);
+    }
 
     // ---- queries
     typename C::Frag qf[2][C::NT];
@@ -853,55 +1041,53 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     st[1].reset();
 
     // ---- local pathway: halo planes z = Z0 - rz .. Z0 + 3 + rz
-    const T* KL = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
-    const T* VL = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
     const uint32_t kmask[2] = {stencil_mask<C>(a, 0, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx),
                                stencil_mask<C>(a, 1, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx)};
-    init_v_padding<C>(Vp, VPS, kPlaneKeys);
-    const PlaneStager<C> stager;
-    const int planes = 4 + 2 * a.rz;
-    for (int hz = 0; hz < planes; ++hz) {
-        const int gz = Z0 - a.rz + hz;
-        if (hz) __syncthreads();
-        stager.stage(a, KL, VL, hz, gz, Y0, X0, win, Kp, Vp, VPS);
-        __syncthreads();
-        if ((unsigned)gz >= (unsigned)a.Z) continue;  // plane outside the grid: nothing to attend
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            if (4 * c >= 4 + 2 * a.ry) continue;
-            const int kap = kperm<C::E, C::KS>(qi);
-            typename C::Frag kf[C::NT], vf[C::MB * C::KSTEPS];
-            load_kfrags<C>(Kp + ((4 * wy + 4 * c + kap / 8) * kPlane + 4 * wx + kap % 8) * C::KSTR + C::E * g, kf);
-#pragma unroll
-            for (int mb = 0; mb < C::MB; ++mb)
-#pragma unroll
-                for (int ks = 0; ks < C::KSTEPS; ++ks) {
-                    const int k0 = ks * C::KS + C::E * g;  // chunk key (4c + k0/8, k0 % 8) of the footprint
-                    vf[mb * C::KSTEPS + ks] = frag_load8<T>(Vp + (32 * mb + qi) * VPS +
-                                                            (4 * wy + 4 * c + k0 / 8) * kPlane + 4 * wx + k0 % 8);
-                }
-            f32x16 bias;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) bias[r] = (kmask[c] >> r) & 1 ? 0.f : -INFINITY;
-#pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                // Column block nb holds query planes 2nb and 2nb + 1.
-                if (hz < 2 * nb || hz > 2 * nb + 1 + 2 * a.rz) continue;
-                f32x16 s = score_tile<C>(kf, qf[nb], bias);
-                if (hz == 2 * nb || hz == 2 * nb + 1 + 2 * a.rz) {  // only one of the two query planes reaches
-                    const int qz = 2 * nb + (qi >> 4);
-                    if ((unsigned)(hz - qz) > (unsigned)(2 * a.rz)) {
-#pragma unroll
-                        for (int r = 0; r < 16; ++r) s[r] = -INFINITY;
-                    }
-                }
-                float p[16];
-                soft_probs<C>(st[nb], s, a.scale_log2, p);
-                soft_accumulate<C>(st[nb], p, vf);
+    if constexpr (kPlaneDma<C>) {
+        for (int hz = 0; hz < planes; ++hz) {
+            const int gz = Z0 - a.rz + hz;
+            unsigned char* const buf = planes_lds + (hz & 1) * PD::BUF;
+            // Plane hz has landed, and every wave is done with plane hz - 1,
+            // whose buffer takes the copy of plane hz + 1.
+            dma_wait();
+            __syncthreads();
+            if (hz + 1 < planes && (unsigned)(gz + 1) < (unsigned)a.Z)
+                PD::copy(a, KL, VL, rowtab + (hz + 1) * kPlaneKeys, planes_lds + ((hz + 1) & 1) * PD::BUF, uwave,
+                         lane);
+            if ((unsigned)gz >= (unsigned)a.Z) continue;  // plane outside the grid: nothing to attend
+            T* const Kb = reinterpret_cast<T*>(buf);
+            const T* const Vb = reinterpret_cast<const T*>(buf + PD::REGION);
+            if (!a.kl_rotated) {
+                PD::rotate(a, Kb, rowtab + hz * kPlaneKeys, hz, win);
+                __syncthreads();
             }
+            plane_chunks<C>(a, Kb,
+                            [&](int c, int mb, int ks) {
+                                return PD::vfrag(Vb, (4 * wy + 4 * c + (ks * C::KS + C::E * g) / 8) * kPlane + 4 * wx,
+                                                 mb, lane);
+                            },
+                            hz, wy, wx, qi, g, kmask, qf, st);
+        }
+    } else {
+        init_v_padding<C>(Vp, VPS, kPlaneKeys);
+        const PlaneStager<C> stager;
+        for (int hz = 0; hz < planes; ++hz) {
+            const int gz = Z0 - a.rz + hz;
+            if (hz) __syncthreads();
+            stager.stage(a, KL, VL, hz, gz, Y0, X0, win, Kp, Vp, VPS);
+            __syncthreads();
+            if ((unsigned)gz >= (unsigned)a.Z) continue;  // plane outside the grid: nothing to attend
+            plane_chunks<C>(a, Kp,
+                            [&](int c, int mb, int ks) {
+                                const int k0 = ks * C::KS + C::E * g;  // chunk key (4c + k0/8, k0 % 8) of the footprint
+                                return frag_load8<T>(Vp + (32 * mb + qi) * VPS + (4 * wy + 4 * c + k0 / 8) * kPlane +
+                                                     4 * wx + k0 % 8);
+                            },
+                            hz, wy, wx, qi, g, kmask, qf, st);
         }
     }
-    T* park = kPark<C> ? reinterpret_cast<T*>(smem + grid_main_bytes<C>()) : nullptr;
+    T* park = kPlaneDma<C> ? reinterpret_cast<T*>(planes_lds)
+                           : (kPark<C> ? reinterpret_cast<T*>(smem + grid_main_bytes<C>()) : nullptr);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         finish_local<C>(a, b, h, qrow[nb], qok[nb], g, st[nb],
@@ -911,7 +1097,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     __syncthreads();  // the summary stages reuse the plane buffer
 
     // ---- global pathway (the rotation window is no longer needed)
-    global_pass<C, 64 * kWaves>(a, bg, Kp, qf, st, lane);
+    global_pass<C, 64 * kWaves>(a, bg, kPlaneDma<C> ? reinterpret_cast<T*>(planes_lds + grid_park_bytes<C>()) : Kp,
+                                qf, st, lane);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         if constexpr (kPark<C>)
@@ -987,13 +1174,14 @@ int fill_dev(const p3d_attn_args& x, AttnDev& d) {
     d.lse_l = x.lse_local, d.lse_g = x.lse_global;
     d.o_l = (char*)x.o_local, d.o_g = (char*)x.o_global;
     d.scale_log2 = kLog2e / sqrtf((float)x.head_dim);
+    d.kl_rotated = x.kl_rotated != 0;
     return P3D_OK;
 }
 
 template <typename T, int D>
 size_t lds_grid() {
     typedef Cfg<T, D> C;
-    return grid_main_bytes<C>() + (kPark<C> ? grid_park_bytes<C>() : 0);
+    return grid_lds_bytes<C>();
 }
 
 template <typename T, int D>

@@ -52,10 +52,23 @@ __device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
 }
 
 // Product and difference without contraction, so the rotation rounds
-// exactly as the separate fp32 multiply / subtract of rope.py:44.
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+// exactly as the separate fp32 multiply / subtract of rope.py:44, in every
+// kernel alike.  HIP's __fmul_rn and __fsub_rn are a plain * and -, which the
+// compiler may fuse into an fma (it contracts by default), and whether it
+// does depends on the surrounding kernel; the pragma marks these operations
+// as not contractible wherever they are inlined.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
 
 // Rotate one channel pair: (x0 c - x1 s, x0 s + x1 c); inverse uses -s.
 __device__ __forceinline__ void rotate_pair(float& x0, float& x1, float c, float s) {

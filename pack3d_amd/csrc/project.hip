@@ -253,6 +253,7 @@ struct PoolFuseDev {
     RopeDev rope;
     char *sk, *svt;
     float* norm;          // [B, G, 64] key-norm slots, zero on entry
+    int rotate_kl;        // store kl rotated by `rope` (rounded, rotated, rounded)
 };
 
 constexpr int kPoolFuseMaxCh = 192;  // G * D: the kg rows of 8 waves fill most of the LDS
@@ -263,11 +264,11 @@ constexpr int kPoolFuseMaxCh = 192;  // G * D: the kg rows of 8 waves fill most 
 //                              and key squares [G D]
 //   wts   [waves][G][2][32] T  slot weights hi, lo of the wave's tokens
 //   xch   [waves][16] float    softmax maxima [8] and sums [8] per head
-//   meta  [D / 2] int4         rotary pair metadata
+//   meta  [G D / 2] int4       rotary pair metadata of each pair of G heads' channels
 //   lwp   [D] float, lbias [64] float
 inline size_t pool_fuse_lds_bytes(int G, int D) {
     return (size_t)kProjWaves * 32 * (G * D + 8) * 2 + (size_t)kProjWaves * G * 64 * 2 + (size_t)kProjWaves * 16 * 4 +
-           (size_t)(D / 2) * 16 + (size_t)D * 4 + 64 * 4;
+           (size_t)(G * D / 2) * 16 + (size_t)D * 4 + 64 * 4;
 }
 
 // Static LDS of k_project / k_project_pool at model width DIM (bytes).
@@ -307,6 +308,9 @@ __device__ __forceinline__ int pick4(int x, int c1, int c2, int c3, int v0, int 
     return x < c2 ? lo : hi;
 }
 
+// Block kinds of k_project_pool.
+constexpr int kQV = 0, kKG = 1, kKL = 2, kPost = 3;
+
 template <typename T, int KS>
 __global__ __launch_bounds__(64 * kProjWaves)
 __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseDev p) {
@@ -326,27 +330,34 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     T* wts_all = rows_all + kProjWaves * 32 * KGS;
     float* xch_all = reinterpret_cast<float*>(wts_all + kProjWaves * G * 64);
     int4* meta = reinterpret_cast<int4*>(xch_all + kProjWaves * 16);
-    float* lwp = reinterpret_cast<float*>(meta + D / 2);
+    float* lwp = reinterpret_cast<float*>(meta + GD / 2);
     float* lbias = lwp + D;
     for (int c = threadIdx.x; c < DIM; c += blockDim.x) {
         lw[c] = load_any(a.ln_w, c, a.ln_dtype);
         lb[c] = load_any(a.ln_b, c, a.ln_dtype);
     }
-    for (int j = threadIdx.x; j < D / 2; j += blockDim.x) meta[j] = pair_meta(p.rope.pairs, j);
+    for (int j = threadIdx.x; j < GD / 2; j += blockDim.x) meta[j] = pair_meta(p.rope.pairs, j % (D / 2));
     for (int c = threadIdx.x; c < D; c += blockDim.x) lwp[c] = p.weight[c];
     for (int c = threadIdx.x; c < 64; c += blockDim.x) lbias[c] = p.bias[c];
     const int kg0 = p.kg0, vg0 = kg0 + GD, gbase = a.q_out + a.kv_out, nout = gbase + 2 * a.heads;
-    // Blocks of 32 output rows over [0, kg0), [kg0, vg0), [vg0, gbase) and [gbase, nout).
-    const int c1 = (kg0 + 31) / 32, c2 = c1 + (GD + 31) / 32, c3 = c2 + (GD + 31) / 32;
+    const int kl0 = a.q_out, vl0 = a.q_out + GD;
+    // Blocks of 32 output rows, in this order: q [0, kl0) and vl [vl0, kg0)
+    // in [0, c1); kg block k and kl block k alternately in [c1, c2) (the two
+    // share the rotation of their channels); vg [vg0, gbase) in [c2, c3); the
+    // gate logits [gbase, nout) after.
+    const int nq = (a.q_out + 31) / 32, nk = (GD + 31) / 32;
+    const int c1 = nq + nk, c2 = c1 + 2 * nk, c3 = c2 + nk;
     const int nblocks = c3 + (2 * a.heads + 31) / 32;
     // Values through selects (pick4), not conditionals over captured
     // variables, which the compiler turns into loads from the closure in
     // scratch memory.
     auto start_of = [=](int ob) __attribute__((always_inline)) -> int {
-        return pick4(ob, c1, c2, c3, 32 * ob, kg0 + 32 * (ob - c1), vg0 + 32 * (ob - c2), gbase + 32 * (ob - c3));
+        const int j = ob - c1;
+        return pick4(ob, c1, c2, c3, ob < nq ? 32 * ob : vl0 + 32 * (ob - nq), (j & 1 ? kl0 : kg0) + 32 * (j >> 1),
+                     vg0 + 32 * (ob - c2), gbase + 32 * (ob - c3));
     };
     auto end_of = [=](int ob) __attribute__((always_inline)) -> int {
-        return pick4(ob, c1, c2, c3, kg0, vg0, gbase, nout);
+        return pick4(ob, c1, c2, c3, ob < nq ? kl0 : kg0, (ob - c1) & 1 ? vl0 : vg0, gbase, nout);
     };
     // Weight row o of the concatenation [Wq; Wkv; Wg].
     auto wrow = [&](int o) __attribute__((always_inline)) -> const T* {
@@ -409,40 +420,57 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     }
 
     T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
-    // (cos, sin) of the lane's rotary pairs in kg block ob (channels
-    // c .. c + 3 for c = ob's first kg channel + 8 qd + 4 g, pairs of one head
-    // since 4 | D), loaded one block ahead so that the table reads' latency
-    // hides behind a block's GEMM.
+    // (cos, sin) of the lane's rotary pairs in kg (and kl) block k (channels
+    // c .. c + 3 for c = 32 k + 8 qd + 4 g, pairs of one head since 4 | D),
+    // loaded a block ahead so that the table reads' latency hides behind a
+    // block's GEMM.
     float2 csn[8];
-    auto load_cs = [&](int ob) __attribute__((always_inline)) {
+    auto load_cs = [&](int k) __attribute__((always_inline)) {
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
-            const int c = min(kg0 + 32 * (ob - c1) - kg0 + 8 * qd + 4 * g, GD - 4), cc = c % D;
+            const int c = min(32 * k + 8 * qd + 4 * g, GD - 4);
 #pragma unroll
             for (int pp = 0; pp < 2; ++pp) {
-                const int4 m = meta[(cc >> 1) + pp];
+                const int4 m = meta[(c >> 1) + pp];
                 csn[2 * qd + pp] = p.rope.table[m.x + m.y * pos[0] + m.z * pos[1] + m.w * pos[2]];
             }
         }
     };
-    // One output block: the GEMM, then the range's epilogue; PRE: q, kl, vl
-    // and kg blocks, else vg and gate blocks.  The block loop runs in two
+    // One output block: the GEMM, then the epilogue of its kind: kQV (q, vl)
+    // and kKL (kl, rotated when rotate_kl) stored; kKG rotated and kept in
+    // LDS for the pooling; kPost vg (weighted sums) and the gate logits.  The block loop runs in two
     // parts around the slot softmax, so no value of that phase is hoisted
     // into a loop and held across it.
-    auto run_block = [&](int ob, auto pre_tag) __attribute__((always_inline)) {
-        constexpr bool PRE = decltype(pre_tag)::value;
+    auto run_block = [&](int ob, auto kind_tag) __attribute__((always_inline)) {
+        constexpr int K = decltype(kind_tag)::value;
         const int o_first = start_of(ob), o_end = end_of(ob);
         const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
+        // A kl block rotates with the (cos, sin) of its kg block, the one just
+        // before it, and then loads those of the next kg block.
+        float2 cs_kl[8];
+        if constexpr (K == kKL) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) cs_kl[k] = csn[k];
+            if (((ob - c1) >> 1) + 1 < nk) load_cs(((ob - c1) >> 1) + 1);
+        }
         f32x16 d;
 #pragma unroll
         for (int r = 0; r < 16; ++r) d[r] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) d = M::mfma(*reinterpret_cast<const Frag*>(wb + 16 * ks), xf[ks], d);
-        if (PRE && ob < c1) {
-            // q / kl / vl through the tile as coalesced 16-byte row pieces (as k_project).
+        if constexpr (K == kQV || K == kKL) {
+            // q / kl / vl through the tile as coalesced 16-byte row pieces (as k_project);
+            // with rotate_kl the kl values are rounded, rotated and rounded again.
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
-                const float v[4] = {d[4 * qd], d[4 * qd + 1], d[4 * qd + 2], d[4 * qd + 3]};
+                float v[4] = {d[4 * qd], d[4 * qd + 1], d[4 * qd + 2], d[4 * qd + 3]};
+                if (K == kKL && p.rotate_kl) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = to_f32(from_f32<T>(v[i]));
+#pragma unroll
+                    for (int pp = 0; pp < 2; ++pp)
+                        rotate_pair(v[2 * pp], v[2 * pp + 1], cs_kl[2 * qd + pp].x, cs_kl[2 * qd + pp].y);
+                }
                 store4<T>(tile + t * OS + acc_row(4 * qd, g), v);
             }
             wave_lds_sync();
@@ -458,13 +486,12 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
                 }
             }
             wave_lds_sync();  // the next block's tile writes follow these reads
-        } else if (PRE) {
+        } else if constexpr (K == kKG) {
             // kg: lane (t, g) holds channels c .. c + 3 of token t for c =
             // o_first - kg0 + 8 qd + 4 g, two rotary pairs of one head (4 | D).
             float2 cs[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) cs[k] = csn[k];
-            if (ob + 1 < c2) load_cs(ob + 1);
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
                 const int c = o_first - kg0 + 8 * qd + 4 * g;
@@ -524,10 +551,13 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
         __syncthreads();
     };
     for (int ob = 0; ob < c1; ++ob) {
-        if (ob == c1 - 1) load_cs(c1);
-        run_block(ob, std::true_type{});
+        if (ob == c1 - 1) load_cs(0);
+        run_block(ob, std::integral_constant<int, kQV>{});
     }
-    for (int ob = c1; ob < c2; ++ob) run_block(ob, std::true_type{});
+    for (int ob = c1; ob < c2; ob += 2) {
+        run_block(ob, std::integral_constant<int, kKG>{});
+        run_block(ob + 1, std::integral_constant<int, kKL>{});
+    }
     {
         // Slot logits of the wave's 32 tokens for every head: lane (t, g)
         // takes half g of each head's channels, lane t ^ 32 the other.
@@ -581,7 +611,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
         for (int c = lane; c < GD; c += 64) sums[c] = park[c];
         wave_lds_sync();  // the next block's tile writes follow these reads
     }
-    for (int ob = c2; ob < nblocks; ++ob) run_block(ob, std::false_type{});
+    for (int ob = c2; ob < nblocks; ++ob) run_block(ob, std::integral_constant<int, kPost>{});
 
     // The fine block's summaries: the even wave adds its partner's sums (the
     // last block's barrier orders them).
@@ -820,7 +850,8 @@ extern "C" int p3d_project(const p3d_project_args* args, void* stream) {
     return args->dtype == P3D_F16 ? launch_project<_Float16>(d, s) : launch_project<__bf16>(d, s);
 }
 
-extern "C" int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, void* stream) {
+extern "C" int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, int32_t rotate_kl,
+                                void* stream) {
     P3D_REQUIRE(args && pool, "null args");
     ProjDev d;
     int rc = project_dev(*args, d);
@@ -860,6 +891,7 @@ extern "C" int p3d_project_pool(const p3d_project_args* args, const p3d_pool_arg
     p.sk = (char*)q.sk;
     p.svt = (char*)q.svt;
     p.norm = q.sk_norm_max;
+    p.rotate_kl = rotate_kl != 0;
     hipStream_t s = as_stream(stream);
     if (!q.norms_cleared) {
         const int n = q.batch * q.kv_heads * 64;

@@ -4,7 +4,9 @@ against the kernels they replace on the same inputs: ``p3d_project`` and then
 the same layer with the fusion switched off.
 
 q, kl, vl and the gate come from the same GEMM code as ``p3d_project``:
-bit-exact.  The summaries differ from ``p3d_pool_fwd``'s only in the order of
+bit-exact, with kl (stored rotated, as the layer asks) bit-exact against
+``p3d_rotate`` of ``p3d_project``'s kl.  The attention kernels give the same
+bits on pre-rotated keys (``kl_rotated``) as on keys they rotate themselves.  The summaries differ from ``p3d_pool_fwd``'s only in the order of
 the fp32 sums (two 32-token halves of a fine block added at the end, instead
 of one 64-slot sweep; the logits' dot products in two halves).  Both kernels'
 summaries are pinned against the oracle's pooling (compression.py restated,
@@ -94,23 +96,36 @@ def _oracle_summaries(layer, sep, plan, rope, m):
     return sk[:, :, :m] * plan.key_scale, sv[:, :, :m]
 
 
-def _compare(layer, x, layout, dtype, oracle=True):
+def _rotated(t, rope):
+    """p3d_rotate of a [B, G, N, d] view into a new contiguous tensor."""
+    b, g, n, d = t.shape
+    out = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    _lib.call("p3d_rotate", _lib.view(t), _lib.view(out), b, g, n, d, _lib.DTYPES[t.dtype], rope.struct(), 0,
+              _lib.stream_of(t.device))
+    return out
+
+
+def _compare(layer, x, layout, dtype, oracle=True, rotate_kl=1):
     dev = x.device
     stream = _lib.stream_of(dev)
     rope = layer._rope(x, layout)
     with torch.no_grad():
         fused = attention._project_buffers(layer, x)
         plan_f = _plan(layer, fused, layout, rope)
-        rc = _lib.lib().p3d_project_pool(fused[0], plan_f.pool_args, stream)
+        rc = _lib.lib().p3d_project_pool(fused[0], plan_f.pool_args, rotate_kl, stream)
         assert rc == 0, _lib.lib().p3d_last_error().decode()
         sep = attention._project_buffers(layer, x)
         _lib.call("p3d_project", sep[0], stream)
         plan_s = _plan(layer, sep, layout, rope)
         plan_s.pool()
+        h, g = layer.heads, layer.kv_heads
+        kl_f = _projection_views(fused[1], fused[2], h, g)[1]
+        kl_s = _projection_views(sep[1], sep[2], h, g)[1]
+        kl_exp = _rotated(kl_s, rope) if rotate_kl else kl_s
     torch.cuda.synchronize()
-    gd = 2 * layer.kv_heads * layer.head_dim
-    for what, got, exp in (("q", fused[1], sep[1]), ("kl, vl", fused[2][..., :gd], sep[2][..., :gd]),
-                           ("gate", fused[3], sep[3])):
+    gd = layer.kv_heads * layer.head_dim
+    for what, got, exp in (("q", fused[1], sep[1]), ("kl", kl_f.contiguous(), kl_exp.contiguous()),
+                           ("vl", fused[2][..., gd:2 * gd], sep[2][..., gd:2 * gd]), ("gate", fused[3], sep[3])):
         diff = (got.float() - exp.float()).abs()
         assert torch.equal(got, exp), (what, int((diff > 0).sum()), float(diff.max()))
     m = layout.geometry.num_summaries
@@ -153,6 +168,50 @@ def test_project_pool_packed_rope_and_morton(gpu):
                               device=gpu)
     x = torch.randn(1, 2048, 192, generator=torch.Generator().manual_seed(4)).to(gpu, dtype)
     _compare(layer, x, layout, dtype)
+
+
+def test_project_pool_unrotated_kl(gpu):
+    """rotate_kl = 0: kl as p3d_project stores it."""
+    print("project+pool kl unrotated", flush=True)
+    dtype = torch.bfloat16
+    layer = _layer(128, 8, 2, 64, dtype, gpu)
+    layout = p3d.build_layout((8, 8, 16), (4, 4, 4), radius=2, pool_size=1, layout="raster_block", device=gpu)
+    x = torch.randn(1, 1024, 128, generator=torch.Generator().manual_seed(8)).to(gpu, dtype)
+    _compare(layer, x, layout, dtype, oracle=False, rotate_kl=0)
+
+
+@pytest.mark.parametrize("dtype,d,grid", [(torch.bfloat16, 48, True), (torch.bfloat16, 32, True),
+                                          (torch.float16, 48, True), (torch.bfloat16, 64, True),
+                                          (torch.bfloat16, 48, False)])
+def test_attention_on_prerotated_keys(gpu, dtype, d, grid):
+    """The core on kl it rotates itself and on kl already rotated (kl_rotated):
+    the same bits, on the brick kernel (the plane-DMA path of bf16 d <= 48 and
+    the register-staged path of the others) and on an arbitrary graph (the
+    indexed path, which then skips its own rotation pass)."""
+    print(f"prerotated keys {dtype} d{d} grid={grid}", flush=True)
+    torch.manual_seed(9)
+    b, h, g, shape = 1, 4, 2, (8, 16, 16)
+    layout = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="native_block_morton", device=gpu)
+    geometry = layout.geometry
+    if not grid:
+        geometry = p3d.prepare_geometry(geometry.neighbors.clone(), geometry.blocks, pool_size=1)
+    n = math.prod(shape)
+    q, kl, vl, kg, vg = (torch.randn(b, x, n, d, device=gpu).to(dtype) for x in (h, g, g, g, g))
+    gate = torch.rand(b, h, n, device=gpu).to(dtype)
+    w, bias = torch.randn(d, device=gpu), torch.randn(64, device=gpu) * 0.3
+    sl, sg = torch.rand(d, device=gpu) + 0.5, torch.rand(d, device=gpu) + 0.5
+    layer = p3d.PACK3DAttention(h * d, heads=h, kv_heads=g, head_dim=d, block_volume=64).to(gpu)
+    rope = layer._rope(torch.empty(b, n, h * d, device=gpu, dtype=dtype), layout)
+    with torch.no_grad():
+        plain = ForwardPlan(q, kl, vl, kg, vg, w, bias, gate, sl, sg, geometry, 0.7, rope, rope)
+        y0, _ = plain.run()
+        klr = _rotated(kl, rope)
+        pre = ForwardPlan(q, klr, vl, kg, vg, w, bias, gate, sl, sg, geometry, 0.7, rope, rope, kl_rotated=True)
+        assert pre.grid == grid
+        y1, _ = pre.run()
+    torch.cuda.synchronize()
+    assert torch.isfinite(y0.float()).all()
+    assert torch.equal(y0, y1), float((y0.float() - y1.float()).abs().max())
 
 
 def test_project_pool_full_size_c2(gpu):

@@ -227,13 +227,13 @@ def test_project_pool_answers_unsupported_before_launch():
     lib = _lib.lib()
     for field, value in (("pool_size", 2), ("slots", 32)):
         setattr(pool, field, value)
-        assert lib.p3d_project_pool(args, pool, None) == _lib.P3D_EUNSUPPORTED
+        assert lib.p3d_project_pool(args, pool, 1, None) == _lib.P3D_EUNSUPPORTED
         setattr(pool, field, {"pool_size": 1, "slots": 64}[field])
     pool.kv_heads = 2       # kv_out no longer 4 * kv_heads * head_dim
-    assert lib.p3d_project_pool(args, pool, None) == 1
+    assert lib.p3d_project_pool(args, pool, 1, None) == 1
     assert b"kv_out" in lib.p3d_last_error()
     pool.kv_heads = g
     pool.dtype = _lib.DTYPES[torch.float16]
-    assert lib.p3d_project_pool(args, pool, None) == 1
+    assert lib.p3d_project_pool(args, pool, 1, None) == 1
     with pytest.raises(RuntimeError, match="null args"):
-        _lib.call("p3d_project_pool", None, None, None)
+        _lib.call("p3d_project_pool", None, None, 0, None)

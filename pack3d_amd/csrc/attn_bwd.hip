@@ -173,59 +173,70 @@ __global__ void k_summary_transpose(BwdDev a, int D) {
     reinterpret_cast<T*>(a.skt)[t_off] = tp<T>(a.sk)[e];
 }
 
-// Stages of SK summaries (64, or 32 when two stages of 64 would not fit in
-// LDS) for the global dQ pass: sk rows and sv rows (row stride KSTR) and sk
-// transposed (row stride SK + EP, zero padding rows up to 32 * MB),
-// double-buffered through registers.
+// Layout of a stage of SK summaries (64, or 32 when two stages of 64 would
+// not fit in LDS) for the global dQ pass: sk rows and sv rows (row stride
+// KSTR) and sk transposed (row stride SK + EP, zero padding rows up to
+// 32 * MB).  Double-buffered.
 template <typename C, int SK>
 struct DqStage {
     typedef typename C::T_ T;
     static constexpr int EP = Piece<T>::N;
     static constexpr int TGS = SK + EP;
-    static constexpr int RPIECES = SK * (C::D / EP);   // per row tensor
-    static constexpr int TPIECES = C::D * (SK / EP);   // transposed
-    static constexpr int RI = (RPIECES + 64 * kWaves - 1) / (64 * kWaves);
-    static constexpr int TI = (TPIECES + 64 * kWaves - 1) / (64 * kWaves);
     static constexpr int SIZE = 2 * SK * C::KSTR + 32 * C::MB * TGS;  // elements
-    uint4 k[RI], v[RI], t[TI];
+};
 
-    __device__ __forceinline__ void load(const BwdDev& a, int64_t bg, int base) {
-        const int limit = min(SK, a.Mp - base) * C::D;
-        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
-        const T* sv = tp<T>(a.sv_rows) + ((int64_t)bg * a.Mp + base) * C::D;
-        const T* skt = tp<T>(a.skt) + ((int64_t)bg * a.Mp + base) * C::D;
+// A dQ stage copied by the LDS DMA: sk rows, sv rows and sk^T in DqStage's
+// layout, each copy covering whole padded rows (lanes on padding
+// slots fetch a piece of the same row), the last copy of a region starting 64
+// slots before its end, and sources clamped into the rows present.  Copies
+// are split evenly over the waves (a wave with fewer repeats the last one).
+template <typename C, int SK>
+struct DqDma {
+    typedef typename C::T_ T;
+    typedef DqStage<C, SK> S;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int KROW = C::KSTR / EP, TROW = S::TGS / EP;  // 16-byte slots per padded row
+    static constexpr int RSLOTS = SK * KROW, TSLOTS = C::D * TROW;
+    static constexpr int RCH = (RSLOTS + 63) / 64, TCH = (TSLOTS + 63) / 64;
+    static constexpr int CH = 2 * RCH + TCH, PER = (CH + kWaves - 1) / kWaves;
+    static_assert(C::KSTR % EP == 0 && S::TGS % EP == 0 && RSLOTS >= 64 && TSLOTS >= 64, "stage layout");
+    uint32_t off[PER];  // byte offset of this lane's source piece in the stage's block
+    int wave;
+
+    __device__ __forceinline__ static int chunk(int w, int i) { return min(w * PER + i, CH - 1); }
+    __device__ __forceinline__ static int region(int c) { return c < RCH ? 0 : (c < 2 * RCH ? 1 : 2); }
+    __device__ __forceinline__ static int first_slot(int c) {
+        const int r = region(c);
+        return r < 2 ? min(64 * (c - r * RCH), RSLOTS - 64) : min(64 * (c - 2 * RCH), TSLOTS - 64);
+    }
+
+    __device__ __forceinline__ DqDma() {
+        wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63;
 #pragma unroll
-        for (int i = 0; i < RI; ++i) {
-            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
-            k[i] = off < limit ? *reinterpret_cast<const uint4*>(sk + off) : uint4{0, 0, 0, 0};
-            v[i] = off < limit ? *reinterpret_cast<const uint4*>(sv + off) : uint4{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            const int off = (threadIdx.x + i * 64 * kWaves) * EP;
-            t[i] = off < limit ? *reinterpret_cast<const uint4*>(skt + off) : uint4{0, 0, 0, 0};
+        for (int i = 0; i < PER; ++i) {
+            const int c = chunk(wave, i), slot = first_slot(c) + lane;
+            int e;
+            if (region(c) < 2) {
+                const int row = slot / KROW, p = slot % KROW;
+                e = row * C::D + (p < C::D / EP ? p : 0) * EP;
+            } else {
+                const int ch = slot / TROW, p = slot % TROW, dp = p < SK / EP ? p : 0;
+                e = (dp / (32 / EP)) * C::D * 32 + ch * 32 + (dp % (32 / EP)) * EP;
+            }
+            off[i] = (uint32_t)e * sizeof(T);
         }
     }
 
-    __device__ __forceinline__ void store(T* stage) const {
+    __device__ __forceinline__ void copy(const BwdDev& a, int64_t bg, int base, T* stage) const {
+        const uint32_t last = (uint32_t)(min(SK, a.Mp - base) * C::D - EP) * sizeof(T);
+        const int64_t e0 = ((int64_t)bg * a.Mp + base) * C::D;
+        const uint32_t lds0 = lds_address(stage);
 #pragma unroll
-        for (int i = 0; i < RI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
-            if (p < RPIECES) {
-                const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
-                *reinterpret_cast<uint4*>(stage + r * C::KSTR + c) = k[i];
-                *reinterpret_cast<uint4*>(stage + SK * C::KSTR + r * C::KSTR + c) = v[i];
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            const int p = threadIdx.x + i * 64 * kWaves;
-            if (p < TPIECES) {
-                const int tt = p / (C::D * (32 / EP));
-                const int rem = p - tt * C::D * (32 / EP);
-                const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
-                *reinterpret_cast<uint4*>(stage + 2 * SK * C::KSTR + ch * TGS + 32 * tt + kk) = t[i];
-            }
+        for (int i = 0; i < PER; ++i) {
+            const int c = chunk(wave, i), r = region(c);
+            const T* src = r == 0 ? tp<T>(a.sk) + e0 : (r == 1 ? tp<T>(a.sv_rows) + e0 : tp<T>(a.skt) + e0);
+            dma_copy16(src, min(off[i], last), lds0 + (uint32_t)(r * RSLOTS + first_slot(c)) * 16u);
         }
     }
 };
@@ -300,14 +311,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
 
     zero_padding_rows<C>(lds + 2 * SK * C::KSTR, S::TGS, SK);
     zero_padding_rows<C>(lds + S::SIZE + 2 * SK * C::KSTR, S::TGS, SK);
-    S regs;
-    regs.load(a, bg, 0);
-    regs.store(lds);
+    const DqDma<C, SK> dma;
+    dma.copy(a, bg, 0, lds);
+    dma_wait();
     __syncthreads();
     int buf = 0;
     for (int base = 0; base < a.M; base += SK) {
         const int next = base + SK;
-        if (next < a.M) regs.load(a, bg, next);
+        // The other buffer held the previous stage, which every wave finished
+        // before the last barrier.
+        if (next < a.M) dma.copy(a, bg, next, lds + (buf ^ 1) * S::SIZE);
         const T* cur = lds + buf * S::SIZE;
 #pragma unroll
         for (int tt = 0; tt < SK / 32; ++tt) {
@@ -338,7 +351,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
                 }
             }
         }
-        if (next < a.M) regs.store(lds + (buf ^ 1) * S::SIZE);
+        dma_wait();
         __syncthreads();
         buf ^= 1;
     }

@@ -178,6 +178,48 @@ __device__ __forceinline__ void load_kfrags(const typename C::T_* krow, typename
     for (int t = 0; t < C::NT; ++t) kf[t] = frag_load16<typename C::T_>(krow + t * C::KS);
 }
 
+// ------------------------------------------------------------- LDS DMA
+// LDS byte address of a pointer into the workgroup's shared memory.
+template <typename T>
+__device__ __forceinline__ uint32_t lds_address(const T* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
+}
+
+// One LDS DMA copy (global_load_lds_dwordx4): lane i's 16 bytes from global
+// memory go to LDS byte address m0 + 16 i, with no register in between.  m0
+// is wave-uniform.  Completion counts on the vector-memory counter.
+__device__ __forceinline__ void dma_copy16(const void* base, uint32_t offset, uint32_t m0) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(offset), "s"(base), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void dma_copy16(const void* src, uint32_t m0) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
+// Wait for this wave's LDS DMA copies and its LDS reads, before the barrier
+// after which another wave's copy may overwrite what they read.
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); }
+
+// Transposed fragment of 16-bit rows for a 32x32x16 A operand: lane l holds
+// column (channel) c0 + l % 32 of the 8 rows row0 .. row0 + 7 (row stride
+// `stride` elements), from two ds_read_b64_tr_b16.  Within a 16-lane block,
+// lane B + 4a + e receives element e of the 8-byte windows addressed by lanes
+// B + a + 4j (j = 0..3), so lane l addresses row row0 + (l % 16) / 4 (four
+// rows further for the second read) at column c0 + 16 ((l / 16) % 2) +
+// 4 (l % 4).  cmax: the last 16-column block that may be read (blocks past it
+// read that one instead; the caller replaces their values).
+template <typename T, typename Frag>
+__device__ __forceinline__ Frag tr_frag(const T* rows, int row0, int stride, int c0, int cmax, int lane) {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) v4s* lds_v4s;
+    const int blk = min(c0 + 16 * ((lane >> 4) & 1), cmax);
+    const T* p = rows + (row0 + ((lane & 15) >> 2)) * stride + blk + 4 * (lane & 3);
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)p);
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p + 4 * stride));
+    const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(Frag, v);
+}
+
 // The running max only moves when a tile's max exceeds it by more than this
 // many log2 units, so the accumulator is rarely rescaled; probabilities are
 // then bounded by 2^kLazy, far inside the fp32 / bf16 / fp16 range.

@@ -185,12 +185,6 @@ struct StageRegs {
     }
 };
 
-// LDS byte address of a pointer into the workgroup's shared memory.
-template <typename T>
-__device__ __forceinline__ uint32_t lds_address(const T* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
-}
-
 // Summary stages of the pipelined sweep, copied by the LDS DMA
 // (global_load_lds_dwordx4): the pieces go from L2 straight into LDS, with no
 // registers to hold them and no LDS store instructions.  One copy writes 64
@@ -253,16 +247,10 @@ struct StageDma {
             const int c = chunk(wave, i);
             const uint32_t m0 = lds0 + (uint32_t)(c < KCH ? first_piece(c) : KPIECES + first_piece(c)) * 16u;
             const T* src = c < KCH ? sk : svt;
-            asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(min(off[i], last)), "s"(src), "{m0}"(m0)
-                         : "memory");
+            dma_copy16(src, min(off[i], last), m0);
         }
     }
 };
-
-// Wait for this wave's LDS DMA copies (they count as vector-memory loads) and
-// its LDS reads, before the barrier after which another wave's copy may
-// overwrite what they read.
-__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory"); }
 
 // One summary stage (two 32-key tiles) on this wave's two column blocks.
 template <typename C, bool BOUND>
@@ -840,7 +828,7 @@ struct PlaneDma {
             const int e = (s < C::D / EP ? s : 0) * EP;
             const T* src = v ? VL + row * a.vsn + e : KL + row * a.ksn + e;
             const uint32_t m0 = lds0 + (v ? (uint32_t)REGION : 0u) + (uint32_t)first * 16u;
-            asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+            dma_copy16(src, m0);
         }
     }
 
@@ -875,24 +863,13 @@ struct PlaneDma {
 
     // Value fragment (A operand of O^T += V^T P^T) of block mb from the
     // key-major V rows: lane l holds channel 32 mb + l % 32 of the 8 keys
-    // key0 .. key0 + 7 (plane key indices, consecutive in x).  Within a
-    // 16-lane block, lane B + 4a + e of ds_read_b64_tr_b16 receives element e
-    // of the 8-byte windows addressed by lanes B + a + 4j (j = 0..3), so lane
-    // l addresses key key0 + (l % 16) / 4 (four keys further for the second
-    // read) at channel 32 mb + 16 ((l / 16) % 2) + 4 (l % 4).  Blocks past D
-    // read channels of the last 16 and are replaced by the padding rows of
-    // O^T (the ones row at channel D, zeros).
+    // key0 .. key0 + 7 (plane key indices, consecutive in x), read with
+    // ds_read_b64_tr_b16 (tr_frag).  Blocks of 16 channels past D read the
+    // last 16 and are replaced by the padding rows of O^T (the ones row at
+    // channel D, zeros).
     __device__ __forceinline__ static typename C::Frag vfrag(const T* V, int key0, int mb, int lane) {
-        typedef short v4s __attribute__((ext_vector_type(4)));
-        typedef short v8s __attribute__((ext_vector_type(8)));
-        typedef __attribute__((address_space(3))) v4s* lds_v4s;
-        const int blk = 32 * mb + 16 * ((lane >> 4) & 1);
-        const T* p = V + (key0 + ((lane & 15) >> 2)) * C::KSTR + min(blk, C::D - 16) + 4 * (lane & 3);
-        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)p);
-        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s)(p + 4 * C::KSTR));
-        const v8s v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        typename C::Frag f = __builtin_bit_cast(typename C::Frag, v);
-        if (32 * mb + 16 >= C::D && blk >= C::D)
+        typename C::Frag f = tr_frag<T, typename C::Frag>(V, key0, C::KSTR, 32 * mb, C::D - 16, lane);
+        if (32 * mb + 16 >= C::D && 32 * mb + 16 * ((lane >> 4) & 1) >= C::D)
             f = frag_fill<T>(C::ONES && 32 * mb + (lane & 31) == C::D ? 1.f : 0.f);
         return f;
     }

@@ -645,7 +645,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
 // is the B operand as loaded), 32 outputs per block.  The block's fp32
 // accumulators go through the wave's tile, and the store phase adds the
 // residual piece and rounds once, as a GEMM with the residual as its C
-// operand does.
+// operand does.  The residual pieces of a block are loaded a block ahead.
 template <typename T, int KS>
 __global__ __launch_bounds__(64 * kProjWaves) __attribute__((amdgpu_waves_per_eu(KS <= 12 ? 4 : 2)))
 void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const T* __restrict__ x, T* __restrict__ out,
@@ -689,9 +689,22 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const T* 
     Frag yf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) yf[ks] = __builtin_bit_cast(Frag, *reinterpret_cast<const u32x4*>(yr + 16 * ks));
+    // Residual pieces: lane (tt = 16 i + lane / 4, pp = lane % 4) of block ob
+    // adds x[tok0 + tt][32 ob + 8 pp .. + 8].
+    auto load_res = [&](int ob, u32x4* r) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t tk = min(tok0 + 16 * i + (lane >> 2), rows - 1);
+            r[i] = *reinterpret_cast<const u32x4*>(x + tk * dim + 32 * ob + 8 * (lane & 3));
+        }
+    };
+    u32x4 resn[2];
+    load_res(0, resn);
 
     for (int ob = 0; ob < nblocks; ++ob) {
         const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
+        u32x4 resv[2] = {resn[0], resn[1]};
+        if (ob + 1 < nblocks) load_res(ob + 1, resn);
         f32x16 d;
 #pragma unroll
         for (int r = 0; r < 16; ++r) d[r] = 0.f;
@@ -709,8 +722,7 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const T* 
             if (tk < rows) {
                 const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp);
                 const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp + 4);
-                const u32x4 res = *reinterpret_cast<const u32x4*>(x + tk * dim + o0);
-                const T* rv = reinterpret_cast<const T*>(&res);
+                const T* rv = reinterpret_cast<const T*>(&resv[i]);
                 u32x4 o;
                 T* ov = reinterpret_cast<T*>(&o);
 #pragma unroll

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 13
+#define P3D_ABI_VERSION 14
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -249,7 +249,7 @@ int p3d_layer_norm_train(const void* x, const void* weight, const void* bias, in
 
 /* LayerNorm backward (torch's layer_norm backward): with xhat = (x - mean)
  * rstd and g = dy * weight, dx = rstd (g - mean(g) - xhat mean(g xhat)) per
- * row, plus dres (may be NULL; [rows, dim] of dy_dtype: the gradient that
+ * row, plus dres (may be NULL; [rows, dim] of dx_dtype: the gradient that
  * reaches x through the residual branch) added in fp32, written as dx_dtype;
  * the affine gradients as fp32 partial sums over `parts` row ranges,
  * partial[part][0][dim] = sum dy xhat and partial[part][1][dim] = sum dy (the
@@ -310,14 +310,17 @@ int p3d_project(const p3d_project_args* args, void* stream);
 int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, int32_t rotate_kl, void* stream);
 
 /* Output projection with the residual (attention.py:89): out = x + y Wo^T for
- * y [rows, k] (the core's output, heads concatenated), Wo [dim, k] and x,
- * out [rows, dim], all of dtype (fp16 or bf16), contiguous and 16-byte
- * aligned; fp32 accumulation and one rounding of x + y Wo^T, as
- * torch.addmm(x, y, Wo^T).  Replaces the layer's to_out nn.Linear and
- * residual add in the no-grad forward.  k in {64, 96, 128, 192, 256, 384,
+ * y [rows, k] (the core's output, heads concatenated) and Wo [dim, k] of
+ * dtype (fp16 or bf16), x and out [rows, dim] of res_dtype, all contiguous
+ * and 16-byte aligned.  res_dtype == dtype: fp32 accumulation and one
+ * rounding of x + y Wo^T, as torch.addmm(x, y, Wo^T); it replaces the
+ * layer's to_out nn.Linear and residual add in the no-grad forward.
+ * res_dtype == P3D_F32 (autocast over an fp32 input): y Wo^T rounded to dtype
+ * and added to the unrounded x in fp32, as the reference's sum of an fp32
+ * residual and a 16-bit to_out output.  k in {64, 96, 128, 192, 256, 384,
  * 512}; dim a multiple of 32, at most 512. */
 int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int32_t k,
-                     int32_t dim, int32_t dtype, void* stream);
+                     int32_t dim, int32_t dtype, int32_t res_dtype, void* stream);
 
 /* Copy of a [batch, heads, tokens, head_dim] tensor between two strided
  * views with contiguous, 16-byte aligned rows: a dense gradient of the

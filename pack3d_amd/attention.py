@@ -26,7 +26,8 @@ from torch import nn
 
 from . import _lib
 from .core import SUPPORTED_HEAD_DIMS, ForwardPlan, _projection_views, _validate_inputs, pack3d_hip_projections
-from .linear import InputProjections, LayerNormTrain, OutputResidual, compute_dtype, layer_norm_train_supported
+from .linear import (InputProjections, LayerNormTrain, OutputResidual, OutputResidualWide, compute_dtype,
+                     layer_norm_train_supported, wide_residual_supported)
 from .geometry import TokenLayout, blocks_consecutive
 from .rope import axial_rope, balanced_pairs, packed_rope
 
@@ -170,7 +171,7 @@ def fused_out_residual(layer, x, y):
     xc = x.contiguous()
     out = torch.empty_like(xc)
     _lib.call("p3d_out_residual", y.data_ptr(), w.data_ptr(), xc.data_ptr(), out.data_ptr(), y.shape[0], k,
-              layer.dim, _lib.DTYPES[dt], _lib.stream_of(x.device))
+              layer.dim, _lib.DTYPES[dt], _lib.DTYPES[dt], _lib.stream_of(x.device))
     return out
 
 
@@ -238,6 +239,9 @@ class PACK3DAttention(nn.Module):
             if layer_norm_train_supported(self.norm, x):
                 if x.dtype == dt:  # the residual copy is the output product's accumulator
                     xn, res = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt, True)
+                elif wide_residual_supported(x, self.heads * self.head_dim, self.dim, dt):
+                    # x itself, for the output product's fp32 residual (one consumer of x)
+                    xn, res = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt, "pass")
                 else:
                     xn = LayerNormTrain.apply(x, self.norm.weight, self.norm.bias, self.norm.eps, dt)
             else:
@@ -280,6 +284,8 @@ class PACK3DAttention(nn.Module):
             if x.dtype != dt:
                 # Autocast over a wider x: the residual keeps x's type and is
                 # not rounded, as in the reference's sum (attention.py:89).
+                if res is not None:  # x as LayerNormTrain passed it through (fp32)
+                    return OutputResidualWide.apply(res, o, self.to_out.weight, dt).view(b, n, self.dim)
                 return x + OutputResidual.apply(None, o, self.to_out.weight, dt).view(b, n, self.dim)
             if res is not None:  # LayerNormTrain's dt copy of x, owned by this step
                 return OutputResidual.apply(res, o, self.to_out.weight, dt, True).view(b, n, self.dim)

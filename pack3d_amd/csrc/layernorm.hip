@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const voi
 // part[block][0 / 1][dim], summed by the caller.  PPL: pieces per lane
 // (ceil(dim / EP / 8)), which sizes the per-lane arrays.
 template <typename TD, typename TI, typename TO, int PPL>
-__global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TD* dres, const TI* x, const void* w,
+__global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* dres, const TI* x, const void* w,
                                                         int param_dtype, const float* mean_in, const float* rstd_in,
                                                         TO* dx, float* part, int64_t rows, int dim, int parts) {
     constexpr int EP = Piece<TI>::N;
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TD* 
                 for (int e = 0; e < EP; ++e) o[e] = rstd * (g[i][e] - mg - xh[i][e] * mgx);
                 if (dres) {
                     float r[EP];
-                    load_n<TD, EP>(dres + row * dim + p * EP, r);
+                    load_n<TO, EP>(dres + row * dim + p * EP, r);
 #pragma unroll
                     for (int e = 0; e < EP; ++e) o[e] += r[e];
                 }
@@ -300,7 +300,7 @@ int launch_ln_bwd(const void* dy, const void* dres, const void* x, const void* w
     case P:                                                                                                      \
         k_layer_norm_bwd<TD, TI, TO, P>                                                                          \
             <<<grid_for(reinterpret_cast<const void*>(k_layer_norm_bwd<TD, TI, TO, P>)), 256, 0, s>>>(          \
-                (const TD*)dy, (const TD*)dres, (const TI*)x, w, pdt, mean, rstd, (TO*)dx, part, rows, dim,      \
+                (const TD*)dy, (const TO*)dres, (const TI*)x, w, pdt, mean, rstd, (TO*)dx, part, rows, dim,      \
                 parts);                                                                                          \
         break;
         CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)

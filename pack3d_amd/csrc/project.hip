@@ -645,11 +645,14 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
 // is the B operand as loaded), 32 outputs per block.  The block's fp32
 // accumulators go through the wave's tile, and the store phase adds the
 // residual piece and rounds once, as a GEMM with the residual as its C
-// operand does.  The residual pieces of a block are loaded a block ahead.
-template <typename T, int KS>
+// operand does.  With a residual and output R = float (autocast over an fp32
+// input), the product is rounded to T and added to the unrounded residual in
+// fp32, as the reference's ``residual + to_out(...)`` does there.
+template <typename T, int KS, typename R>
 __global__ __launch_bounds__(64 * kProjWaves) __attribute__((amdgpu_waves_per_eu(KS <= 12 ? 4 : 2)))
-void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const T* __restrict__ x, T* __restrict__ out,
+void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* __restrict__ x, R* __restrict__ out,
                     int64_t rows, int dim) {
+    constexpr int RP = (int)sizeof(R) / 2;  // 16-byte pieces per 8 outputs
     typedef Mma<T> M;
     typedef typename M::Frag Frag;
     constexpr int K = 16 * KS;
@@ -691,20 +694,34 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const T* 
     for (int ks = 0; ks < KS; ++ks) yf[ks] = __builtin_bit_cast(Frag, *reinterpret_cast<const u32x4*>(yr + 16 * ks));
     // Residual pieces: lane (tt = 16 i + lane / 4, pp = lane % 4) of block ob
     // adds x[tok0 + tt][32 ob + 8 pp .. + 8].
-    auto load_res = [&](int ob, u32x4* r) __attribute__((always_inline)) {
+    auto load_res = [&](int ob, u32x4 (*r)[RP]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int64_t tk = min(tok0 + 16 * i + (lane >> 2), rows - 1);
-            r[i] = *reinterpret_cast<const u32x4*>(x + tk * dim + 32 * ob + 8 * (lane & 3));
+#pragma unroll
+            for (int h = 0; h < RP; ++h)
+                r[i][h] = *reinterpret_cast<const u32x4*>(x + tk * dim + 32 * ob + 8 * (lane & 3) + h * (8 / RP));
         }
     };
-    u32x4 resn[2];
-    load_res(0, resn);
+    // 16-bit residuals are loaded a block ahead; fp32 ones, twice the
+    // registers, at the start of their own block (before its GEMM), which
+    // keeps the kernel within the 128 registers of 4 waves per SIMD.
+    constexpr bool AHEAD = RP == 1;
+    u32x4 resn[2][RP];
+    if constexpr (AHEAD) load_res(0, resn);
 
     for (int ob = 0; ob < nblocks; ++ob) {
         const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
-        u32x4 resv[2] = {resn[0], resn[1]};
-        if (ob + 1 < nblocks) load_res(ob + 1, resn);
+        u32x4 resv[2][RP];
+        if constexpr (AHEAD) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int h = 0; h < RP; ++h) resv[i][h] = resn[i][h];
+            if (ob + 1 < nblocks) load_res(ob + 1, resn);
+        } else {
+            load_res(ob, resv);
+        }
         f32x16 d;
 #pragma unroll
         for (int r = 0; r < 16; ++r) d[r] = 0.f;
@@ -722,15 +739,21 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const T* 
             if (tk < rows) {
                 const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp);
                 const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp + 4);
-                const T* rv = reinterpret_cast<const T*>(&resv[i]);
-                u32x4 o;
-                T* ov = reinterpret_cast<T*>(&o);
+                const R* rv = reinterpret_cast<const R*>(&resv[i][0]);
+                u32x4 o[RP];
+                R* ov = reinterpret_cast<R*>(&o[0]);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    ov[e] = from_f32<T>(lo[e] + to_f32(rv[e]));
-                    ov[4 + e] = from_f32<T>(hi[e] + to_f32(rv[4 + e]));
+                    if constexpr (std::is_same<R, float>::value) {
+                        ov[e] = to_f32(from_f32<T>(lo[e])) + rv[e];
+                        ov[4 + e] = to_f32(from_f32<T>(hi[e])) + rv[4 + e];
+                    } else {
+                        ov[e] = from_f32<T>(lo[e] + to_f32(rv[e]));
+                        ov[4 + e] = from_f32<T>(hi[e] + to_f32(rv[4 + e]));
+                    }
                 }
-                *reinterpret_cast<u32x4*>(out + tk * dim + o0) = o;
+#pragma unroll
+                for (int h = 0; h < RP; ++h) *reinterpret_cast<u32x4*>(out + tk * dim + o0 + h * (8 / RP)) = o[h];
             }
         }
         wave_lds_sync();
@@ -757,15 +780,15 @@ int launch_project(const ProjDev& d, hipStream_t s) {
     return check_launch("p3d_project");
 }
 
-template <typename T>
+template <typename T, typename R>
 int launch_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int k, int dim,
                         hipStream_t s) {
     const unsigned blocks = (unsigned)cdiv(cdiv(rows, 32), kProjWaves);
     switch (k) {
-#define CASE(KK)                                                                                               \
-    case KK:                                                                                                   \
-        k_out_residual<T, KK / 16><<<blocks, 64 * kProjWaves, 0, s>>>((const T*)y, (const T*)wo, (const T*)x, \
-                                                                      (T*)out, rows, dim);                     \
+#define CASE(KK)                                                                                                  \
+    case KK:                                                                                                      \
+        k_out_residual<T, KK / 16, R><<<blocks, 64 * kProjWaves, 0, s>>>((const T*)y, (const T*)wo, (const R*)x, \
+                                                                         (R*)out, rows, dim);                     \
         break;
         CASE(64) CASE(96) CASE(128) CASE(192) CASE(256) CASE(384) CASE(512)
 #undef CASE
@@ -801,16 +824,20 @@ __global__ void k_zero_norm_slots(float* p, int n) {
 using namespace p3d;
 
 extern "C" int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, int64_t rows, int32_t k,
-                                int32_t dim, int32_t dtype, void* stream) {
+                                int32_t dim, int32_t dtype, int32_t res_dtype, void* stream) {
     P3D_REQUIRE(y && wo && x && out, "null pointer argument");
     P3D_REQUIRE(dtype == P3D_F16 || dtype == P3D_BF16, "dtype must be fp16 or bf16");
+    P3D_REQUIRE(res_dtype == dtype || res_dtype == P3D_F32, "the residual must be of dtype or fp32");
     P3D_REQUIRE(rows >= 1, "need at least one row");
     P3D_REQUIRE(dim >= 32 && dim % 32 == 0 && dim <= kProjMaxDim, "dim must be a multiple of 32, at most 512");
     P3D_REQUIRE(aligned16(y) && aligned16(wo) && aligned16(x) && aligned16(out), "pointers must be 16-byte aligned");
     P3D_REQUIRE(cdiv(rows, 32 * kProjWaves) < (1LL << 31), "too many rows");
     hipStream_t s = as_stream(stream);
-    return dtype == P3D_F16 ? launch_out_residual<_Float16>(y, wo, x, out, rows, k, dim, s)
-                            : launch_out_residual<__bf16>(y, wo, x, out, rows, k, dim, s);
+    if (res_dtype == P3D_F32)
+        return dtype == P3D_F16 ? launch_out_residual<_Float16, float>(y, wo, x, out, rows, k, dim, s)
+                                : launch_out_residual<__bf16, float>(y, wo, x, out, rows, k, dim, s);
+    return dtype == P3D_F16 ? launch_out_residual<_Float16, _Float16>(y, wo, x, out, rows, k, dim, s)
+                            : launch_out_residual<__bf16, __bf16>(y, wo, x, out, rows, k, dim, s);
 }
 
 namespace {

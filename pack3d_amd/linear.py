@@ -91,10 +91,11 @@ class LayerNormTrain(torch.autograd.Function):
 
     With residual=True the forward also returns x rounded to dt as a
     [rows, dim] tensor, written from the same read of x: the residual operand
-    of the output product (OutputResidual with x_owned=True).  The backward
-    then adds that output's gradient into dx inside the kernel, where autograd
-    would otherwise cast it to x's dtype and sum the two gradients of x in a
-    separate pass."""
+    of the output product (OutputResidual with x_owned=True).  With
+    residual="pass" it returns x itself as [rows, dim] (the unrounded residual
+    of autocast over a wider x, for OutputResidualWide).  Either way the
+    backward adds that output's gradient into dx inside the kernel, where
+    autograd would otherwise sum the two gradients of x in a separate pass."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, eps, dt, residual=False):
@@ -111,6 +112,8 @@ class LayerNormTrain(torch.autograd.Function):
         ctx.save_for_backward(x2, weight, mean, rstd)
         ctx.meta = (x.shape, bias.dtype)
         ctx.set_materialize_grads(False)
+        if residual == "pass":
+            return y.view(x.shape), x2
         if residual:
             return y.view(x.shape), xc
         return y.view(x.shape)
@@ -125,8 +128,8 @@ class LayerNormTrain(torch.autograd.Function):
         dy2 = _rows(dy).contiguous()
         if dy2.dtype not in _lib.DTYPES:
             dy2 = dy2.float()
-        dr = None if dres is None else _rows(dres).to(dy2.dtype).contiguous()
         dx = torch.empty_like(x2)
+        dr = None if dres is None else _rows(dres).to(dx.dtype).contiguous()
         parts = max(1, min(1024, rows // 256))
         part = torch.empty(parts, 2, dim, dtype=torch.float32, device=x2.device)
         _lib.call("p3d_layer_norm_bwd", dy2.data_ptr(), 0 if dr is None else dr.data_ptr(), x2.data_ptr(),
@@ -182,6 +185,44 @@ class InputProjections(torch.autograd.Function):
             dx = torch.zeros(x16.shape, dtype=x16.dtype, device=x16.device)
         dbg = None if dgl is None else _rows(dgl).float().sum(0).to(bg_dt)
         return dx.view(shape).to(x_dt), grads[0], grads[1], grads[2], dbg, None
+
+
+def wide_residual_supported(x, k, dim, dt):
+    """Whether p3d_out_residual takes an fp32 residual x [.., dim] for the
+    product of width k in the 16-bit type dt."""
+    return (x.is_cuda and x.dtype == torch.float32 and dt in (torch.float16, torch.bfloat16)
+            and k in (64, 96, 128, 192, 256, 384, 512) and dim % 32 == 0 and dim <= 512)
+
+
+class OutputResidualWide(torch.autograd.Function):
+    """x + y Wo^T under autocast over an fp32 input (attention.py:89): the
+    product in the 16-bit type dt, rounded to dt, added to the unrounded fp32
+    residual x [rows, dim], as the reference's ``residual + to_out(...)`` sums
+    an fp32 tensor and a 16-bit one; y [rows, k].  One kernel
+    (``p3d_out_residual`` with an fp32 residual) instead of the product, a
+    16-bit intermediate and a torch add.  The backward gives dx = dout
+    (fp32), dy = dout Wo and an fp32 weight gradient, as OutputResidual's."""
+
+    @staticmethod
+    def forward(ctx, x, y, wo, dt):
+        y16 = y.to(dt).contiguous()
+        wo16 = wo.to(dt).contiguous()
+        x2 = x.contiguous()
+        rows, dim = x2.shape
+        out = torch.empty_like(x2)
+        _lib.call("p3d_out_residual", y16.data_ptr(), wo16.data_ptr(), x2.data_ptr(), out.data_ptr(), rows,
+                  y16.shape[1], dim, _lib.DTYPES[dt], _lib.DTYPES[torch.float32], _lib.stream_of(x2.device))
+        ctx.save_for_backward(y16, wo16)
+        ctx.meta = (y.dtype, wo.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        y16, wo16 = ctx.saved_tensors
+        y_dt, wo_dt = ctx.meta
+        d16 = dout.to(y16.dtype)
+        dy = torch.mm(d16, wo16).to(y_dt)
+        return dout, dy, weight_grad(d16, y16).to(wo_dt), None
 
 
 class OutputResidual(torch.autograd.Function):

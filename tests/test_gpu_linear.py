@@ -111,13 +111,14 @@ def test_layer_training_gradients_match_torch_linear(gpu, dtype):
 @pytest.mark.parametrize("x_dtype,y_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float16),
                                               (torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32)])
 @pytest.mark.parametrize("rows,dim", [(1, 192), (1003, 192), (517, 64), (300, 512)])
-@pytest.mark.parametrize("residual", [False, True])
+@pytest.mark.parametrize("residual", [False, True, "pass"])
 def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, rows, dim, residual):
     """LayerNormTrain against torch.layer_norm in fp64 on the same inputs: the
     output to one rounding of the output type, dx to fp32 accuracy, the
     affine gradients summed over the rows.  With the residual copy: the copy
     is x cast to the output type (bit-exact), and its gradient is added to
-    dx."""
+    dx.  With the pass-through: x itself, its gradient (in x's type) added
+    to dx."""
     if dim // (16 // torch.tensor([], dtype=x_dtype).element_size()) > 64:
         pytest.skip("more than 64 pieces per row")
     print(f"layer norm train {rows}x{dim} {x_dtype}->{y_dtype} residual={residual}", flush=True)
@@ -126,9 +127,13 @@ def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, ro
     w = torch.randn(dim, device=gpu, generator=gen)
     b = torch.randn(dim, device=gpu, generator=gen)
     dy = torch.randn(rows, dim, device=gpu, generator=gen).to(y_dtype)
-    dres = torch.randn(rows, dim, device=gpu, generator=gen).to(y_dtype)
+    dres = torch.randn(rows, dim, device=gpu, generator=gen).to(x_dtype if residual == "pass" else y_dtype)
     xg, wg, bg = (t.clone().requires_grad_() for t in (x, w, b))
-    if residual:
+    if residual == "pass":
+        y, xr = linear.LayerNormTrain.apply(xg, wg, bg, 1e-5, y_dtype, "pass")
+        assert xr.dtype == x_dtype and torch.equal(xr, x)
+        torch.autograd.backward([y, xr], [dy, dres])
+    elif residual:
         y, xc = linear.LayerNormTrain.apply(xg, wg, bg, 1e-5, y_dtype, True)
         assert xc.dtype == y_dtype and torch.equal(xc, x.to(y_dtype))
         torch.autograd.backward([y, xc], [dy, dres])
@@ -150,6 +155,34 @@ def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, ro
     tol = 1e-5 if x_dtype == torch.float32 else 1e-2
     assert rel_l2(xg.grad, xd.grad) < tol, rel_l2(xg.grad, xd.grad)
     assert rel_l2(wg.grad, wd.grad) < 1e-5 and rel_l2(bg.grad, bd.grad) < 1e-5
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,dim,k", [(777, 192, 192), (300, 64, 128), (33, 512, 96)])
+def test_output_residual_wide_matches_torch(gpu, dt, rows, dim, k):
+    """OutputResidualWide (p3d_out_residual with an fp32 residual) against
+    x + (y Wo^T in dt) as torch computes it under autocast: the product
+    rounded to dt (the kernel's fp32 sum may round the other way, one unit
+    of dt at the product), added to the unrounded fp32 x; and its
+    gradients: dx = dout, dy and dWo against torch's in fp32."""
+    print(f"output residual wide {rows}x{dim} k{k} {dt}", flush=True)
+    gen = torch.Generator(device=gpu).manual_seed(rows + dim + k)
+    x = torch.randn(rows, dim, device=gpu, generator=gen) * 4
+    y = torch.randn(rows, k, device=gpu, generator=gen).to(dt)
+    w = torch.randn(dim, k, device=gpu, generator=gen) / math.sqrt(k)
+    xg, yg, wg = (t.clone().requires_grad_() for t in (x, y, w))
+    out = linear.OutputResidualWide.apply(xg, yg, wg, dt)
+    assert out.dtype == torch.float32
+    prod = torch.mm(y, w.to(dt).t())
+    step = {torch.bfloat16: 2 ** -8, torch.float16: 2 ** -11}[dt]
+    err = (out.detach() - (x + prod.float())).abs()
+    assert (err <= 2 * step * prod.float().abs() + 1e-6).all(), float(err.max())
+    dout = torch.randn(rows, dim, device=gpu, generator=gen)
+    out.backward(dout)
+    assert torch.equal(xg.grad, dout)
+    d16 = dout.to(dt)
+    assert rel_l2(yg.grad.float(), (d16.float() @ w.to(dt).float())) < 1e-2
+    assert rel_l2(wg.grad, d16.float().t() @ y.float()) < 1e-2
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -187,8 +220,21 @@ def test_layer_autocast_keeps_the_wide_residual(gpu, grad):
     lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
     x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1)) * 4
     xg = x.to(gpu).requires_grad_(grad)
-    with torch.set_grad_enabled(grad), torch.autocast("cuda", dtype=torch.bfloat16):
-        y = layer(xg, lay_h)
+    calls = []
+    real = _lib.call
+
+    def counting(name, *args):
+        calls.append(name)
+        return real(name, *args)
+
+    linear._lib.call = counting
+    try:
+        with torch.set_grad_enabled(grad), torch.autocast("cuda", dtype=torch.bfloat16):
+            y = layer(xg, lay_h)
+    finally:
+        linear._lib.call = real
+    if grad:  # the fp32 residual goes through the output product's own kernel
+        assert "p3d_out_residual" in calls, calls
     with torch.no_grad():
         exp = oracle(x, lay_r)
     assert y.dtype == torch.float32

@@ -93,109 +93,17 @@ __device__ __forceinline__ void load_q(const typename C::T_* row, bool valid, Ro
 }
 
 // ---------------------------------------------------------------- summaries
-// Summary stages of 64 keys, double-buffered in LDS through registers:
-// K rows (natural order, row stride KSTR) and V transposed (row stride VGS).
-// A stage is one contiguous block of sk ([64][D]) and one of svt
-// ([2][D][32]), so a thread's piece p sits at element offset p * EP in both;
-// the LDS offsets of its pieces are fixed and computed once.
-template <typename C, int WG>
-struct StageRegs {
-    typedef typename C::T_ T;
-    static constexpr int EP = Piece<T>::N;
-    static constexpr int VGS = 64 + EP;
-    static constexpr int KPIECES = 64 * (C::D / EP);
-    static constexpr int VPIECES = C::D * (64 / EP);
-    static constexpr int KI = (KPIECES + WG - 1) / (WG);
-    static constexpr int VI = (VPIECES + WG - 1) / (WG);
-    uint4 k[KI], v[VI];
-    int klds[KI], vlds[VI];
-
-    __device__ __forceinline__ StageRegs() {
-#pragma unroll
-        for (int i = 0; i < KI; ++i) {
-            const int p = threadIdx.x + i * WG;
-            const int r = p / (C::D / EP), c = (p - r * (C::D / EP)) * EP;
-            klds[i] = r * C::KSTR + c;
-        }
-#pragma unroll
-        for (int i = 0; i < VI; ++i) {
-            const int p = threadIdx.x + i * WG;
-            const int tt = p / (C::D * (32 / EP));
-            const int rem = p - tt * C::D * (32 / EP);
-            const int ch = rem / (32 / EP), kk = (rem - ch * (32 / EP)) * EP;
-            vlds[i] = 64 * C::KSTR + ch * VGS + 32 * tt + kk;
-        }
-    }
-
-    // Stage [base, base + 64) (32 or 64 valid rows; pad rows of sk / svt are zero).
-    __device__ __forceinline__ void load(const AttnDev& a, int64_t bg, int base) {
-        const int limit = min(64, a.Mp - base) * C::D;  // elements present in each block
-        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
-        const T* svt = tp<T>(a.svt) + ((int64_t)bg * a.Mp + base) * C::D;
-#pragma unroll
-        for (int i = 0; i < KI; ++i) {
-            const int off = (threadIdx.x + i * WG) * EP;
-            k[i] = off < limit ? *reinterpret_cast<const uint4*>(sk + off) : uint4{0, 0, 0, 0};
-        }
-#pragma unroll
-        for (int i = 0; i < VI; ++i) {
-            const int off = (threadIdx.x + i * WG) * EP;
-            v[i] = off < limit ? *reinterpret_cast<const uint4*>(svt + off) : uint4{0, 0, 0, 0};
-        }
-    }
-
-    // Branch-free forms for the pipelined sweep, whose stage loop must stay
-    // one basic block.  Every thread loads from a valid address: offsets are
-    // clamped into the stage's present rows, so a piece past them repeats
-    // one of this (b, g)'s summary rows (finite; its keys are masked or
-    // skipped by the sweep).  Pieces beyond the stage's count are stored into
-    // row padding that no fragment read touches (K columns [D, KSTR), V^T
-    // columns [64, VGS)).
-    __device__ __forceinline__ void load_clamped(const AttnDev& a, int64_t bg, int base) {
-        const int last = min(64, a.Mp - base) * C::D - EP;
-        const T* sk = tp<T>(a.sk) + ((int64_t)bg * a.Mp + base) * C::D;
-        const T* svt = tp<T>(a.svt) + ((int64_t)bg * a.Mp + base) * C::D;
-#pragma unroll
-        for (int i = 0; i < KI; ++i)
-            k[i] = *reinterpret_cast<const uint4*>(sk + min((int)(threadIdx.x + i * WG) * EP, last));
-#pragma unroll
-        for (int i = 0; i < VI; ++i)
-            v[i] = *reinterpret_cast<const uint4*>(svt + min((int)(threadIdx.x + i * WG) * EP, last));
-    }
-    __device__ __forceinline__ void store_all(T* stage) const {
-        static_assert(C::KSTR - C::D >= EP && VGS - 64 >= EP, "no row padding for the spare pieces");
-        const int spare_k = (threadIdx.x % 64) * C::KSTR + C::D;
-        const int spare_v = 64 * C::KSTR + (threadIdx.x % C::D) * VGS + 64;
-#pragma unroll
-        for (int i = 0; i < KI; ++i)
-            *reinterpret_cast<uint4*>(stage + (threadIdx.x + i * WG < KPIECES ? klds[i] : spare_k)) = k[i];
-#pragma unroll
-        for (int i = 0; i < VI; ++i)
-            *reinterpret_cast<uint4*>(stage + (threadIdx.x + i * WG < VPIECES ? vlds[i] : spare_v)) = v[i];
-    }
-
-    // Write the staged pieces into a stage buffer (K rows then V rows).
-    __device__ __forceinline__ void store(T* stage) const {
-#pragma unroll
-        for (int i = 0; i < KI; ++i)
-            if (threadIdx.x + i * WG < KPIECES) *reinterpret_cast<uint4*>(stage + klds[i]) = k[i];
-#pragma unroll
-        for (int i = 0; i < VI; ++i)
-            if (threadIdx.x + i * WG < VPIECES) *reinterpret_cast<uint4*>(stage + vlds[i]) = v[i];
-    }
-};
-
-// Summary stages of the pipelined sweep, copied by the LDS DMA
-// (global_load_lds_dwordx4): the pieces go from L2 straight into LDS, with no
-// registers to hold them and no LDS store instructions.  One copy writes 64
-// consecutive 16-byte pieces of LDS, lane i the piece at M0 + 16 i, from a
-// global address of the lane's choosing.  The stage keeps the layout of
-// StageRegs (K rows of KSTR, V^T rows of VGS): a copy spans whole padded
-// rows, its lanes on padding slots fetch a piece of the same row (finite,
-// never read), and the last copy of each region starts 64 pieces before the
-// region's end, so it rewrites its predecessor's tail with the same data
-// instead of running into the V^T padding rows (the ones row and zeros,
-// written once).  Copies are split evenly over the waves; a wave with fewer
+// Summary stages of 64 keys, copied by the LDS DMA (global_load_lds_dwordx4):
+// the pieces go from L2 straight into LDS, with no registers to hold them and
+// no LDS store instructions.  One copy writes 64 consecutive 16-byte pieces
+// of LDS, lane i the piece at M0 + 16 i, from a global address of the lane's
+// choosing.  A stage holds K rows (natural order, row stride KSTR) and V
+// transposed (rows of VGS): one contiguous block of sk ([64][D]) and one of
+// svt ([2][D][32]).  A copy spans whole padded rows, its lanes on padding
+// slots fetch a piece of the same row (finite, never read), and the last copy
+// of each region starts 64 pieces before the region's end, so it rewrites its
+// predecessor's tail with the same data instead of running into the V^T
+// padding rows (the ones row and zeros, written once).  Copies are split evenly over the waves; a wave with fewer
 // repeats the last copy, so every wave issues the same instructions.
 // Completion is tracked by the vector-memory counter (dma_wait).
 template <typename C, int WG>
@@ -304,17 +212,19 @@ __device__ __forceinline__ void global_sweep(const AttnDev& a, int64_t bg, typen
     constexpr int STAGE = 64 * C::KSTR + 32 * C::MB * VGS;
     init_v_padding<C>(lds + 64 * C::KSTR, VGS, 64);
     init_v_padding<C>(lds + STAGE + 64 * C::KSTR, VGS, 64);
-    StageRegs<C, WG> regs;
-    regs.load(a, bg, 0);
-    regs.store(lds);
+    const StageDma<C, WG> dma;
+    dma.copy(a, bg, 0, lds);
+    dma_wait();
     __syncthreads();
     int buf = 0;
     for (int base = 0; base < a.M; base += 64) {
         const int next = base + 64;
-        if (next < a.M) regs.load(a, bg, next);
+        // The other buffer held the previous stage, which every wave finished
+        // before the last barrier.
+        if (next < a.M) dma.copy(a, bg, next, lds + (buf ^ 1) * STAGE);
         T* cur = lds + buf * STAGE;
         global_stage<C, BOUND>(a, base, cur, cur + 64 * C::KSTR, VGS, qf, st, negm, lane);
-        if (next < a.M) regs.store(lds + (buf ^ 1) * STAGE);
+        dma_wait();
         __syncthreads();
         buf ^= 1;
     }

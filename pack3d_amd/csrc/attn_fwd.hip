@@ -683,7 +683,7 @@ __device__ __forceinline__ uint32_t stencil_mask(const AttnDev& a, int c, int g,
     return m;
 }
 
-// Local-pathway plane staging by the LDS DMA (bf16, head_dim <= 48).  Each
+// Local-pathway plane staging by the LDS DMA (16-bit types, head_dim <= 48).  Each
 // halo plane is copied into one of two plane buffers while the previous plane
 // is scored, so no wave waits on global memory between planes.  A buffer holds
 // K and V in the same key-major layout (key row stride KSTR: D / 8 data slots
@@ -694,7 +694,7 @@ __device__ __forceinline__ uint32_t stencil_mask(const AttnDev& a, int c, int g,
 // outside the grid take the row of the nearest grid key (finite, and masked
 // by the stencil).
 template <typename C>
-constexpr bool kPlaneDma = kPiped<C>;
+constexpr bool kPlaneDma = sizeof(typename C::T_) == 2 && C::D <= 48;
 
 template <typename C>
 struct PlaneDma {
@@ -810,7 +810,8 @@ constexpr bool kPark = kPlaneDma<C> || grid_main_bytes<C>() + grid_park_bytes<C>
 template <typename C>
 constexpr size_t grid_dma_bytes() {
     constexpr size_t ep = Piece<typename C::T_>::N;
-    constexpr size_t stages = 3 * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(typename C::T_);
+    constexpr size_t stages =
+        (kPiped<C> ? 3 : 2) * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(typename C::T_);
     constexpr size_t summary = grid_park_bytes<C>() + stages;
     return kRopeWindowBytes + (PlaneDma<C>::BYTES > summary ? PlaneDma<C>::BYTES : summary);
 }

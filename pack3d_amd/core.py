@@ -108,8 +108,11 @@ class ForwardPlan:
 
     Splitting construction from launch lets callers time or replay the
     pooling and attention kernels individually.  ``kl_rotated``: kl already
-    holds the rotated keys (``p3d_project_pool`` with rotate_kl), so neither
-    the grid kernel nor the indexed path rotates it again.
+    holds the rotated keys (``p3d_project_pool`` with rotate_kl).  Otherwise
+    kl is rotated once into a copy before the attention kernel (``klr``, which
+    the backward reuses): the brick kernel would rotate each halo key again
+    for every brick and query head that reads it, and the indexed kernel
+    gathers it per edge.
     """
 
     def __init__(self, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature,
@@ -166,6 +169,13 @@ class ForwardPlan:
         tag = brick_tag(geometry)
         self.grid = tag is not None
         self.pre = []  # (name, args) launched before the attention kernel
+        if not rope.identity and not kl_rotated:
+            klr = torch.empty(kl.shape, dtype=kl.dtype, device=dev)
+            self.pre.append(("p3d_rotate", (_lib.view(kl), _lib.view(klr), b, g, n, d, dt, rope.struct(), 0)))
+            kl = klr
+            self._keep.append(klr)
+            a.kl_rotated = 1
+        self.klr = kl  # the keys as the attention kernels read them (rotated unless rope is the identity)
         if self.grid:
             shape, radius, mapping = tag
             a.q, a.kl = _lib.view(q), _lib.view(kl)
@@ -176,15 +186,9 @@ class ForwardPlan:
             self._keep.append(mapping)
             self.attn_name = "p3d_attn_fwd_grid"
         else:
-            # Arbitrary graph: local K rotated once into a copy (it is
-            # gathered per edge); q rotates on load in both kernels.  The
+            # Arbitrary graph: q rotates on load in both kernels.  The
             # indexed local kernel writes sl * o_L into y, and the rows kernel
             # adds the summary branch in its epilogue.
-            if not rope.identity and not kl_rotated:
-                klr = torch.empty(kl.shape, dtype=kl.dtype, device=dev)
-                self.pre.append(("p3d_rotate", (_lib.view(kl), _lib.view(klr), b, g, n, d, dt, rope.struct(), 0)))
-                kl = klr
-                self._keep.append(klr)
             a.q, a.kl = _lib.view(q), _lib.view(kl)
             a.rope = rope.struct()
             a.o_local_in = None
@@ -221,8 +225,9 @@ class _Pack3DHip(torch.autograd.Function):
     """First-order autograd of the core (autograd.py:8-28 of amilworks/Pack3D).
 
     The forward saves the inputs, the summaries (sk, svt, norm slots), o_L,
-    o_G and the two log-sum-exps; nothing of size N x M.  The backward
-    refuses a geometry mutated since the forward.
+    o_G and the two log-sum-exps, and, unless the rotation is the identity,
+    kl as the plan rotated it (the backward's rotated keys); nothing of size
+    N x M.  The backward refuses a geometry mutated since the forward.
     """
 
     @staticmethod
@@ -232,7 +237,7 @@ class _Pack3DHip(torch.autograd.Function):
         y, saved = plan.run()
         ctx.save_for_backward(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, saved["sk"], saved["svt"],
                               plan.sk_norm_max, saved["o_local"], saved["o_global"], saved["lse_local"],
-                              saved["lse_global"])
+                              saved["lse_global"], plan.klr if plan.klr is not kl else None)
         ctx.geometry, ctx.temperature, ctx.rope, ctx.pool_rope = geometry, temperature, rope, pool_rope
         ctx.key_scale = plan.key_scale
         return y
@@ -241,9 +246,22 @@ class _Pack3DHip(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, dy):
         ctx.geometry.check_unmodified()
-        grads = backward(dy, *ctx.saved_tensors, ctx.geometry, ctx.temperature, ctx.rope, ctx.pool_rope,
-                         ctx.key_scale)
+        *state, klr = ctx.saved_tensors
+        grads = backward(dy, *state, ctx.geometry, ctx.temperature, ctx.rope, ctx.pool_rope, ctx.key_scale,
+                         klr=klr)
         return (*grads, None, None, None, None)
+
+
+def _rotated(x, rope: RopeSpec):
+    """x [B, heads, N, d] rotated by ``rope`` into a new contiguous tensor
+    (x itself for the identity rotation)."""
+    if rope.identity:
+        return x
+    b, heads, n, d = x.shape
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _lib.call("p3d_rotate", _lib.view(_kernel_view(x)), _lib.view(out), b, heads, n, d, _lib.DTYPES[x.dtype],
+              rope.struct(), 0, _lib.stream_of(x.device))
+    return out
 
 
 def _mix_parts(rows):
@@ -258,13 +276,15 @@ def _splits(n, m, bg):
 
 
 def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm_max, o_local, o_global,
-             lse_local, lse_global, geometry, temperature, rope, pool_rope, key_scale, out=None):
+             lse_local, lse_global, geometry, temperature, rope, pool_rope, key_scale, out=None, klr=None):
     """The ten gradients of the core (kernels.py:313-356 of amilworks/Pack3D):
     dq, dkl, dkg with respect to the unrotated inputs (the rotation's backward
     is fused), dvl, dvg, dweight, dbias, dgate, dsl, dsg.  `out` may give
     (dq, dkl, dvl, dkg, dvg) as [B, *, N, d] views (16-byte aligned rows)
     that the kernels write in place, such as column ranges of the
-    projections' gradients; they are returned in their place."""
+    projections' gradients; they are returned in their place.  `klr`: kl
+    already rotated by `rope` (as the forward used it), else it is rotated
+    here."""
     b, h, n, d = q.shape
     g = kl.shape[1]
     dev, dt = q.device, _lib.DTYPES[q.dtype]
@@ -275,13 +295,9 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     q, kl, vl, kg, vg = (_kernel_view(t) for t in (q, kl, vl, kg, vg))
     dy = _kernel_view(dy if dy.dtype == q.dtype else dy.to(q.dtype))
     keep = []
-    if rope.identity:
-        qr, klr = q, kl
-    else:
-        qr = torch.empty(q.shape, dtype=q.dtype, device=dev)
-        klr = torch.empty(kl.shape, dtype=kl.dtype, device=dev)
-        for src, dst, heads in ((q, qr, h), (kl, klr, g)):
-            _lib.call("p3d_rotate", _lib.view(src), _lib.view(dst), b, heads, n, d, dt, rope.struct(), 0, stream)
+    qr = _rotated(q, rope)
+    if klr is None:
+        klr = _rotated(kl, rope)
     gate_k = gate if gate.dtype in _lib.DTYPES else gate.float()
     sl32, sg32 = param_f32(sl), param_f32(sg)
     parts = _mix_parts(b * h * n)
@@ -372,8 +388,10 @@ class _Pack3DProjections(torch.autograd.Function):
         plan = ForwardPlan(q, kl, vl, kg, vg, weight, bias, gate, sl, sg, geometry, temperature, rope, rope,
                            save_state=True)
         y, saved = plan.run()
+        # plan.klr: kl rotated once by the plan, which the backward reuses
         ctx.save_for_backward(qp, kvp, weight, bias, gate, sl, sg, saved["sk"], saved["svt"], plan.sk_norm_max,
-                              saved["o_local"], saved["o_global"], saved["lse_local"], saved["lse_global"])
+                              saved["o_local"], saved["o_global"], saved["lse_local"], saved["lse_global"],
+                              plan.klr if plan.klr is not kl else None)
         ctx.geometry, ctx.temperature, ctx.rope, ctx.key_scale = geometry, temperature, rope, plan.key_scale
         ctx.heads, ctx.kv_heads = heads, kv_heads
         return y
@@ -382,11 +400,11 @@ class _Pack3DProjections(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, dy):
         ctx.geometry.check_unmodified()
-        qp, kvp, weight, bias, gate, sl, sg, *state = ctx.saved_tensors
+        qp, kvp, weight, bias, gate, sl, sg, *state, klr = ctx.saved_tensors
         views = _projection_views(qp, kvp, ctx.heads, ctx.kv_heads)
         dqp, dkvp = torch.empty_like(qp), torch.empty_like(kvp)
         grads = backward(dy, *views, weight, bias, gate, sl, sg, *state, ctx.geometry, ctx.temperature, ctx.rope,
-                         ctx.rope, ctx.key_scale, out=_projection_views(dqp, dkvp, ctx.heads, ctx.kv_heads))
+                         ctx.rope, ctx.key_scale, out=_projection_views(dqp, dkvp, ctx.heads, ctx.kv_heads), klr=klr)
         return (dqp, dkvp, *grads[5:], None, None, None, None, None)
 
 

@@ -150,6 +150,25 @@ __device__ __forceinline__ void settle(const X& x) {
     asm volatile("" ::"v"(x));
 }
 
+// settle() of every element of each argument (arrays, nested or not).
+template <typename X>
+__device__ __forceinline__ void settle_all(const X& x) {
+    settle(x);
+}
+__device__ __forceinline__ void settle_all(const float2& x) {
+    settle(x.x);
+    settle(x.y);
+}
+template <typename X, size_t N>
+__device__ __forceinline__ void settle_all(const X (&x)[N]) {
+#pragma unroll
+    for (size_t i = 0; i < N; ++i) settle_all(x[i]);
+}
+template <typename... A>
+__device__ __forceinline__ void settle_loads(const A&... a) {
+    (settle_all(a), ...);
+}
+
 // Raw buffer resource over [base, base + bytes) of global memory, for buffer
 // loads with a scalar base and 32-bit per-lane byte offsets (offsets past
 // `bytes` read zero).  base must be wave-uniform; it is moved to scalar
@@ -174,6 +193,18 @@ __device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
 
 __device__ __forceinline__ float buffer_load_f32(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, offset, 0, 0));
+}
+
+// 16-byte store at byte offset `offset` of the resource r over `bytes`
+// bytes (a multiple of 16), made by the lanes with ok set: the others aim
+// past the end, where the hardware's range check drops the store.  No
+// branch surrounds it, so every wave issues the same number of vector
+// memory operations on every path, and a later s_waitcnt vmcnt for a load
+// issued before it can count past it instead of waiting for its write
+// acknowledgement.
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t r, uint32_t bytes, uint32_t offset, bool ok,
+                                               u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, ok ? offset : bytes, 0, 0);
 }
 
 // --------------------------------------------------------------- wave

@@ -119,19 +119,23 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     }
     const int gbase = a.q_out + a.kv_out, nout = gbase + 2 * a.heads;
     const int nblocks = (nout + 31) / 32;
-    // Weight row o of the concatenation [Wq; Wkv; Wg] (rows past nout are zero).
+    // Weight row o of the concatenation [Wq; Wkv; Wg].
     auto wrow = [&](int o) __attribute__((always_inline)) -> const T* {
         return o < a.q_out ? reinterpret_cast<const T*>(a.wq) + (int64_t)o * DIM
                : o < gbase ? reinterpret_cast<const T*>(a.wkv) + (int64_t)(o - a.q_out) * DIM
                            : reinterpret_cast<const T*>(a.wg) + (int64_t)(o - gbase) * DIM;
     };
+    // Every lane loads every time, with no branch and no select on the value
+    // (either would make the wave wait for the load there): rows past nout
+    // repeat row nout - 1, whose outputs are never stored, and the pieces
+    // past PIECES are loaded and not staged.
     u32x4 wreg[PPT];
     auto fetch = [&](int ob) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (DIM / 8), c = (pc % (DIM / 8)) * 8;
-            const int o = 32 * ob + r;
-            wreg[i] = (pc < PIECES && o < nout) ? *reinterpret_cast<const u32x4*>(wrow(o) + c) : u32x4{0u, 0u, 0u, 0u};
+            const int pc = threadIdx.x + i * 64 * kProjWaves, pcc = min(pc, PIECES - 1);
+            const int r = pcc / (DIM / 8), c = (pcc % (DIM / 8)) * 8, o = 32 * ob + r;
+            wreg[i] = *reinterpret_cast<const u32x4*>(wrow(min(o, nout - 1)) + c);
         }
     };
     auto stage = [&](int buf) __attribute__((always_inline)) {
@@ -143,7 +147,7 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     };
     fetch(0);
     stage(0);
-    if (nblocks > 1) fetch(1);
+    fetch(min(1, nblocks - 1));
     __syncthreads();
 
     const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
@@ -157,6 +161,10 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
 
     // ---- D = W X^T, 32 outputs at a time
     T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
+    const uint32_t qbytes = 32u * a.q_out * sizeof(T), kvbytes = 32u * a.kv_out * sizeof(T);
+    const __amdgpu_buffer_rsrc_t qrsrc = buffer_rsrc(reinterpret_cast<T*>(a.q) + tok0 * a.q_out, qbytes);
+    const __amdgpu_buffer_rsrc_t kvrsrc = buffer_rsrc(reinterpret_cast<T*>(a.kv) + tok0 * a.kv_out, kvbytes);
+    settle_loads(wreg, xf);
     for (int ob = 0; ob < nblocks; ++ob) {
         const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
         f32x16 d;
@@ -164,10 +172,13 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
         for (int r = 0; r < 16; ++r) d[r] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) d = M::mfma(*reinterpret_cast<const Frag*>(wb + 16 * ks), xf[ks], d);
-        if (32 * ob < gbase) {
+        {
             // q / kv outputs of the block through the tile: row t, columns
             // acc_row(4 qd, g) .. +3, then 16-byte pieces (token tt, outputs
-            // 8 pp .. +7) with four consecutive lanes per token.
+            // 8 pp .. +7) with four consecutive lanes per token.  Every block
+            // runs this (the gate's block stores nothing here), and each piece
+            // is one masked store into q and one into kv (a block may straddle
+            // them), so that every block issues the same stores.
 #pragma unroll
             for (int qd = 0; qd < 4; ++qd) {
                 const float v[4] = {d[4 * qd], d[4 * qd + 1], d[4 * qd + 2], d[4 * qd + 3]};
@@ -177,13 +188,11 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int tt = 16 * i + (lane >> 2), pp = lane & 3, o0 = 32 * ob + 8 * pp;
-                const int64_t tk = tok0 + tt;
-                if (tk < a.rows && o0 < gbase) {
-                    const u32x4 piece = *reinterpret_cast<const u32x4*>(tile + tt * OS + 8 * pp);
-                    T* dst = o0 < a.q_out ? reinterpret_cast<T*>(a.q) + tk * a.q_out + o0
-                                          : reinterpret_cast<T*>(a.kv) + tk * a.kv_out + (o0 - a.q_out);
-                    *reinterpret_cast<u32x4*>(dst) = piece;
-                }
+                const bool ok = tok0 + tt < a.rows && o0 < gbase;
+                const u32x4 piece = *reinterpret_cast<const u32x4*>(tile + tt * OS + 8 * pp);
+                buffer_store16(qrsrc, qbytes, (uint32_t)(tt * a.q_out + o0) * sizeof(T), ok && o0 < a.q_out, piece);
+                buffer_store16(kvrsrc, kvbytes, (uint32_t)(tt * a.kv_out + o0 - a.q_out) * sizeof(T),
+                               ok && o0 >= a.q_out, piece);
             }
             wave_lds_sync();  // the next block's tile writes follow these reads
         }
@@ -209,10 +218,10 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
                 }
             }
         }
-        if (ob + 1 < nblocks) {
-            stage((ob + 1) & 1);
-            if (ob + 2 < nblocks) fetch(ob + 2);
-        }
+        // Unconditional (a stage after the last block fills a buffer no
+        // block reads), so that every block issues the same loads.
+        stage((ob + 1) & 1);
+        fetch(min(ob + 2, nblocks - 1));
         __syncthreads();
     }
 }
@@ -367,12 +376,16 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     };
     u32x4 wreg[PPT];
     auto fetch = [&](int ob) __attribute__((always_inline)) {
-        const int o0 = start_of(ob), oe = end_of(ob);
+        // A block's rows are consecutive rows of one weight matrix.  Loads as
+        // k_project's: rows past the block's end repeat its last row (their
+        // outputs are never stored or summed).
+        const int o0 = start_of(ob), n = end_of(ob) - o0;
+        const T* wbase = wrow(o0);
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (DIM / 8), c = (pc % (DIM / 8)) * 8;
-            const int o = o0 + r;
-            wreg[i] = (pc < PIECES && o < oe) ? *reinterpret_cast<const u32x4*>(wrow(o) + c) : u32x4{0u, 0u, 0u, 0u};
+            const int pc = threadIdx.x + i * 64 * kProjWaves, pcc = min(pc, PIECES - 1);
+            const int r = pcc / (DIM / 8), c = (pcc % (DIM / 8)) * 8;
+            wreg[i] = *reinterpret_cast<const u32x4*>(wbase + (int64_t)min(r, n - 1) * DIM + c);
         }
     };
     auto stage = [&](int buf) __attribute__((always_inline)) {
@@ -384,7 +397,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     };
     fetch(0);
     stage(0);
-    if (nblocks > 1) fetch(1);
+    fetch(min(1, nblocks - 1));
     __syncthreads();
 
     // Wave-uniform quantities in scalar registers: the batch and token of the
@@ -404,8 +417,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     float* xch = xch_all + wave * 16;
     const float* xch_pair = xch_all + (wave ^ 1) * 16;
 
-    Frag xf[KS];
-    layer_norm_frags<T, KS>(a, lw, lb, tok, live, g, xf);
+    Frag xf[KS];  // the LayerNorm'd row, filled after the first table loads are issued
     int pos[3];
     {
         // rope_position32 without its branch (a branch here doubled the
@@ -451,7 +463,7 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
         if constexpr (K == kKL) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) cs_kl[k] = csn[k];
-            if (((ob - c1) >> 1) + 1 < nk) load_cs(((ob - c1) >> 1) + 1);
+            load_cs(min(((ob - c1) >> 1) + 1, nk - 1));  // unconditional: the same loads in every block
         }
         f32x16 d;
 #pragma unroll
@@ -474,16 +486,20 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
                 store4<T>(tile + t * OS + acc_row(4 * qd, g), v);
             }
             wave_lds_sync();
+            // The block's outputs lie wholly in q or wholly in kv: one
+            // resource over the wave's 32 rows of that tensor.
+            const bool in_q = o_first < a.q_out;
+            const int ostride = in_q ? a.q_out : a.kv_out;
+            T* obase = in_q ? reinterpret_cast<T*>(a.q) + tok0 * a.q_out + o_first
+                            : reinterpret_cast<T*>(a.kv) + tok0 * a.kv_out + (o_first - a.q_out);
+            const uint32_t obytes = 32u * ostride * sizeof(T);
+            const __amdgpu_buffer_rsrc_t orsrc = buffer_rsrc(obase, obytes);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                const int tt = 16 * i + (lane >> 2), pp = lane & 3, o0 = o_first + 8 * pp;
-                const int64_t tk = tok0 + tt;
-                if (tk < a.rows && o0 < o_end) {
-                    const u32x4 piece = *reinterpret_cast<const u32x4*>(tile + tt * OS + 8 * pp);
-                    T* dst = o0 < a.q_out ? reinterpret_cast<T*>(a.q) + tk * a.q_out + o0
-                                          : reinterpret_cast<T*>(a.kv) + tk * a.kv_out + (o0 - a.q_out);
-                    *reinterpret_cast<u32x4*>(dst) = piece;
-                }
+                const int tt = 16 * i + (lane >> 2), pp = lane & 3;
+                const u32x4 piece = *reinterpret_cast<const u32x4*>(tile + tt * OS + 8 * pp);
+                buffer_store16(orsrc, obytes, (uint32_t)(tt * ostride + 8 * pp) * sizeof(T),
+                               live && o_first + 8 * pp < o_end, piece);
             }
             wave_lds_sync();  // the next block's tile writes follow these reads
         } else if constexpr (K == kKG) {
@@ -544,16 +560,16 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
                 }
             }
         }
-        if (ob + 1 < nblocks) {
-            stage((ob + 1) & 1);
-            if (ob + 2 < nblocks) fetch(ob + 2);
-        }
+        // Unconditional (a stage after the last block fills a buffer no
+        // block reads), so that every block issues the same loads.
+        stage((ob + 1) & 1);
+        fetch(min(ob + 2, nblocks - 1));
         __syncthreads();
     };
-    for (int ob = 0; ob < c1; ++ob) {
-        if (ob == c1 - 1) load_cs(0);
-        run_block(ob, std::integral_constant<int, kQV>{});
-    }
+    load_cs(0);
+    layer_norm_frags<T, KS>(a, lw, lb, tok, live, g, xf);
+    settle_loads(wreg, csn, xf);
+    for (int ob = 0; ob < c1; ++ob) run_block(ob, std::integral_constant<int, kQV>{});
     for (int ob = c1; ob < c2; ob += 2) {
         run_block(ob, std::integral_constant<int, kKG>{});
         run_block(ob + 1, std::integral_constant<int, kKL>{});
@@ -667,9 +683,9 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* 
     auto fetch = [&](int ob) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PPT; ++i) {
-            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (K / 8), c = (pc % (K / 8)) * 8;
-            wreg[i] = pc < PIECES ? *reinterpret_cast<const u32x4*>(wo + (int64_t)(32 * ob + r) * K + c)
-                                  : u32x4{0u, 0u, 0u, 0u};
+            const int pc = threadIdx.x + i * 64 * kProjWaves, pcc = min(pc, PIECES - 1);
+            const int r = pcc / (K / 8), c = (pcc % (K / 8)) * 8;
+            wreg[i] = *reinterpret_cast<const u32x4*>(wo + (int64_t)(32 * ob + r) * K + c);
         }
     };
     auto stage = [&](int buf) __attribute__((always_inline)) {
@@ -681,13 +697,15 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* 
     };
     fetch(0);
     stage(0);
-    if (nblocks > 1) fetch(1);
+    fetch(min(1, nblocks - 1));
     __syncthreads();
 
     const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
     const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + (threadIdx.x >> 6)) * 32, tok = tok0 + t;
     const bool live = tok < rows;
     float* tile = otile[threadIdx.x >> 6];
+    const uint32_t obytes = 32u * dim * sizeof(R);
+    const __amdgpu_buffer_rsrc_t orsrc = buffer_rsrc(out + tok0 * dim, obytes);
     const T* yr = y + (live ? tok : 0) * K + 8 * g;
     Frag yf[KS];
 #pragma unroll
@@ -703,25 +721,17 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* 
                 r[i][h] = *reinterpret_cast<const u32x4*>(x + tk * dim + 32 * ob + 8 * (lane & 3) + h * (8 / RP));
         }
     };
-    // 16-bit residuals are loaded a block ahead; fp32 ones, twice the
-    // registers, at the start of their own block (before its GEMM), which
-    // keeps the kernel within the 128 registers of 4 waves per SIMD.
-    constexpr bool AHEAD = RP == 1;
-    u32x4 resn[2][RP];
-    if constexpr (AHEAD) load_res(0, resn);
+    // Each block's residual pieces are loaded a block ahead, into the
+    // registers the block before has just consumed (a copy between two sets
+    // would wait for the loads in flight).  Per block the vector memory
+    // operations go: stores, next residual, next weights; each wait then
+    // falls on loads issued a block earlier.
+    u32x4 resv[2][RP];
+    load_res(0, resv);
+    settle_loads(wreg, yf, resv);
 
     for (int ob = 0; ob < nblocks; ++ob) {
         const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
-        u32x4 resv[2][RP];
-        if constexpr (AHEAD) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int h = 0; h < RP; ++h) resv[i][h] = resn[i][h];
-            if (ob + 1 < nblocks) load_res(ob + 1, resn);
-        } else {
-            load_res(ob, resv);
-        }
         f32x16 d;
 #pragma unroll
         for (int r = 0; r < 16; ++r) d[r] = 0.f;
@@ -735,32 +745,34 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* 
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int tt = 16 * i + (lane >> 2), pp = lane & 3, o0 = 32 * ob + 8 * pp;
-            const int64_t tk = tok0 + tt;
-            if (tk < rows) {
-                const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp);
-                const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp + 4);
-                const R* rv = reinterpret_cast<const R*>(&resv[i][0]);
-                u32x4 o[RP];
-                R* ov = reinterpret_cast<R*>(&o[0]);
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + tt * OS + 8 * pp + 4);
+            const R* rv = reinterpret_cast<const R*>(&resv[i][0]);
+            u32x4 o[RP];
+            R* ov = reinterpret_cast<R*>(&o[0]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if constexpr (std::is_same<R, float>::value) {
-                        ov[e] = to_f32(from_f32<T>(lo[e])) + rv[e];
-                        ov[4 + e] = to_f32(from_f32<T>(hi[e])) + rv[4 + e];
-                    } else {
-                        ov[e] = from_f32<T>(lo[e] + to_f32(rv[e]));
-                        ov[4 + e] = from_f32<T>(hi[e] + to_f32(rv[4 + e]));
-                    }
+            for (int e = 0; e < 4; ++e) {
+                if constexpr (std::is_same<R, float>::value) {
+                    ov[e] = to_f32(from_f32<T>(lo[e])) + rv[e];
+                    ov[4 + e] = to_f32(from_f32<T>(hi[e])) + rv[4 + e];
+                } else {
+                    ov[e] = from_f32<T>(lo[e] + to_f32(rv[e]));
+                    ov[4 + e] = from_f32<T>(hi[e] + to_f32(rv[4 + e]));
                 }
-#pragma unroll
-                for (int h = 0; h < RP; ++h) *reinterpret_cast<u32x4*>(out + tk * dim + o0 + h * (8 / RP)) = o[h];
             }
+            // Masked stores without a branch: the next block's wait for its
+            // weights then counts past them.
+#pragma unroll
+            for (int h = 0; h < RP; ++h)
+                buffer_store16(orsrc, obytes, (uint32_t)(tt * dim + o0 + h * (8 / RP)) * sizeof(R), tok0 + tt < rows,
+                               o[h]);
         }
+        load_res(min(ob + 1, nblocks - 1), resv);
         wave_lds_sync();
-        if (ob + 1 < nblocks) {
-            stage((ob + 1) & 1);
-            if (ob + 2 < nblocks) fetch(ob + 2);
-        }
+        // Unconditional (a stage after the last block fills a buffer no
+        // block reads), so that every block issues the same loads.
+        stage((ob + 1) & 1);
+        fetch(min(ob + 2, nblocks - 1));
         __syncthreads();
     }
 }

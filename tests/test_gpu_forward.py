@@ -271,11 +271,14 @@ def test_layer_norm_kernel_matches_torch(gpu, dtype, dim):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("dim,heads,kv_heads,d", [(192, 4, 4, 48), (64, 2, 1, 32), (128, 4, 2, 16), (256, 2, 2, 64)])
+@pytest.mark.parametrize("dim,heads,kv_heads,d", [(192, 4, 4, 48), (64, 2, 1, 32), (128, 4, 2, 16), (256, 2, 2, 64),
+                                                (96, 3, 1, 16)])
 def test_fused_projections_match_torch(gpu, dtype, dim, heads, kv_heads, d):
     """p3d_project against the separate torch ops it replaces (LayerNorm, the
     three linear maps, the gate softmax), with random LayerNorm affine and
-    gate bias; rows not a multiple of the 128-token tile."""
+    gate bias; rows not a multiple of the 128-token tile.  With 3 heads of 16
+    (q_out 48, kv_out 64) a 32-output block holds the end of q and the start
+    of kv, and another the end of kv and the gate logits."""
     from pack3d_amd.attention import fused_projections
     print(f"fused projections {dim} h{heads} g{kv_heads} d{d} {dtype}", flush=True)
     torch.manual_seed(dim + d)

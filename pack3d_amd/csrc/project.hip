@@ -52,20 +52,27 @@ __device__ __forceinline__ void store4(T* dst, const float (&v)[4]) {
     *reinterpret_cast<T4*>(dst) = o;
 }
 
-// LayerNorm of a wave's 32 tokens into the B fragments of the projection
-// GEMM: lane l holds token l % 32 and, for every 16-channel k-step ks,
-// channels 16 ks + 8 (l / 32) .. +8, normalised in fp32 (statistics shared
-// with lane l ^ 32, which holds the other half of the row) and rounded to
-// the storage type as torch's LayerNorm output is.  lw / lb: the affine
-// parameters in LDS as fp32.
+// The rows of a wave's 32 tokens for the LayerNorm below: lane l loads token
+// l % 32's channels 16 ks + 8 (l / 32) .. +8 for every 16-channel k-step ks
+// (row 0 in dead lanes).  Apart from the arithmetic, so that a kernel can
+// issue these loads first and let their latency pass under its set-up.
 template <typename T, int KS>
-__device__ __forceinline__ void layer_norm_frags(const ProjDev& a, const float* lw, const float* lb, int64_t tok,
-                                                 bool live, int g, typename Mma<T>::Frag (&xf)[KS]) {
+__device__ __forceinline__ void layer_norm_load(const ProjDev& a, int64_t tok, bool live, int g, u32x4 (&raw)[KS]) {
     constexpr int DIM = 16 * KS;
     const T* xr = reinterpret_cast<const T*>(a.x) + (live ? tok : 0) * DIM + 8 * g;
-    u32x4 raw[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(xr + 16 * ks);
+}
+
+// LayerNorm of the half rows `raw` (layer_norm_load) into the B fragments of
+// the projection GEMM: normalised in fp32 (statistics shared with lane l ^
+// 32, which holds the other half of the row) and rounded to the storage type
+// as torch's LayerNorm output is.  lw / lb: the affine parameters in LDS as
+// fp32.
+template <typename T, int KS>
+__device__ __forceinline__ void layer_norm_math(const ProjDev& a, const float* lw, const float* lb, int g,
+                                                const u32x4 (&raw)[KS], typename Mma<T>::Frag (&xf)[KS]) {
+    constexpr int DIM = 16 * KS;
     float sum = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -113,6 +120,14 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     constexpr int OS = 32 + 8;                      // output tile row stride (elements)
     __shared__ __align__(16) T wbuf[2][32 * WS];
     __shared__ __align__(16) T otile[kProjWaves][32 * OS];
+    const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
+    const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + (threadIdx.x >> 6)) * 32, tok = tok0 + t;
+    const bool live = tok < a.rows;
+    // The token rows first: their latency passes under the set-up below
+    // (rows past 256 channels would hold too many registers through it).
+    constexpr bool kEarlyRows = KS <= 16;
+    u32x4 xraw[KS];
+    if constexpr (kEarlyRows) layer_norm_load<T, KS>(a, tok, live, g, xraw);
     for (int c = threadIdx.x; c < DIM; c += blockDim.x) {
         lw[c] = load_any(a.ln_w, c, a.ln_dtype);
         lb[c] = load_any(a.ln_b, c, a.ln_dtype);
@@ -150,14 +165,12 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     fetch(min(1, nblocks - 1));
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
-    const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + (threadIdx.x >> 6)) * 32, tok = tok0 + t;
     T* tile = otile[threadIdx.x >> 6];
-    const bool live = tok < a.rows;
 
     // ---- LayerNorm of the lane's half row (channels 16 ks + 8 g + j)
     Frag xf[KS];
-    layer_norm_frags<T, KS>(a, lw, lb, tok, live, g, xf);
+    if constexpr (!kEarlyRows) layer_norm_load<T, KS>(a, tok, live, g, xraw);
+    layer_norm_math<T, KS>(a, lw, lb, g, xraw, xf);
 
     // ---- D = W X^T, 32 outputs at a time
     T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
@@ -341,6 +354,32 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     int4* meta = reinterpret_cast<int4*>(xch_all + kProjWaves * 16);
     float* lwp = reinterpret_cast<float*>(meta + GD / 2);
     float* lbias = lwp + D;
+    // Wave-uniform quantities in scalar registers: the batch and token of the
+    // wave's first row (rows < 2^31, and a wave's 32 rows never straddle a
+    // batch since tokens is a multiple of 64).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
+    const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + wave) * 32, tok = tok0 + t;
+    const int bw = (int)tok0 / p.tokens, n0 = (int)tok0 - bw * p.tokens;
+    // rows is a multiple of 64: a wave, and the pair that holds its fine block,
+    // is wholly live or not.
+    const bool live = tok0 < a.rows;
+    // The token rows and their rotary coordinates first: their latency passes
+    // under the set-up below.
+    u32x4 xraw[KS];
+    layer_norm_load<T, KS>(a, tok, live, g, xraw);
+    int pos[3];
+    {
+        // rope_position32 without its branch (a branch here doubled the
+        // kernel's registers): a packed rotation reads three words of the
+        // pair table, always valid, and discards them.
+        const int n = live ? n0 + t : 0;
+        const int* c = p.rope.packed ? p.rope.pairs : reinterpret_cast<const int*>(p.rope.coords) + 6 * n;
+        const int c0 = c[0], c1 = c[2], c2 = c[4];
+        pos[0] = p.rope.packed ? n : c0;
+        pos[1] = p.rope.packed ? 0 : c1;
+        pos[2] = p.rope.packed ? 0 : c2;
+    }
     for (int c = threadIdx.x; c < DIM; c += blockDim.x) {
         lw[c] = load_any(a.ln_w, c, a.ln_dtype);
         lb[c] = load_any(a.ln_b, c, a.ln_dtype);
@@ -400,36 +439,14 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
     fetch(min(1, nblocks - 1));
     __syncthreads();
 
-    // Wave-uniform quantities in scalar registers: the batch and token of the
-    // wave's first row (rows < 2^31, and a wave's 32 rows never straddle a
-    // batch since tokens is a multiple of 64).
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
-    const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + wave) * 32, tok = tok0 + t;
-    const int bw = (int)tok0 / p.tokens, n0 = (int)tok0 - bw * p.tokens;
     T* tile = otile[wave];
-    // rows is a multiple of 64: a wave, and the pair that holds its fine block,
-    // is wholly live or not.
-    const bool live = tok0 < a.rows;
     T* krows = rows_all + wave * 32 * KGS;
     float* sums = reinterpret_cast<float*>(krows);  // after the kg sums: kg sums, vg sums, key squares
     T* wts = wts_all + wave * G * 64;
     float* xch = xch_all + wave * 16;
     const float* xch_pair = xch_all + (wave ^ 1) * 16;
 
-    Frag xf[KS];  // the LayerNorm'd row, filled after the first table loads are issued
-    int pos[3];
-    {
-        // rope_position32 without its branch (a branch here doubled the
-        // kernel's registers): a packed rotation reads three words of the
-        // pair table, always valid, and discards them.
-        const int n = live ? n0 + t : 0;
-        const int* c = p.rope.packed ? p.rope.pairs : reinterpret_cast<const int*>(p.rope.coords) + 6 * n;
-        const int c0 = c[0], c1 = c[2], c2 = c[4];
-        pos[0] = p.rope.packed ? n : c0;
-        pos[1] = p.rope.packed ? 0 : c1;
-        pos[2] = p.rope.packed ? 0 : c2;
-    }
+    Frag xf[KS];  // the LayerNorm'd row, computed after the first table loads are issued
 
     T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
     // (cos, sin) of the lane's rotary pairs in kg (and kl) block k (channels
@@ -567,8 +584,8 @@ __attribute__((amdgpu_waves_per_eu(2))) void k_project_pool(ProjDev a, PoolFuseD
         __syncthreads();
     };
     load_cs(0);
-    layer_norm_frags<T, KS>(a, lw, lb, tok, live, g, xf);
-    settle_loads(wreg, csn, xf);
+    layer_norm_math<T, KS>(a, lw, lb, g, xraw, xf);
+    settle_loads(wreg, xf);  // the table loads stay in flight under the q / vl blocks
     for (int ob = 0; ob < c1; ++ob) run_block(ob, std::integral_constant<int, kQV>{});
     for (int ob = c1; ob < c2; ob += 2) {
         run_block(ob, std::integral_constant<int, kKG>{});
@@ -679,33 +696,14 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* 
     __shared__ __align__(16) T wbuf[2][32 * WS];
     __shared__ __align__(16) float otile[kProjWaves][32 * OS];
     const int nblocks = dim / 32;
-    u32x4 wreg[PPT];
-    auto fetch = [&](int ob) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int pc = threadIdx.x + i * 64 * kProjWaves, pcc = min(pc, PIECES - 1);
-            const int r = pcc / (K / 8), c = (pcc % (K / 8)) * 8;
-            wreg[i] = *reinterpret_cast<const u32x4*>(wo + (int64_t)(32 * ob + r) * K + c);
-        }
-    };
-    auto stage = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < PPT; ++i) {
-            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (K / 8), c = (pc % (K / 8)) * 8;
-            if (pc < PIECES) *reinterpret_cast<u32x4*>(&wbuf[buf][r * WS + c]) = wreg[i];
-        }
-    };
-    fetch(0);
-    stage(0);
-    fetch(min(1, nblocks - 1));
-    __syncthreads();
-
     const int lane = threadIdx.x & 63, g = lane >> 5, t = lane & 31;
     const int64_t tok0 = ((int64_t)blockIdx.x * kProjWaves + (threadIdx.x >> 6)) * 32, tok = tok0 + t;
     const bool live = tok < rows;
     float* tile = otile[threadIdx.x >> 6];
     const uint32_t obytes = 32u * dim * sizeof(R);
     const __amdgpu_buffer_rsrc_t orsrc = buffer_rsrc(out + tok0 * dim, obytes);
+    // The token rows and the first residual pieces first: their latency
+    // passes under the first weight block's fetch and staging.
     const T* yr = y + (live ? tok : 0) * K + 8 * g;
     Frag yf[KS];
 #pragma unroll
@@ -728,6 +726,26 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* 
     // falls on loads issued a block earlier.
     u32x4 resv[2][RP];
     load_res(0, resv);
+    u32x4 wreg[PPT];
+    auto fetch = [&](int ob) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * 64 * kProjWaves, pcc = min(pc, PIECES - 1);
+            const int r = pcc / (K / 8), c = (pcc % (K / 8)) * 8;
+            wreg[i] = *reinterpret_cast<const u32x4*>(wo + (int64_t)(32 * ob + r) * K + c);
+        }
+    };
+    auto stage = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PPT; ++i) {
+            const int pc = threadIdx.x + i * 64 * kProjWaves, r = pc / (K / 8), c = (pc % (K / 8)) * 8;
+            if (pc < PIECES) *reinterpret_cast<u32x4*>(&wbuf[buf][r * WS + c]) = wreg[i];
+        }
+    };
+    fetch(0);
+    stage(0);
+    fetch(min(1, nblocks - 1));
+    __syncthreads();
     settle_loads(wreg, yf, resv);
 
     for (int ob = 0; ob < nblocks; ++ob) {

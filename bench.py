@@ -9,7 +9,10 @@ Xavier-uniform to_q / to_kv / to_out from seed 0, pool_weight = slot_bias = 0
 
 A step is one layer forward (LayerNorm, projections, gate, fused core,
 to_out, residual) under torch.inference_mode with every input resident in
-HBM.  Prints one JSON line; see DESIGN.md for the fields.
+HBM.  The layer's output is checked against the oracle layer before the line
+is printed (a failed check raises).  The same line carries the c4 layer
+forward + backward with its summary-backward kernels, and the
+incremental peak of allocated bytes of both.  Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -177,42 +180,83 @@ def summary_pathway_ms(plan, steps, stream):
     return time_events(run, max(5, steps), stream)
 
 
-def cpu_baseline(shape, threads, repeats=3):
-    """The oracle (a restatement of the reference CPU path) on the whole c2 layer.
+def oracle_layer(layer):
+    """The oracle layer (a restatement of the reference CPU path) holding the
+    benchmark layer's weights, as rounded to its storage type, in fp32."""
+    from oracle import pack3d_oracle as ref
+
+    oracle = ref.PACK3DAttention(DIM, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
+                                 block_volume=math.prod(BLOCK))
+    oracle.load_state_dict({k: v.detach().float().cpu() for k, v in layer.state_dict().items()})
+    return oracle
+
+
+def cpu_baseline(layer, x, shape, threads, repeats=3):
+    """The oracle on the whole c2 layer, timed; returns (record, output).
 
     The oracle layer runs in fp32, as the reference computes its core for
-    bf16 inputs (reference.py:18), over every token and every query row (in
-    chunks of 512 query rows, which the reference's dense guards would
-    refuse at this size). The value is the median of ``repeats`` runs after a
-    warm-up on 256 rows. About 4 s per run on the GPU box's host.
+    bf16 inputs (reference.py:18), on the benchmark layer's weights and input
+    (bf16 values held in fp32), over every token and every query row (in
+    chunks of 512 query rows, which the reference's dense guards would refuse
+    at this size).  The value is the median of ``repeats`` runs after a
+    warm-up on 256 rows; the last run's output feeds the correctness gate.
+    About 4-6 s per run on the GPU box's host.
     """
     from oracle import pack3d_oracle as ref
 
     torch.set_num_threads(threads)
     n = math.prod(shape)
-    torch.manual_seed(0)
-    layer = ref.PACK3DAttention(DIM, heads=HEADS, kv_heads=KV_HEADS, head_dim=HEAD_DIM,
-                                block_volume=math.prod(BLOCK))
-    for lin in (layer.to_q, layer.to_kv, layer.to_out):
-        torch.nn.init.xavier_uniform_(lin.weight)
-    with torch.no_grad():
-        layer.pool_weight.zero_()
-        layer.slot_bias.zero_()
+    oracle = oracle_layer(layer)
     layout = ref.build_layout(shape, BLOCK, radius=RADIUS, pool_size=1, layout="raster_block")
-    x = torch.randn(1, n, DIM, generator=torch.Generator().manual_seed(1))
+    xf = x.detach().float().cpu()
     times = []
     with torch.inference_mode():
-        layer(x, layout, rows=torch.arange(256), chunk=256)  # warm-up
+        oracle(xf, layout, rows=torch.arange(256), chunk=256)  # warm-up
         for _ in range(repeats):
             t0 = time.perf_counter()
-            layer(x, layout, chunk=512)
+            out = oracle(xf, layout, chunk=512)
             times.append(time.perf_counter() - t0)
     med = sorted(times)[len(times) // 2]
-    return {"value": round(1000.0 * med, 1), "unit": "ms/layer", "cores": threads, "kind": "port",
-            "host_cpus": os.cpu_count(),
-            "sample": (f"the whole c2 layer forward (all {n} tokens and query rows) through the oracle in fp32 "
-                       f"on {threads} threads (the one-GPU box's CPU share; the host reports {os.cpu_count()} "
-                       f"CPUs); median of {repeats} runs ({', '.join(f'{t:.2f}' for t in times)} s)")}
+    record = {"value": round(1000.0 * med, 1), "unit": "ms/layer", "cores": threads, "kind": "port",
+              "host_cpus": os.cpu_count(),
+              "sample": (f"the whole c2 layer forward (all {n} tokens and query rows) through the oracle in fp32 "
+                         f"on {threads} threads (the one-GPU box's CPU share; the host reports {os.cpu_count()} "
+                         f"CPUs); median of {repeats} runs ({', '.join(f'{t:.2f}' for t in times)} s)")}
+    return record, out
+
+
+def correctness_gate(layer, x, got, shape, expected=None, sample_rows=8192):
+    """The benchmark layer's own output against the oracle layer: the bar of
+    the north star (max abs <= 2e-2 in bf16 on unit-scale activations) beyond
+    the output's own rounding to bf16 (half an ulp, 2^-8 |y|), on every row
+    when ``expected`` (the oracle's whole-layer output) is given, else on
+    ``sample_rows`` evenly spaced rows.  Raises when the bar is missed, so a
+    broken kernel never reports a time (benchmarks/attention.py:99-114 of
+    amilworks/Pack3D gates its timing the same way)."""
+    from oracle import pack3d_oracle as ref
+
+    n = math.prod(shape)
+    xf = x.detach().float().cpu()
+    if expected is None:
+        rows = torch.arange(0, n, max(1, n // sample_rows))
+        oracle = oracle_layer(layer)
+        layout = ref.build_layout(shape, BLOCK, radius=RADIUS, pool_size=1, layout="raster_block")
+        with torch.inference_mode():
+            expected = oracle(xf, layout, rows=rows, chunk=512)
+        got, xf = got[:, rows.to(got.device)], xf[:, rows]
+    else:
+        rows = None
+    got, exp = got.float().cpu(), expected.float()
+    diff = (got - exp).abs()
+    beyond = float((diff - 2 ** -8 * exp.abs()).max())
+    # The attention's share of y (y minus the residual x) as a relative L2.
+    rel = float(((got - xf) - (exp - xf)).norm() / (exp - xf).norm())
+    gate = {"rows": n if rows is None else int(rows.numel()), "max_abs": round(float(diff.max()), 6),
+            "max_abs_beyond_output_rounding": round(beyond, 6), "bar": 2e-2,
+            "rel_l2_attention_part": float(f"{rel:.4g}")}
+    if not (beyond <= 2e-2 and rel < 3.5e-2):
+        raise RuntimeError(f"correctness gate failed: {gate}")
+    return gate
 
 
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "traffic_c2.md")
@@ -281,10 +325,14 @@ def traffic_probe():
 C4_SHAPE = (32, 128, 64)
 
 
-def bench_c4(steps, warmup):
+def bench_c4(steps, warmup, kernels=False):
     """c4: layer forward + backward on 32 x 128 x 64
     (262,144 tokens), batch 1, raster, bf16 autocast, upstream gradient N(0, 1).
-    A step is one forward and one backward to every parameter and the input."""
+    A step is one forward and one backward to every parameter and the input.
+    Also the incremental peak of allocated bytes over a step (as
+    benchmarks/attention.py:133-143 of amilworks/Pack3D measures it) and,
+    with ``kernels``, the mean durations of the summary dQ and dK/dV passes
+    inside the steps (HIP events on the launch stream)."""
     import pack3d_amd as p3d
 
     dev = torch.device("cuda:0")
@@ -316,14 +364,58 @@ def bench_c4(steps, warmup):
         step()
     torch.cuda.synchronize()
     ms = 1000.0 * (time.perf_counter() - t0) / steps
-    return {"metric": "ms per PACK3D layer fwd+bwd @c4 (32x128x64, 262,144 tokens) bf16 autocast",
-            "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup,
-            "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-            "dtype": "bf16", "data": "synthetic",
-            "config": {"workload": "c4: PACK3D layer forward + backward, 32x128x64 volume, batch 1, raster, "
-                                   "bf16 autocast", "dim": DIM, "heads": HEADS, "kv_heads": KV_HEADS,
-                       "head_dim": HEAD_DIM, "radius": RADIUS, "block": list(BLOCK), "pool_size": 1,
-                       "tokens_per_s": round(n / (ms * 1e-3)), "parallelism": "single GPU"}}
+    layer.zero_grad(set_to_none=True)
+    x.grad = None
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    out = {"metric": "ms per PACK3D layer fwd+bwd @c4 (32x128x64, 262,144 tokens) bf16 autocast",
+           "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup,
+           "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+           "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": "c4: PACK3D layer forward + backward, 32x128x64 volume, batch 1, raster, "
+                                  "bf16 autocast", "dim": DIM, "heads": HEADS, "kv_heads": KV_HEADS,
+                      "head_dim": HEAD_DIM, "radius": RADIUS, "block": list(BLOCK), "pool_size": 1,
+                      "tokens_per_s": round(n / (ms * 1e-3)), "parallelism": "single GPU",
+                      "incremental_peak_allocated_bytes": int(peak)}}
+    if kernels:
+        from pack3d_amd import _lib
+
+        stream = torch.cuda.current_stream(dev)
+        marks = {}
+
+        def mark(name):
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(stream)
+            marks.setdefault(name, []).append(ev)
+
+        real = _lib.lib
+        timed = _TimedLib(real(), ("p3d_global_bwd_dq", "p3d_global_bwd_dkv"), mark)
+        _lib.lib = lambda: timed
+        try:
+            for _ in range(steps):
+                step()
+        finally:
+            _lib.lib = real
+        torch.cuda.synchronize()
+        times = {name: sum(ev[i].elapsed_time(ev[i + 1]) for i in range(0, len(ev), 2)) / (len(ev) // 2)
+                 for name, ev in marks.items()}
+        m = layout.geometry.num_summaries
+        base_flops = HEADS * n * m * HEAD_DIM
+        for key, name, kernel, mult in (
+                ("roofline_global_dq", "p3d_global_bwd_dq",
+                 "k_global_dq (summary dQ: scores, dP and dQ = dS sk; with the 1.6 MB summary transpose)", 6),
+                ("roofline_global_dkv", "p3d_global_bwd_dkv",
+                 "k_global_dkv (summary dK/dV: scores, dP, dK = dS^T q, dV = P^T dO)", 8)):
+            flops = mult * base_flops
+            tf = flops / (times[name] * 1e-3) / 1e12
+            out[key] = {"kernel": kernel, "bound": "mfma", "ms": round(times[name], 4), "achieved": round(tf, 2),
+                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                        "algorithmic_flops": flops}
+    return out
 
 
 def probe_rates():
@@ -374,7 +466,10 @@ def main():
     # covers it, so the timed steps measure the steady state.
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=50)
-    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-cpu-baseline", action="store_true",
+                   help="skip the CPU timing; the correctness gate then checks a sample of rows")
+    p.add_argument("--c4-steps", type=int, default=10, help="timed c4 forward + backward steps")
+    p.add_argument("--c4-warmup", type=int, default=10)
     p.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     p.add_argument("--traffic-probe", action="store_true",
                    help="only run the launch sequence that the HBM traffic counters are collected over")
@@ -438,6 +533,18 @@ def main():
         ms_core = time_events(plan.run, max(5, a.steps), stream)
         ms_summary = summary_pathway_ms(plan, a.steps, stream)
 
+        # Incremental peak of allocated bytes over one layer step (as
+        # benchmarks/attention.py:133-143 of amilworks/Pack3D measures it),
+        # and the layer's output for the correctness gate.
+        del q, kl, vl, kg, vg, gate, rope, plan
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated(dev)
+        torch.cuda.reset_peak_memory_stats(dev)
+        y = layer(x, layout)
+        torch.cuda.synchronize()
+        peak_c2 = torch.cuda.max_memory_allocated(dev) - base
+    c4 = bench_c4(a.c4_steps, a.c4_warmup, kernels=True)
+
     m = layout.geometry.num_summaries
     edges = valid_edges(SHAPE, RADIUS)
     flops_summary = 4 * HEADS * n * m * HEAD_DIM
@@ -452,7 +559,12 @@ def main():
     proj_pool_bytes = (n * DIM + n * HEADS * HEAD_DIM + 2 * n * KV_HEADS * HEAD_DIM + n * HEADS
                        + 2 * KV_HEADS * m * HEAD_DIM) * 2
     proj_pool_gbs = proj_pool_bytes / (ms_proj_pool * 1e-3) / 1e9
-    cpu = None if a.no_cpu_baseline else cpu_baseline(SHAPE, a.cpu_threads)
+    if a.no_cpu_baseline:
+        cpu = None
+        gate = correctness_gate(layer, x, y, SHAPE)
+    else:
+        cpu, expected = cpu_baseline(layer, x, SHAPE, a.cpu_threads)
+        gate = correctness_gate(layer, x, y, SHAPE, expected)
     traffic = load_traffic()
     out = {
         "metric": METRIC, "value": round(ms_layer, 4), "unit": "ms", "n_gpus": 1, "steps": a.steps,
@@ -466,7 +578,9 @@ def main():
                    "ms_attn_kernel": round(ms_attn, 4), "ms_summary_pathway": round(ms_summary, 4),
                    "ms_layer_unfused": round(ms_layer_unfused, 4),
                    "ms_pool_kernel_unfused_layer": round(ms_pool, 4),
+                   "incremental_peak_allocated_bytes": int(peak_c2),
                    "parallelism": "single GPU"},
+        "correctness_gate": gate,
         "roofline": {"kernel": "k_attn_grid (fused local+global forward)", "bound": "mfma",
                      "achieved": round(attn_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get("attn_bytes_per_launch"),
@@ -490,6 +604,11 @@ def main():
                                   "frac": round(proj_pool_gbs / PEAK_HBM_GBS, 4),
                                   "traffic": traffic.get("project_pool_bytes_per_launch"),
                                   "algorithmic_bytes": proj_pool_bytes},
+        "c4_fwd_bwd": {"workload": c4["config"]["workload"], "ms": c4["value"], "steps": c4["steps"],
+                       "warmup": c4["warmup"], "tokens_per_s": c4["config"]["tokens_per_s"],
+                       "incremental_peak_allocated_bytes": c4["config"]["incremental_peak_allocated_bytes"]},
+        "roofline_global_dq": c4["roofline_global_dq"],
+        "roofline_global_dkv": c4["roofline_global_dkv"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

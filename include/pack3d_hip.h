@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 14
+#define P3D_ABI_VERSION 15
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -408,6 +408,15 @@ int p3d_local_bwd_grid(const p3d_bwd_args* args, const int32_t grid[3], const in
 /* Summary pathway backward (kernels.py:184-237): dq_global and the split
  * partials dsk_part / dsv_part (sv_rows and skt are filled first). */
 int p3d_global_bwd(const p3d_bwd_args* args, void* stream);
+
+/* The two halves of p3d_global_bwd, for callers that time or order them
+ * separately: _dq fills sv_rows and skt and computes dq_global
+ * (kernels.py:179-207, the _global_dq pass); _dkv computes the split
+ * partials dsk_part / dsv_part (kernels.py:209-240, the _global_dkv pass)
+ * and reads the skt / sv_rows that _dq wrote, so it runs after it on the
+ * same stream. */
+int p3d_global_bwd_dq(const p3d_bwd_args* args, void* stream);
+int p3d_global_bwd_dkv(const p3d_bwd_args* args, void* stream);
 
 /* dq = R^T round(round(dq_local) + round(dq_global)) and dkl = R^T round(dk_local)
  * (kernels.py:202-206 rounding; R^T the inverse rotation of rope), written

@@ -25,7 +25,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 14  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 15  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -112,6 +112,8 @@ SIGNATURES = {
     "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),
     "p3d_local_bwd_grid": ([ctypes.POINTER(BwdArgs), _P, _P, _P, _P], c_int32),
     "p3d_global_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
+    "p3d_global_bwd_dq": ([ctypes.POINTER(BwdArgs), _P], c_int32),
+    "p3d_global_bwd_dkv": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_finish_bwd": ([ctypes.POINTER(BwdArgs), ctypes.POINTER(Rope), View, View, _P], c_int32),
     "p3d_pool_bwd": ([ctypes.POINTER(PoolArgs), _P, _P, c_int32, View, View, _P, _P, _P], c_int32),
 }

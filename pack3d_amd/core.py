@@ -343,7 +343,8 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
     else:
         nb, rev = geometry.neighbors, geometry.reverse_neighbors
         _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)
-    _lib.call("p3d_global_bwd", a, stream)
+    _lib.call("p3d_global_bwd_dq", a, stream)
+    _lib.call("p3d_global_bwd_dkv", a, stream)
     _lib.call("p3d_finish_bwd", a, rope.struct(), _lib.view(dq), _lib.view(dkl), stream)
 
     w32 = param_f32(weight)

@@ -768,14 +768,21 @@ extern "C" int p3d_mix_bwd(const p3d_bwd_args* args, void* stream) {
 }
 
 
-extern "C" int p3d_global_bwd(const p3d_bwd_args* args, void* stream) {
+namespace {
+int global_bwd_args(const p3d_bwd_args* args, BwdDev& d) {
     P3D_REQUIRE(args, "null args");
-    BwdDev d;
     if (int rc = fill_bwd(*args, d)) return rc;
     P3D_REQUIRE(args->splits >= 1, "splits must be positive");
     P3D_REQUIRE(args->sk && args->svt && args->sv_rows && args->skt && args->dog && args->lse_global &&
                     args->delta_global && args->dq_global && args->dsk_part && args->dsv_part,
                 "null pointer argument");
+    return P3D_OK;
+}
+}  // namespace
+
+extern "C" int p3d_global_bwd_dq(const p3d_bwd_args* args, void* stream) {
+    BwdDev d;
+    if (int rc = global_bwd_args(args, d)) return rc;
     hipStream_t s = as_stream(stream);
     const int64_t te = (int64_t)d.B * d.G * d.Mp * args->head_dim;
     switch (args->dtype) {
@@ -784,8 +791,19 @@ extern "C" int p3d_global_bwd(const p3d_bwd_args* args, void* stream) {
         default: k_summary_transpose<__bf16><<<(unsigned)cdiv(te, 256), 256, 0, s>>>(d, args->head_dim); break;
     }
     P3D_BWD_DISPATCH(launch_dq, args->head_dim, d, args->dtype, s);
-    P3D_BWD_DISPATCH(launch_dkv, args->head_dim, d, args->dtype, s);
-    return check_launch("p3d_global_bwd");
+    return check_launch("p3d_global_bwd_dq");
+}
+
+extern "C" int p3d_global_bwd_dkv(const p3d_bwd_args* args, void* stream) {
+    BwdDev d;
+    if (int rc = global_bwd_args(args, d)) return rc;
+    P3D_BWD_DISPATCH(launch_dkv, args->head_dim, d, args->dtype, as_stream(stream));
+    return check_launch("p3d_global_bwd_dkv");
+}
+
+extern "C" int p3d_global_bwd(const p3d_bwd_args* args, void* stream) {
+    if (int rc = p3d_global_bwd_dq(args, stream)) return rc;
+    return p3d_global_bwd_dkv(args, stream);
 }
 
 template <typename T, int D>

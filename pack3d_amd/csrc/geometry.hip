@@ -288,7 +288,9 @@ __global__ void k_check_layout(LayoutDims d, const int64_t* order, const int64_t
 
 // ------------------------------------------------------ stencil match
 // raster index -> packed row from a layout's order (order[i] = raster index of
-// row i); entries outside [0, n) are counted in flags[0].
+// row i; map starts at -1); entries outside [0, n) and raster indices that
+// appear twice (order is then no permutation, and some raster index is left
+// without a row) are counted in flags[0].
 __global__ void k_scatter_order(const int64_t* order, int64_t n, int32_t* map, int32_t* flags) {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -297,7 +299,7 @@ __global__ void k_scatter_order(const int64_t* order, int64_t n, int32_t* map, i
         atomicAdd(&flags[0], 1);
         return;
     }
-    map[t] = (int32_t)i;
+    if (atomicExch(&map[t], (int32_t)i) != -1) atomicAdd(&flags[0], 1);
 }
 
 // Counts in flags[1] the entries of nb [N, W] that differ from the complete

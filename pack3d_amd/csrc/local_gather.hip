@@ -162,8 +162,11 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_gather_fwd(GDev a) {
             for (int e = 0; e < C::EP; ++e) q[i * C::EP + e] = elem<T>(raw, e);
             rope_apply(a.rope, pos, c0, q + i * C::EP, C::EP);
         }
+        // The rotated q is rounded to the storage type, as rope.py:48 returns
+        // it and as the backward (which recomputes P from the saved log-sum-exp
+        // on the rounded copy) sees it.
 #pragma unroll
-        for (int c = 0; c < C::CH; ++c) q[c] *= a.scale_log2;
+        for (int c = 0; c < C::CH; ++c) q[c] = to_f32(from_f32<T>(q[c])) * a.scale_log2;
     }
     const T* K = reinterpret_cast<const T*>(a.kl) + sl.b * a.ksb + sl.kvh * a.ksh;
     const T* V = reinterpret_cast<const T*>(a.vl) + sl.b * a.vsb + sl.kvh * a.vsh;

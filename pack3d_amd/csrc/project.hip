@@ -945,6 +945,9 @@ extern "C" int p3d_project_pool(const p3d_project_args* args, const p3d_pool_arg
         return fail(P3D_EUNSUPPORTED,
                     "pooled projections need head_dim 16/32/48/64, kv_heads * head_dim <= 192, 64-slot fine "
                     "blocks of pool_size 1 over tokens a multiple of 64, and dim 64/96/128/192/256 within the LDS");
+    // k_project_pool indexes tokens, batches and summaries in 32 bits.
+    if (args->rows >= ((int64_t)1 << 31))
+        return fail(P3D_EUNSUPPORTED, "pooled projections take fewer than 2^31 rows");
     PoolFuseDev p;
     p.G = q.kv_heads;
     p.D = q.head_dim;

@@ -59,3 +59,36 @@ def rel_l2(a, b):
 
 def max_abs(a, b):
     return float((a.detach().double().cpu() - b.detach().double().cpu()).abs().max())
+
+
+def oracle_layer_grads(oracle, x, layout, dy, chunk=2048):
+    """The oracle layer's output and gradients (input and every parameter,
+    by name) for the upstream gradient ``dy``, in fp32, without an autograd
+    graph over more than one chunk of query rows of the core, so that it runs
+    at 262,144 tokens: the projections (LayerNorm, to_q, to_kv, RoPE, gate)
+    and to_out are differentiated by autograd over the whole volume, the core
+    by ``pack3d_reference_grads`` (chunked).  The same values as autograd of
+    ``oracle(x, layout)`` up to summation order, which
+    tests/test_oracle_layer.py checks on a small volume."""
+    from oracle.pack3d_oracle import pack3d_reference, pack3d_reference_grads
+
+    work = torch.float64 if x.dtype == torch.float64 else torch.float32
+    x = x.detach().to(work).clone().requires_grad_()
+    b, n = x.shape[0], x.shape[1]
+    with torch.enable_grad():
+        q, kl, vl, kg, vg, gate = oracle.project(x, layout)
+        core_in = [t.detach() for t in (q, kl, vl, kg, vg)]
+        params = [oracle.pool_weight, oracle.slot_bias, gate.detach(), oracle.local_scale, oracle.global_scale]
+        params = [t.detach() for t in params]
+        core = pack3d_reference(*core_in, *params, layout.geometry, temperature=oracle.temperature, chunk=chunk)
+        core_leaf = core.detach().requires_grad_()
+        y = x + oracle.to_out(core_leaf.transpose(1, 2).reshape(b, n, -1))
+        y.backward(dy.to(work))
+        grads = pack3d_reference_grads(*core_in, *params, layout.geometry, core_leaf.grad,
+                                       temperature=oracle.temperature, chunk=chunk)
+        torch.autograd.backward([q, kl, vl, kg, vg, gate], [grads[0], grads[1], grads[2], grads[3], grads[4],
+                                                             grads[7]])
+    named = {name: p.grad for name, p in oracle.named_parameters()}
+    named["pool_weight"], named["slot_bias"] = grads[5], grads[6]
+    named["local_scale"], named["global_scale"] = grads[8], grads[9]
+    return y.detach(), x.grad, named

@@ -90,13 +90,30 @@ def reference_layout(oracle_layout, device=None):
     return layout if device is None else layout.to(device)
 
 
-class ReferenceLayerWithHip(OracleLayer):
-    """The reference layer's forward (attention.py:53-89) with the third,
-    explicit ``hip`` branch of INTEGRATION.md in place of its dispatch."""
+# attention.py:29 of the reference, and the whitelist INTEGRATION.md's patch
+# of that line gives the hip backend.
+REFERENCE_HEAD_DIMS = (16, 32, 64, 128)
+PATCHED_HEAD_DIMS = (16, 32, 48, 64, 128)
 
-    def __init__(self, *args, **kwargs):
-        super().__init__(*args, **kwargs)
-        self.backend = "hip"
+
+class ReferenceLayerWithHip(OracleLayer):
+    """The reference layer's constructor guards (attention.py:27-36, with
+    line 29 patched as INTEGRATION.md writes it unless ``patched`` is False)
+    and forward (attention.py:53-89) with the third, explicit ``hip`` branch
+    of INTEGRATION.md in place of its dispatch."""
+
+    def __init__(self, dim, *, heads=4, kv_heads=2, head_dim=32, block_volume=8, backend="hip",
+                 position_encoding="axial", temperature=1.0, patched=True):
+        if any(type(v) is not int or v <= 0 for v in (dim, heads, kv_heads, head_dim, block_volume)):
+            raise ValueError("dimensions must be positive integers")
+        widths = PATCHED_HEAD_DIMS if patched and backend == "hip" else REFERENCE_HEAD_DIMS
+        if heads % kv_heads or head_dim not in widths or block_volume > 64:
+            raise ValueError("unsupported grouped-head dimensions or block volume")
+        if backend not in (("reference", "triton", "hip") if patched else ("reference", "triton")):
+            raise ValueError("backend must be explicitly reference, triton or hip")
+        super().__init__(dim, heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_volume=block_volume,
+                         position_encoding=position_encoding, temperature=temperature)
+        self.backend = backend
 
     def forward(self, x, layout):
         layout.check_unmodified()

@@ -202,3 +202,64 @@ def test_every_gradient_grid_shapes(gpu, dtype, shape, block, radius, kind, head
     got = torch.autograd.grad(y, xs, up.to(gpu))
     exp = torch.autograd.grad(e, rs, up)
     _compare(got, exp, dtype, f"grid {shape}")
+
+
+def _c4_layer(shape, gpu, seed=0):
+    """The c4 benchmark layer (bench.py --c4): Xavier projections from
+    ``seed``, default pooling, gate and LayerNorm parameters; fp32 parameters
+    on the GPU under bf16 autocast, and the oracle layer on the same weights."""
+    torch.manual_seed(seed)
+    layer = p3d.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    for lin in (layer.to_q, layer.to_kv, layer.to_out):
+        torch.nn.init.xavier_uniform_(lin.weight)
+    oracle = ref.PACK3DAttention(192, heads=4, kv_heads=4, head_dim=48, block_volume=64)
+    oracle.load_state_dict(layer.state_dict())
+    return layer.to(gpu), oracle
+
+
+def _autocast_layer_vs_oracle(gpu, shape, what, chunk):
+    """The layer under bf16 autocast over an fp32 input, as the c4 step runs
+    it (LayerNormTrain, the fused projections, _Pack3DProjections with view
+    outputs, OutputResidualWide, the HIP weight gradients): output, dx and
+    every parameter gradient against the oracle layer's fp32 gradients, at
+    the reference's bf16 relative-L2 bar (tests/test_triton.py:83)."""
+    from tests._cases import oracle_layer_grads
+
+    n = math.prod(shape)
+    layer, oracle = _c4_layer(shape, gpu)
+    lay_h = p3d.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    lay_r = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    x = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(1))
+    dy = torch.randn(1, n, 192, generator=torch.Generator().manual_seed(2))
+    xh = x.to(gpu).requires_grad_()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = layer(xh, lay_h)
+    y.backward(dy.to(gpu))
+    torch.cuda.synchronize()
+    exp_y, exp_dx, exp_named = oracle_layer_grads(oracle, x, lay_r, dy, chunk=chunk)
+    got = {"y - x": (y.float().cpu() - x), "dx": xh.grad.cpu()}
+    exp = {"y - x": exp_y - x, "dx": exp_dx}
+    for name, p in layer.named_parameters():
+        got[name] = p.grad.cpu()
+        exp[name] = exp_named[name]
+    for name in got:
+        a, e = got[name], exp[name]
+        assert a is not None and torch.isfinite(a).all(), (what, name)
+        err = rel_l2(a.float(), e.float())
+        print(f"  {what} {name}: rel_l2={err:.3g}", flush=True)
+        assert err < TOL[torch.bfloat16], (what, name, err)
+
+
+def test_layer_autocast_gradients_match_oracle(gpu):
+    """The c4 path on a small anisotropic grid (8 x 16 x 16)."""
+    print("layer autocast backward 8x16x16", flush=True)
+    _autocast_layer_vs_oracle(gpu, (8, 16, 16), "autocast 8x16x16", chunk=512)
+
+
+def test_full_size_c4_layer_gradients(gpu):
+    """c4 at full size (32 x 128 x 64, 262,144 tokens): the layer's output,
+    dx and the gradients of LayerNorm, to_q, to_kv, the gate, the pooling,
+    the scales and to_out against the oracle, whose core is differentiated
+    chunk by chunk over query rows."""
+    print("full size c4 layer backward", flush=True)
+    _autocast_layer_vs_oracle(gpu, (32, 128, 64), "c4 layer", chunk=2048)

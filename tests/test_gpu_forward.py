@@ -397,3 +397,80 @@ def test_pool_32_over_64_slots(gpu, dtype):
     exp = torch.autograd.grad(e, rs, up)
     for a, b in zip(got, exp):
         assert rel_l2(a.float(), b.float()) < REL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_indexed_local_rotates_and_rounds_q_like_a_prerotated_copy(gpu, dtype):
+    """The indexed local kernel rotates q on load and rounds the result to the
+    storage type, as rope.py:48 returns it and as the backward (which
+    recomputes P on a rounded rotated copy against the saved log-sum-exp)
+    sees it: o_L, its log-sum-exp and y are bit-identical to a run on q
+    rotated beforehand by p3d_rotate with the identity rotation."""
+    from pack3d_amd.core import ForwardPlan, _rotated, brick_tag
+    from pack3d_amd.rope import identity_rope
+
+    print(f"indexed local rotate-on-load vs pre-rotated q {dtype}", flush=True)
+    shape = (8, 8, 16)
+    lay_o = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    hg = p3d.prepare_geometry(lay_o.geometry.neighbors.to(gpu), lay_o.geometry.blocks.to(gpu), 1)
+    assert brick_tag(hg) is None  # untagged: the indexed local kernel runs
+    n = math.prod(shape)
+    q, kl, vl, kg, vg, w, b, gate, sl, sg = (t.to(gpu) for t in
+                                             random_core_inputs(1, 4, 2, n, 48, 64, dtype, seed=77, scale=2.0))
+    coords = lay_o.coords.to(gpu)
+    rope = hip_axial(48, shape, coords)
+    with torch.no_grad():
+        y1, s1 = ForwardPlan(q, kl, vl, kg, vg, w, b, gate, sl, sg, hg, 1.0, rope, rope, save_state=True).run()
+        ident = identity_rope(48, gpu)
+        y2, s2 = ForwardPlan(_rotated(q, rope), _rotated(kl, rope), vl, kg, vg, w, b, gate, sl, sg, hg, 1.0,
+                             ident, rope, save_state=True).run()
+        torch.cuda.synchronize()
+    assert torch.equal(s1["o_local"], s2["o_local"])
+    assert torch.equal(s1["lse_local"], s2["lse_local"])
+    assert torch.equal(y1, y2)
+
+
+def test_full_size_c2_bench_layer_matches_oracle(gpu):
+    """The exact layer step bench.py times (c2: 64^3 bf16, batch 1, raster,
+    no grad; Xavier projections, mean pooling), asserted to take the fused
+    projection pooling (p3d_project_pool: kl stored rotated, kg / vg never
+    written), against the oracle layer on the same (rounded) weights and input
+    on every row: max-abs <= 2e-2 beyond the output's own rounding to bf16,
+    and the attention's share of y (y - x) within the reference's bf16
+    relative-L2 bar."""
+    import bench
+    from pack3d_amd import _lib
+    from pack3d_amd.attention import PACK3DAttention
+
+    print("full size c2 bench layer vs oracle", flush=True)
+    shape = bench.SHAPE
+    n = math.prod(shape)
+    layer = bench.build_layer(gpu, torch.bfloat16)
+    assert isinstance(layer, PACK3DAttention)
+    lay = p3d.build_layout(shape, bench.BLOCK, radius=bench.RADIUS, pool_size=1, layout="raster_block", device=gpu)
+    x = torch.randn(1, n, bench.DIM, generator=torch.Generator().manual_seed(1)).to(gpu, torch.bfloat16)
+    calls = []
+    real = _lib.lib
+    _lib.lib = lambda: bench._TimedLib(real(), ("p3d_project_pool", "p3d_attn_fwd_grid"), calls.append)
+    try:
+        with torch.inference_mode():
+            y = layer(x, lay)
+        torch.cuda.synchronize()
+    finally:
+        _lib.lib = real
+    assert "p3d_project_pool" in calls and "p3d_attn_fwd_grid" in calls, calls
+    oracle = bench.oracle_layer(layer)
+    lay_r = ref.build_layout(shape, bench.BLOCK, radius=bench.RADIUS, pool_size=1, layout="raster_block")
+    xf = x.float().cpu()
+    with torch.inference_mode():
+        exp = oracle(xf, lay_r, chunk=512)
+    got = y.float().cpu()
+    diff = (got - exp).abs()
+    beyond = float((diff - 2 ** -8 * exp.abs()).max())
+    rel = rel_l2(got - xf, exp - xf)
+    print(f"  max_abs={float(diff.max()):.3g} beyond rounding={beyond:.3g} rel_l2(y - x)={rel:.3g}", flush=True)
+    assert torch.isfinite(got).all()
+    assert beyond <= 2e-2
+    assert rel < REL[torch.bfloat16]
+    gate = bench.correctness_gate(layer, x, y, shape, exp)
+    assert gate["max_abs_beyond_output_rounding"] == round(beyond, 6)

@@ -112,21 +112,27 @@ def test_adopt_proves_repacked_layout_and_rejects_other_tables(gpu):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_integration_registration_block(gpu, dtype):
-    """The reference layer with the hip branch as INTEGRATION.md writes it, on a
-    reference-shaped radius-two layout, against the oracle layer: outputs and
-    every gradient."""
-    print(f"integration block {dtype}", flush=True)
+@pytest.mark.parametrize("dim,heads,kv_heads,d", [(96, 4, 2, 32), (192, 4, 4, 48)])
+def test_integration_registration_block(gpu, dtype, dim, heads, kv_heads, d):
+    """The reference layer with the hip branch as INTEGRATION.md writes it
+    (constructor guards included), on a reference-shaped radius-two layout,
+    against the oracle layer: outputs and every gradient.  At the BASELINE
+    widths (dim 192, 4 / 4 heads, head_dim 48) the unpatched line 29 of the
+    reference's constructor refuses the layer; the patched one builds it."""
+    print(f"integration block dim{dim} h{heads} g{kv_heads} d{d} {dtype}", flush=True)
+    if d == 48:
+        with pytest.raises(ValueError, match="unsupported grouped-head"):
+            ReferenceLayerWithHip(dim, heads=heads, kv_heads=kv_heads, head_dim=d, block_volume=64, patched=False)
     torch.manual_seed(0)
     shape = (8, 8, 16)
     lay_o = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="native_block_morton")
     lay = reference_layout(lay_o, gpu)
-    oracle = ref.PACK3DAttention(96, heads=4, kv_heads=2, head_dim=32, block_volume=64)
-    layer = ReferenceLayerWithHip(96, heads=4, kv_heads=2, head_dim=32, block_volume=64)
+    oracle = ref.PACK3DAttention(dim, heads=heads, kv_heads=kv_heads, head_dim=d, block_volume=64)
+    layer = ReferenceLayerWithHip(dim, heads=heads, kv_heads=kv_heads, head_dim=d, block_volume=64)
     layer.load_state_dict(oracle.state_dict())
     layer = layer.to(gpu)
-    x = torch.randn(1, math.prod(shape), 96, generator=torch.Generator().manual_seed(1))
-    dy = torch.randn(1, math.prod(shape), 96, generator=torch.Generator().manual_seed(2))
+    x = torch.randn(1, math.prod(shape), dim, generator=torch.Generator().manual_seed(1))
+    dy = torch.randn(1, math.prod(shape), dim, generator=torch.Generator().manual_seed(2))
     xg = x.to(gpu).requires_grad_()
     xo = x.clone().requires_grad_()
     if dtype == torch.float32:
@@ -148,3 +154,40 @@ def test_integration_registration_block(gpu, dtype):
         r = rel_l2(a.float(), b)
         print(f"  d{name}: rel_l2={r:.3g}", flush=True)
         assert r < (1e-4 if dtype == torch.float32 else 5e-2), name
+
+
+def test_stencil_match_counts_a_duplicated_order_entry(gpu):
+    """An order that repeats a raster index is no permutation: some raster
+    index is left without a row.  p3d_stencil_match counts it, so no tag is
+    recorded even for a neighbour table built to agree with the resulting map
+    (whichever of the two rows wins the scatter), and the brick kernels, which
+    use the map unchecked, never see it."""
+    import types
+
+    from pack3d_amd import _lib
+    from pack3d_amd.geometry import grid_tag
+
+    print("stencil match with a duplicated order entry", flush=True)
+    shape = (8, 8, 16)
+    n = math.prod(shape)
+    lay_o = ref.build_layout(shape, (4, 4, 4), radius=2, pool_size=1, layout="raster_block")
+    nb0 = lay_o.geometry.neighbors.long()  # raster order: packed index = raster index
+    order = torch.arange(n, dtype=torch.int64)
+    order[5] = 6  # rows 5 and 6 both claim raster index 6; raster index 5 has no row
+    for winner in (5, 6):
+        mapping = torch.arange(n, dtype=torch.int64)
+        mapping[5] = -1
+        mapping[6] = winner
+        nb = torch.where(nb0[order] >= 0, mapping[nb0[order].clamp_min(0)], -1).to(torch.int32)
+        nb_g, order_g = nb.to(gpu).contiguous(), order.to(gpu)
+        out = torch.empty(n, dtype=torch.int32, device=gpu)
+        flags = torch.empty(8, dtype=torch.int32, device=gpu)
+        _lib.call("p3d_stencil_match", _lib.i64x3(shape), _lib.i64x3((2, 2, 2)), order_g.data_ptr(),
+                  nb_g.data_ptr(), nb.shape[1], out.data_ptr(), flags.data_ptr(), _lib.stream_of(gpu))
+        torch.cuda.synchronize()
+        assert int(flags[0]) >= 1, (winner, flags.tolist())
+        geom = types.SimpleNamespace(neighbors=nb_g, blocks=lay_o.geometry.blocks.to(gpu), tensors=(nb_g,),
+                                     _radius_one_grid=None)
+        lay = types.SimpleNamespace(grid_shape=shape, order=order_g, geometry=geom)
+        p3d.adopt_layout(lay)
+        assert grid_tag(geom) is None

@@ -299,3 +299,30 @@ def test_planted_slip_fails_a_pin(slip):
         assert worst < 1e-12, errs
     else:
         assert worst > 1e-6, f"slip {slip} passes every pin: {errs}"
+
+
+def test_chunked_layer_gradients_equal_autograd():
+    """tests/_cases.oracle_layer_grads (projections by autograd, the core by
+    the chunked pack3d_reference_grads) gives the same input and parameter
+    gradients as autograd of the whole oracle layer, in fp64, with chunks
+    smaller than the volume and random pooling parameters."""
+    from tests._cases import oracle_layer_grads
+
+    torch.manual_seed(4)
+    layer = PACK3DAttention(32, heads=4, kv_heads=2, head_dim=16, block_volume=8).double()
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.add_(0.1 * torch.randn_like(p))
+    layout = build_layout((4, 4, 6), (2, 2, 2), radius=1, pool_size=2, layout="native_block_morton")
+    gen = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 96, 32, generator=gen, dtype=F64)
+    dy = torch.randn(2, 96, 32, generator=gen, dtype=F64)
+    y, dx, named = oracle_layer_grads(layer, x, layout, dy, chunk=40)
+    xr = x.clone().requires_grad_()
+    layer.zero_grad(set_to_none=True)
+    yr = layer(xr, layout)
+    yr.backward(dy)
+    torch.testing.assert_close(y, yr.detach(), atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(dx, xr.grad, atol=1e-11, rtol=1e-11)
+    for name, p in layer.named_parameters():
+        torch.testing.assert_close(named[name], p.grad, atol=1e-11, rtol=1e-11, msg=name)

@@ -322,6 +322,65 @@ def traffic_probe():
     print("traffic probe done", flush=True)
 
 
+def gather_probe():
+    """Launch sequence profiled for the indexed-gather and rotation kernels
+    (run under rocprofv3 --kernel-trace / --pmc).
+
+    A 1 GiB fill evicts the caches and an elementwise add over 256 MiB gives
+    the counter calibration, as in --traffic-probe; then, three times each,
+    the core forward + backward (pack3d_hip_rope, every input differentiated)
+    on geometries that carry no grid tag, so that the indexed kernels
+    k_local_gather_fwd / _dq / _dkv run (with k_rotate on kl), at:
+      * c2: the 64^3 bf16 core inputs of the benchmark layer on the radius-2
+        tables of build_layout passed through prepare_geometry (a reference-
+        shaped geometry that adopt_layout has not proven);
+      * the adapter's Allen-15 shape: 32 x 128 x 64 bf16, 8 query / 2 kv
+        heads, head_dim 64, radius 1, (1, 4, 4) blocks, pool 16, N(0, 0.5^2)
+        inputs.
+    """
+    import pack3d_amd as p3d
+    from pack3d_amd.rope import axial_rope
+
+    dev = torch.device("cuda:0")
+    n = math.prod(SHAPE)
+    layer = build_layer(dev, torch.bfloat16)
+    layout = p3d.build_layout(SHAPE, BLOCK, radius=RADIUS, pool_size=1, layout="raster_block", device=dev)
+    x = torch.randn(1, n, DIM, generator=torch.Generator().manual_seed(1)).to(dev, torch.bfloat16)
+    flush = torch.empty(256 * 1024 * 1024, dtype=torch.float32, device=dev)
+    src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    with torch.no_grad():
+        q, kl, vl, kg, vg, gate, rope = layer.core_inputs(x, layout)
+    c2 = dict(inputs=[t.contiguous() for t in (q, kl, vl, kg, vg)],
+              params=[layer.pool_weight.detach(), layer.slot_bias.detach(), gate.contiguous(),
+                      layer.local_scale.detach(), layer.global_scale.detach()],
+              geometry=p3d.prepare_geometry(layout.geometry.neighbors, layout.geometry.blocks, 1), rope=rope)
+    shape15 = (32, 128, 64)
+    n15 = math.prod(shape15)
+    lay15 = p3d.build_layout(shape15, (1, 4, 4), radius=1, pool_size=16, layout="raster_block", device=dev)
+    gen = torch.Generator().manual_seed(15)
+    inputs15 = [(torch.randn(1, h, n15, 64, generator=gen) * 0.5).to(dev, torch.bfloat16) for h in (8, 2, 2, 2, 2)]
+    params15 = [(torch.randn(64, generator=gen) * 0.2).to(dev), (torch.randn(16, generator=gen) * 0.2).to(dev),
+                torch.rand(1, 8, n15, generator=gen).to(dev, torch.bfloat16),
+                (1 + 0.1 * torch.randn(64, generator=gen)).to(dev), (0.25 + 0.1 * torch.randn(64, generator=gen)).to(dev)]
+    allen = dict(inputs=inputs15, params=params15,
+                 geometry=p3d.prepare_geometry(lay15.geometry.neighbors, lay15.geometry.blocks, 16),
+                 rope=axial_rope(64, shape15, lay15.coords))
+    for case in (c2, allen):
+        assert p3d.core.brick_tag(case["geometry"]) is None
+    for _ in range(3):
+        flush.fill_(0.0)
+        torch.add(src, 1.0, out=dst)
+        for case in (c2, allen):
+            flush.fill_(0.0)
+            xs = [t.detach().requires_grad_() for t in case["inputs"]]
+            y = p3d.pack3d_hip_rope(*xs, *case["params"], case["geometry"], case["rope"])
+            dy = torch.ones_like(y)
+            torch.autograd.grad(y, xs, dy)
+    torch.cuda.synchronize()
+    print("gather probe done", flush=True)
+
+
 C4_SHAPE = (32, 128, 64)
 
 
@@ -473,6 +532,8 @@ def main():
     p.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     p.add_argument("--traffic-probe", action="store_true",
                    help="only run the launch sequence that the HBM traffic counters are collected over")
+    p.add_argument("--gather-probe", action="store_true",
+                   help="only run the launch sequence the indexed-gather and rotation counters are collected over")
     p.add_argument("--c4", action="store_true",
                    help="time the c4 layer forward + backward instead (one JSON line of its own)")
     p.add_argument("--probe-rates", action="store_true",
@@ -486,6 +547,9 @@ def main():
         sys.exit(2)
     if a.traffic_probe:
         traffic_probe()
+        return
+    if a.gather_probe:
+        gather_probe()
         return
     if a.c4:
         print(json.dumps(bench_c4(a.steps, a.warmup)), flush=True)
@@ -504,6 +568,12 @@ def main():
     layout = p3d.build_layout(SHAPE, BLOCK, radius=RADIUS, pool_size=1, layout="raster_block", device=dev)
     x = torch.randn(1, n, DIM, generator=torch.Generator().manual_seed(1)).to(dev, dtype)
     stream = torch.cuda.current_stream(dev)
+
+    # The c4 forward + backward leg runs first: its few hundred milliseconds
+    # of sustained work also bring the GPU to the clocks it holds under load,
+    # so that the c2 steps right after it are timed at those clocks rather
+    # than on the ramp of a freshly started process.
+    c4 = bench_c4(a.c4_steps, a.c4_warmup, kernels=True)
 
     with torch.inference_mode():
         for _ in range(a.warmup):
@@ -543,7 +613,6 @@ def main():
         y = layer(x, layout)
         torch.cuda.synchronize()
         peak_c2 = torch.cuda.max_memory_allocated(dev) - base
-    c4 = bench_c4(a.c4_steps, a.c4_warmup, kernels=True)
 
     m = layout.geometry.num_summaries
     edges = valid_edges(SHAPE, RADIUS)

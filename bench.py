@@ -164,16 +164,17 @@ def summary_pathway_ms(plan, steps, stream):
 
     The rows kernel runs the same summary pass (rotated queries against all
     summaries on MFMA, fixed Cauchy-Schwarz reference point) and the same
-    epilogue as the fused grid kernel, for every query row, with the local
-    term read from a zero fp32 buffer instead of computed: its duration is
-    the summary pathway's cost plus that extra read (4 B x H x N x d).
+    epilogue as the fused grid kernel, for every query row, in the mode the
+    indexed path uses: the local term sl * o_L is read from y (here the
+    layer's y, rewritten by every call) and y = that + gate * sg * o_G is
+    stored.  Its duration is the summary pathway's cost plus that read of y
+    (2 B x H x N x d, 100.7 MB at c2).
     """
     from pack3d_amd import _lib
 
     a = plan.attn_args
     rows = _lib.AttnArgs.from_buffer_copy(a)
-    o_local = torch.zeros(a.batch * a.heads * a.tokens * a.head_dim, dtype=torch.float32, device=plan.device)
-    rows.o_local_in = o_local.data_ptr()
+    rows.o_local_in = None
     rows.lse_local = None
     run = lambda: _lib.call("p3d_attn_fwd_rows", rows, stream.cuda_stream)
     run()
@@ -479,13 +480,14 @@ def bench_c4(steps, warmup, kernels=False):
 
 def probe_rates():
     """Issue rates and co-issue of the units the summary pathway uses
-    (p3d_probe_issue_rates), every operand in registers, at 1, 2 and 4 waves
+    (p3d_probe_issue_rates of the measurement library libpack3d_probe.so), every operand in registers, at 1, 2 and 4 waves
     per SIMD on every CU: SIMD cycles per wave-iteration (time x the run's
     shader clock / iterations per SIMD) and, for the single kinds, rates per
     second.  The clock comes from the waves' own shader-clock and 100 MHz
     wall-clock counters."""
     from pack3d_amd import _lib
 
+    probe = _lib.probe_lib()
     dev = torch.device("cuda:0")
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     stream = torch.cuda.current_stream(dev)
@@ -500,9 +502,11 @@ def probe_rates():
         for kind, name in kinds.items():
             if kind == 4 and wps > 2:
                 continue  # its registers allow at most 3 waves per SIMD
-            run = lambda: _lib.call("p3d_probe_issue_rates", kind, iters, blocks, cycles.data_ptr(),
-                                    stream.cuda_stream)
-            _lib.call("p3d_probe_issue_rates", kind, 64, blocks, cycles.data_ptr(), stream.cuda_stream)
+            def call(n):
+                if probe.p3d_probe_issue_rates(kind, n, blocks, cycles.data_ptr(), stream.cuda_stream):
+                    raise RuntimeError(probe.p3d_last_error().decode())
+            run = lambda: call(iters)
+            call(64)
             ms = time_events(run, 3, stream)
             c = cycles.view(-1, 2).double().sum(0).tolist()
             ghz = c[0] / c[1] * 0.1  # shader cycles per 10 ns tick -> GHz
@@ -657,7 +661,7 @@ def main():
         "roofline_exp": {"kernel": "k_attn_grid", "bound": "valu-transcendental", "achieved": float(f"{exp_rate:.4g}"),
                          "peak": PEAK_EXP_PER_S, "unit": "exp/s", "frac": round(exp_rate / PEAK_EXP_PER_S, 4),
                          "algorithmic_exps": exps},
-        "roofline_summary": {"kernel": "k_attn_rows (summary pathway + epilogue, local term from a zero buffer)",
+        "roofline_summary": {"kernel": "k_attn_rows (summary pathway + epilogue, local term read from y)",
                              "bound": "mfma", "achieved": round(flops_summary / (ms_summary * 1e-3) / 1e12, 2),
                              "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                              "frac": round(flops_summary / (ms_summary * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),

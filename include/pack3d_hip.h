@@ -440,14 +440,6 @@ int p3d_pool_bwd(const p3d_pool_args* pool, const float* dsk_part, const float* 
  * matmul to pin that layout on the device. */
 int p3d_selftest_mfma(int32_t dtype, const void* a, const void* b, float* d, void* stream);
 
-/* Issue-rate probe: blocks x 4 waves each run iters iterations of kind
- * (0: 16 v_exp_f32 chains, 1: 16 v_fma_f32 chains, 2: 4 bf16 32x32x16
- * MFMAs, 3: 0 and 2 together, independent, 4: the pipelined summary-sweep
- * tile pattern of head_dim 48, two tiles and column blocks) and write their
- * shader-clock cycles and 100 MHz wall-clock ticks to cycles[2 * wave],
- * cycles[2 * wave + 1] (blocks * 8 values).  Measures the issue rates and
- * co-issue the summary pathway is bound by. */
-int p3d_probe_issue_rates(int32_t kind, int64_t iters, int32_t blocks, long long* cycles, void* stream);
 
 /* sizeof of p3d_view, p3d_rope, p3d_pool_args, p3d_attn_args, p3d_bwd_args,
  * p3d_project_args into out[6], so a binding can check its struct mirrors. */

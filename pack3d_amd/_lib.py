@@ -95,7 +95,6 @@ SIGNATURES = {
     "p3d_local_fwd_indexed": ([ctypes.POINTER(AttnArgs), _P, c_int32, _P], c_int32),
     "p3d_selftest_mfma": ([c_int32, _P, _P, _P, _P], c_int32),
     "p3d_struct_sizes": ([_P], c_int32),
-    "p3d_probe_issue_rates": ([c_int32, c_int64, c_int32, _P, _P], c_int32),
     "p3d_rotate": ([View, View, c_int32, c_int32, c_int32, c_int32, c_int32, ctypes.POINTER(Rope), c_int32, _P],
                    c_int32),
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
@@ -140,6 +139,30 @@ def lib():
                     raise RuntimeError("pack3d_amd HIP library ABI mismatch; rebuild it")
                 _lib = handle
     return _lib
+
+
+PROBE_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libpack3d_probe.so")
+_probe = None
+
+
+def probe_lib():
+    """The measurement library (``include/pack3d_probe.h``): the issue-rate
+    probe behind ``bench.py --probe-rates``.  Not part of the product
+    library; loaded only when asked for."""
+    global _probe
+    if _probe is None:
+        with _lock:
+            if _probe is None:
+                if not os.path.exists(PROBE_PATH):
+                    raise RuntimeError(f"probe library missing at {PROBE_PATH}; build it with "
+                                       "`python -m pack3d_amd.build`")
+                handle = ctypes.CDLL(PROBE_PATH)
+                handle.p3d_probe_issue_rates.argtypes = [c_int32, c_int64, c_int32, _P, _P]
+                handle.p3d_probe_issue_rates.restype = c_int32
+                handle.p3d_last_error.argtypes = []
+                handle.p3d_last_error.restype = ctypes.c_char_p
+                _probe = handle
+    return _probe
 
 
 def call(name, *args):

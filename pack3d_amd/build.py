@@ -14,8 +14,10 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
+PROBE_SRC = os.path.join(HERE, "probe")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libpack3d_hip.so")
+PROBE_LIB = os.path.join(HERE, "libpack3d_probe.so")
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are disabled for device code: the compiler forms them
@@ -53,23 +55,33 @@ def _compile(src, hipcc, verbose):
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link the shared library; returns its path."""
-    hipcc = _hipcc()
-    os.makedirs(BUILD, exist_ok=True)
-    sources = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
-    workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")), 8)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objs = list(pool.map(lambda s: _compile(s, hipcc, verbose), sources))
-    tmp = LIB + ".tmp"
+def _link(hipcc, objs, out, verbose):
+    tmp = out + ".tmp"
     cmd = [hipcc, "--hip-link", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
            "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB}", flush=True)
+        print(f"built {out}", flush=True)
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source and link the shared libraries: the product
+    library from csrc/, and the measurement library (the issue-rate probe of
+    probe/, with the status functions it reports through); returns the
+    product library's path."""
+    hipcc = _hipcc()
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    probes = sorted(os.path.join(PROBE_SRC, f) for f in os.listdir(PROBE_SRC) if f.endswith(".hip"))
+    workers = min(len(sources) + len(probes), int(os.environ.get("MAX_JOBS", "8")), 8)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        objs = list(pool.map(lambda s: _compile(s, hipcc, verbose), sources + probes))
+    _link(hipcc, objs[:len(sources)], LIB, verbose)
+    status = os.path.join(BUILD, "status.hip.o")
+    _link(hipcc, objs[len(sources):] + [status], PROBE_LIB, verbose)
     return LIB
 
 

@@ -12,9 +12,25 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "pack3d_hip.h")
 
 
-def _declared():
-    text = open(HEADER).read()
+PROBE_HEADER = os.path.join(ROOT, "include", "pack3d_probe.h")
+
+
+def _declared(header=HEADER):
+    text = open(header).read()
     return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(p3d_\w+)\s*\(", text, re.M)))
+
+
+def test_probe_library_is_separate_from_the_product():
+    """The issue-rate probe is measurement scaffolding: its own library
+    exports what include/pack3d_probe.h declares, and the product library
+    does not export it."""
+    from pack3d_amd import _lib
+    probe = ctypes.CDLL(_lib.PROBE_PATH)
+    for name in _declared(PROBE_HEADER):
+        assert hasattr(probe, name), name
+    product = ctypes.CDLL(_lib.LIB_PATH)
+    assert not hasattr(product, "p3d_probe_issue_rates")
+    assert "p3d_probe_issue_rates" not in _declared()
 
 
 def test_library_exports_every_declared_symbol():

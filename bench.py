@@ -159,6 +159,28 @@ def layer_ms_unfused(layer, x, layout, steps):
         attention.pooled_core = real
 
 
+def layer_ms_graph(layer, x, layout, warmup, steps):
+    """ms per layer step replayed from a HIP graph of one step (captured
+    after two warm-up steps on a side stream), and the graph's output."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            layer(x, layout)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = layer(x, layout)
+    for _ in range(max(1, warmup)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    return 1000.0 * (time.perf_counter() - t0) / steps, out
+
+
 def summary_pathway_ms(plan, steps, stream):
     """Mean duration (ms) of the summary pathway alone on the plan's inputs.
 
@@ -589,6 +611,10 @@ def main():
         torch.cuda.synchronize()
         ms_layer = 1000.0 * (time.perf_counter() - t0) / a.steps
 
+        # The same step captured in a HIP graph and replayed (the way a
+        # serving loop runs it: no per-kernel launch from the host).
+        ms_graph, y_graph = layer_ms_graph(layer, x, layout, a.warmup, a.steps)
+
         # Per-kernel durations inside the same layer steps: HIP events on the
         # launch stream around the layer's launches (a second pass over the
         # steps, so the first one runs without them); then the layer step with
@@ -617,6 +643,8 @@ def main():
         y = layer(x, layout)
         torch.cuda.synchronize()
         peak_c2 = torch.cuda.max_memory_allocated(dev) - base
+        if not torch.equal(y_graph, y):
+            raise RuntimeError("the graph-replayed layer step differs from the eager step")
 
     m = layout.geometry.num_summaries
     edges = valid_edges(SHAPE, RADIUS)
@@ -649,6 +677,7 @@ def main():
                    "tokens_per_s": round(n / (ms_layer * 1e-3)), "ms_layer": round(ms_layer, 4),
                    "ms_core": round(ms_core, 4), "ms_project_pool_kernel": round(ms_proj_pool, 4),
                    "ms_attn_kernel": round(ms_attn, 4), "ms_summary_pathway": round(ms_summary, 4),
+                   "ms_layer_graph": round(ms_graph, 4),
                    "ms_layer_unfused": round(ms_layer_unfused, 4),
                    "ms_pool_kernel_unfused_layer": round(ms_pool, 4),
                    "incremental_peak_allocated_bytes": int(peak_c2),

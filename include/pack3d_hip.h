@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 15
+#define P3D_ABI_VERSION 16
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -384,6 +384,10 @@ typedef struct p3d_bwd_args {
     p3d_view dv_local;          /* out: [B,G,N,D] view (dtype), 16-byte aligned rows */
     float* dsk_part;            /* out: [splits,B,G,Mp,D] fp32, true key units */
     float* dsv_part;            /* out: [splits,B,G,Mp,D] fp32 */
+    const void* q_t;            /* optional: rotated q transposed, [B*H][D][N] (p3d_transpose_rows) */
+    const void* dog_t;          /* optional: dog transposed, [B*H][D][N]; with both, fp16 / bf16,
+                                   N >= 64 and N a multiple of 8, p3d_global_bwd_dkv copies its
+                                   transposed query stages from them by LDS DMA */
 } p3d_bwd_args;
 
 /* Fusion step (kernels.py:106-127): dO_L = round(dy sl), dO_G = round(dy gate
@@ -417,6 +421,14 @@ int p3d_global_bwd(const p3d_bwd_args* args, void* stream);
  * same stream. */
 int p3d_global_bwd_dq(const p3d_bwd_args* args, void* stream);
 int p3d_global_bwd_dkv(const p3d_bwd_args* args, void* stream);
+
+/* dst[(b H + h) D + c][n] = src[b][h][n][c] for fp16 / bf16 (tokens a
+ * multiple of 8, src rows 16-byte aligned): the transposed copies q_t and
+ * dog_t of p3d_bwd_args.  The reference has no counterpart (its Triton dK/dV
+ * kernel loads q and dO tiles transposed, kernels.py:209-240); this build
+ * stages them for the summary dK/dV pass. */
+int p3d_transpose_rows(p3d_view src, void* dst, int32_t batch, int32_t heads, int32_t tokens, int32_t head_dim,
+                       int32_t dtype, void* stream);
 
 /* dq = R^T round(round(dq_local) + round(dq_global)) and dkl = R^T round(dk_local)
  * (kernels.py:202-206 rounding; R^T the inverse rotation of rope), written

@@ -25,7 +25,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 15  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 16  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -65,7 +65,8 @@ class BwdArgs(ctypes.Structure):
                 ("dy", View), ("dol", c_void_p), ("dog", c_void_p), ("delta_local", c_void_p),
                 ("delta_global", c_void_p), ("dgate", c_void_p), ("dsl_part", c_void_p), ("dsg_part", c_void_p),
                 ("sv_rows", c_void_p), ("skt", c_void_p), ("dq_local", c_void_p), ("dq_global", c_void_p),
-                ("dk_local", c_void_p), ("dv_local", View), ("dsk_part", c_void_p), ("dsv_part", c_void_p)]
+                ("dk_local", c_void_p), ("dv_local", View), ("dsk_part", c_void_p), ("dsv_part", c_void_p),
+                ("q_t", c_void_p), ("dog_t", c_void_p)]
 
 
 class ProjectArgs(ctypes.Structure):
@@ -113,6 +114,7 @@ SIGNATURES = {
     "p3d_global_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_global_bwd_dq": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_global_bwd_dkv": ([ctypes.POINTER(BwdArgs), _P], c_int32),
+    "p3d_transpose_rows": ([View, _P, c_int32, c_int32, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_finish_bwd": ([ctypes.POINTER(BwdArgs), ctypes.POINTER(Rope), View, View, _P], c_int32),
     "p3d_pool_bwd": ([ctypes.POINTER(PoolArgs), _P, _P, c_int32, View, View, _P, _P, _P], c_int32),
 }

@@ -344,6 +344,13 @@ def backward(dy, q, kl, vl, kg, vg, weight, bias, gate, sl, sg, sk, svt, sk_norm
         nb, rev = geometry.neighbors, geometry.reverse_neighbors
         _lib.call("p3d_local_bwd_indexed", a, nb.data_ptr(), nb.shape[1], rev.data_ptr(), rev.shape[1], stream)
     _lib.call("p3d_global_bwd_dq", a, stream)
+    if q.dtype != torch.float32 and n >= 64 and n % 8 == 0:
+        # Transposed copies of the rotated q and of dO_G: the summary dK/dV
+        # pass copies its transposed query stages from them by LDS DMA.
+        bufs["q_t"], bufs["dog_t"] = empty(b * h * d * n), empty(b * h * d * n)
+        _lib.call("p3d_transpose_rows", _lib.view(qr), bufs["q_t"].data_ptr(), b, h, n, d, dt, stream)
+        _lib.call("p3d_transpose_rows", _lib.view(bufs["dog"]), bufs["dog_t"].data_ptr(), b, h, n, d, dt, stream)
+        a.q_t, a.dog_t = bufs["q_t"].data_ptr(), bufs["dog_t"].data_ptr()
     _lib.call("p3d_global_bwd_dkv", a, stream)
     _lib.call("p3d_finish_bwd", a, rope.struct(), _lib.view(dq), _lib.view(dkl), stream)
 

@@ -13,6 +13,8 @@
 //
 // All q / k inputs here are already rotated (the host rotates them once);
 // summary keys are stored times log2(e)/sqrt(d) as in the forward.
+#include <type_traits>
+
 #include "attn_common.hpp"
 
 namespace p3d {
@@ -43,6 +45,7 @@ struct BwdDev {
     char* dv_l;
     int64_t dvsb, dvsh, dvsn;
     float *dsk_part, *dsv_part;
+    const char *q_t, *dog_t;  // optional: q and dO_G transposed, [B*H][D][N]
 };
 
 template <typename T>
@@ -376,7 +379,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
 // dO_G transposed (row stride SK + EP, zero padding rows), and -lse_G (log2
 // units; -inf past the last query) and -Delta_G.  Each thread moves PI
 // 16-byte pieces.
-template <typename C, int SK>
+template <typename C, int SK, bool TDMA = false>
 struct KvStage {
     typedef typename C::T_ T;
     static constexpr int EP = Piece<T>::N;
@@ -454,13 +457,15 @@ struct KvStage {
             if (r < SK) {
                 *reinterpret_cast<uint4*>(stage + r * C::KSTR + c) = q[i];
                 *reinterpret_cast<uint4*>(stage + SK * C::KSTR + r * C::KSTR + c) = d[i];
-                const T* qv = reinterpret_cast<const T*>(&q[i]);
-                const T* dv = reinterpret_cast<const T*>(&d[i]);
-                const int col = swz_col<MASK>(c, r);  // rows c .. c + EP - 1 share one group swizzle
+                if constexpr (!TDMA) {
+                    const T* qv = reinterpret_cast<const T*>(&q[i]);
+                    const T* dv = reinterpret_cast<const T*>(&d[i]);
+                    const int col = swz_col<MASK>(c, r);  // rows c .. c + EP - 1 share one group swizzle
 #pragma unroll
-                for (int e = 0; e < EP; ++e) {
-                    qt[(c + e) * TGS + col] = qv[e];
-                    dt[(c + e) * TGS + col] = dv[e];
+                    for (int e = 0; e < EP; ++e) {
+                        qt[(c + e) * TGS + col] = qv[e];
+                        dt[(c + e) * TGS + col] = dv[e];
+                    }
                 }
             }
         }
@@ -473,6 +478,58 @@ struct KvStage {
     }
 };
 
+// The transposed query and dO_G regions of a dK/dV stage (16-bit types),
+// copied by the LDS DMA from transposed copies in HBM ([B*H][D][N], one row
+// of N queries per channel) instead of being written from the staged rows
+// by 2-byte LDS stores.  A region row c (channel) holds the stage's SK
+// queries in pieces of EP; physical piece P of row c holds logical query
+// group P ^ swizzle(c) (the layout swz_col<MASK> gives the stores), piece
+// SK / EP is padding (its lanes fetch group 0 again).  A copy writes 64
+// consecutive pieces; the last copy of a region starts 64 pieces before the
+// region's end.  Copies are split evenly over the waves (a wave with fewer
+// repeats its last one).
+template <typename C, int SK>
+struct KvTransDma {
+    typedef typename C::T_ T;
+    typedef KvStage<C, SK, true> S;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int PR = S::TGS / EP;               // pieces per region row
+    static constexpr int SLOTS = C::D * PR;
+    static constexpr int CH = (SLOTS + 63) / 64;
+    static constexpr int PER = (2 * CH + kWaves - 1) / kWaves;
+    static_assert(S::TGS % EP == 0 && SLOTS >= 64 && sizeof(T) == 2, "transposed stage layout");
+    uint32_t off[PER];  // byte offset of this lane's source piece from the stage's first query of channel 0
+    int wave;
+
+    __device__ __forceinline__ static int chunk(int w, int i) { return min(w * PER + i, 2 * CH - 1); }
+    __device__ __forceinline__ static int first_slot(int c) { return min(64 * (c % CH), SLOTS - 64); }
+
+    __device__ __forceinline__ KvTransDma(int n) {
+        wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int slot = first_slot(chunk(wave, i)) + lane;
+            const int row = slot / PR, pp = slot % PR;
+            const int group = pp < SK / EP ? pp ^ ((row >> 3) & S::MASK) : 0;
+            off[i] = (uint32_t)(row * n + group * EP) * sizeof(T);
+        }
+    }
+
+    // Copy queries [bp, bp + SK) of head plane bh into the stage at `stage`.
+    __device__ __forceinline__ void copy(const BwdDev& a, int64_t bh, int bp, T* stage) const {
+        const int64_t e0 = bh * C::D * (int64_t)a.N + bp;
+        const uint32_t lds0 = lds_address(stage + S::ROWS);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = chunk(wave, i), r = c / CH;
+            const T* src = (r == 0 ? tp<T>(a.q_t) : tp<T>(a.dog_t)) + e0;
+            dma_copy16(src, off[i], lds0 + (uint32_t)(r * 32 * C::MB * S::TGS) * sizeof(T) +
+                                        (uint32_t)first_slot(c) * 16u);
+        }
+    }
+};
+
 // Global dK / dV of the summaries (kernels.py:209-237): lane = summary (a
 // wave owns 32), queries streamed in stages of 64 over this split's range of
 // every query head of the kv group.  S[q][key] = q . sk (log2 units) with the
@@ -480,11 +537,20 @@ struct KvStage {
 // sv; dS = P (dP - Delta); dK^T += q^T dS, dV^T += dO^T P (dS and P enter as
 // B operands).  Writes fp32 partials [split][bg][m][D]; dK is in true units
 // (divided by sqrt(d)), before the pooling's 1/count.
-template <typename T, int D>
+template <typename C, int SK>
+using KvStageR = KvStage<C, SK>;
+
+// Stand-in for KvTransDma where the transposed regions are staged from registers.
+struct NoTransDma {
+    __device__ __forceinline__ explicit NoTransDma(int) {}
+};
+
+// TDMA: the transposed regions come by LDS DMA from a.q_t / a.dog_t.
+template <typename T, int D, bool TDMA>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
     typedef Cfg<T, D> C;
-    constexpr int SK = stage_rows<C, KvStage>();
-    typedef KvStage<C, SK> S;
+    constexpr int SK = stage_rows<C, KvStageR>();
+    typedef KvStage<C, SK, TDMA> S;
     extern __shared__ __align__(16) unsigned char smem[];
     T* lds = reinterpret_cast<T*>(smem);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, qi = lane & 31;
@@ -533,10 +599,14 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
                       min(SK, min(q1, a.N) - bp));
         };
         int nq = q0;
+        int64_t tbh = bh0;  // head plane of the stage at nq, for the transposed copies
         S regs;
         regs.init(a.qsn, min(SK, a.N) - 1);
         load_stage(regs, nq);
+        const std::conditional_t<TDMA, KvTransDma<C, SK>, NoTransDma> tdma(a.N);
+        if constexpr (TDMA) tdma.copy(a, tbh, min(nq, last), lds);
         regs.store(lds);
+        if constexpr (TDMA) dma_wait();
         __syncthreads();
         int buf = 0;
         for (int it = 0; it < total; ++it) {
@@ -548,8 +618,13 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
                 do_head += (int64_t)a.N * D;
                 ls_head += a.N;
                 dl_head += a.N;
+                ++tbh;
             }
             if (more) load_stage(regs, nq);
+            // The other buffer held the previous stage, which every wave
+            // finished before the last barrier.
+            if constexpr (TDMA)
+                if (more) tdma.copy(a, tbh, min(nq, last), lds + (buf ^ 1) * S::SIZE);
             const T* cur = lds + buf * S::SIZE;
             const float* nlse = reinterpret_cast<const float*>(cur + S::ROWS + S::TRANS);
             const float* ndlt = nlse + SK;
@@ -589,6 +664,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dkv(BwdDev a) {
                 }
             }
             if (more) regs.store(lds + (buf ^ 1) * S::SIZE);
+            if constexpr (TDMA) dma_wait();
             __syncthreads();
             buf ^= 1;
         }
@@ -664,6 +740,39 @@ __global__ __launch_bounds__(256) void k_finish_bwd(BwdDev a, RopeDev rope, int 
     store_piece<T>(reinterpret_cast<T*>(o.data) + b * o.sb + h * o.sh + (int64_t)n * o.sn + piece * EP, x);
 }
 
+// ------------------------------------------------------------ transpose
+// dst[(b H + h) D + c][n] = src[b][h][n][c] for 16-bit rows (N a multiple
+// of 8): a thread loads an 8-row x 8-channel block as eight 16-byte pieces,
+// transposes it in registers and stores eight 16-byte pieces, one per
+// channel.  Consecutive threads take consecutive channel pieces of a row
+// group, so the loads are whole row spans.
+struct TrDev {
+    const uint16_t* src;
+    int64_t sb, sh, sn;
+    uint16_t* dst;
+    int H, N, D;
+};
+
+__global__ __launch_bounds__(256) void k_transpose_rows(TrDev a) {
+    const int cgs = a.D / 8;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)(a.N / 8) * cgs) return;
+    const int rg = (int)(idx / cgs), cg = (int)(idx - (int64_t)rg * cgs);
+    const int bh = blockIdx.y, b = bh / a.H, h = bh - b * a.H;
+    const uint16_t* src = a.src + b * a.sb + h * a.sh + (int64_t)(8 * rg) * a.sn + 8 * cg;
+    uint16_t in[8][8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) *reinterpret_cast<uint4*>(in[r]) = *reinterpret_cast<const uint4*>(src + r * a.sn);
+    uint16_t out[8][8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) out[c][r] = in[r][c];
+    uint16_t* dst = a.dst + ((int64_t)bh * a.D + 8 * cg) * a.N + 8 * rg;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) *reinterpret_cast<uint4*>(dst + (int64_t)c * a.N) = *reinterpret_cast<const uint4*>(out[c]);
+}
+
 int fill_bwd(const p3d_bwd_args& x, BwdDev& d) {
     const int es = dtype_size(x.dtype);
     P3D_REQUIRE(x.dtype >= P3D_F32 && x.dtype <= P3D_BF16, "unknown dtype");
@@ -698,6 +807,7 @@ int fill_bwd(const p3d_bwd_args& x, BwdDev& d) {
     d.dq_l = x.dq_local, d.dq_g = x.dq_global, d.dk_l = x.dk_local;
     d.dv_l = (char*)x.dv_local.data, d.dvsb = x.dv_local.sb, d.dvsh = x.dv_local.sh, d.dvsn = x.dv_local.sn;
     d.dsk_part = x.dsk_part, d.dsv_part = x.dsv_part;
+    d.q_t = (const char*)x.q_t, d.dog_t = (const char*)x.dog_t;
     return P3D_OK;
 }
 
@@ -708,7 +818,7 @@ size_t lds_dq() {
 
 template <typename C>
 size_t lds_dkv() {
-    return (size_t)2 * KvStage<C, stage_rows<C, KvStage>()>::SIZE * sizeof(typename C::T_);
+    return (size_t)2 * KvStage<C, stage_rows<C, KvStageR>()>::SIZE * sizeof(typename C::T_);
 }
 
 template <int D>
@@ -733,10 +843,24 @@ void launch_dq(const BwdDev& d, int dtype, hipStream_t s) {
 template <int D>
 void launch_dkv(const BwdDev& d, int dtype, hipStream_t s) {
     const dim3 grid((unsigned)cdiv(d.M, 32 * kWaves), (unsigned)d.splits, (unsigned)(d.B * d.G));
+    // The transposed copies are used when given, for 16-bit types whose
+    // stages are 64 queries that every stage's window holds (N >= 64, and N
+    // a multiple of 8 so that every window starts on a 16-byte piece).
+    const bool tdma = d.q_t && d.dog_t && dtype != P3D_F32 && d.N >= 64 && d.N % 8 == 0;
     switch (dtype) {
-        case P3D_F32: k_global_dkv<float, D><<<grid, 64 * kWaves, lds_dkv<Cfg<float, D>>(), s>>>(d); break;
-        case P3D_F16: k_global_dkv<_Float16, D><<<grid, 64 * kWaves, lds_dkv<Cfg<_Float16, D>>(), s>>>(d); break;
-        default: k_global_dkv<__bf16, D><<<grid, 64 * kWaves, lds_dkv<Cfg<__bf16, D>>(), s>>>(d); break;
+        case P3D_F32: k_global_dkv<float, D, false><<<grid, 64 * kWaves, lds_dkv<Cfg<float, D>>(), s>>>(d); break;
+        case P3D_F16:
+            if (tdma)
+                k_global_dkv<_Float16, D, true><<<grid, 64 * kWaves, lds_dkv<Cfg<_Float16, D>>(), s>>>(d);
+            else
+                k_global_dkv<_Float16, D, false><<<grid, 64 * kWaves, lds_dkv<Cfg<_Float16, D>>(), s>>>(d);
+            break;
+        default:
+            if (tdma)
+                k_global_dkv<__bf16, D, true><<<grid, 64 * kWaves, lds_dkv<Cfg<__bf16, D>>(), s>>>(d);
+            else
+                k_global_dkv<__bf16, D, false><<<grid, 64 * kWaves, lds_dkv<Cfg<__bf16, D>>(), s>>>(d);
+            break;
     }
 }
 
@@ -848,4 +972,21 @@ extern "C" int p3d_finish_bwd(const p3d_bwd_args* args, const p3d_rope* rope, p3
         default: dispatch_finish<__bf16>(d, r, args->head_dim, dq, dkl, s); break;
     }
     return check_launch("p3d_finish_bwd");
+}
+
+extern "C" int p3d_transpose_rows(p3d_view src, void* dst, int32_t batch, int32_t heads, int32_t tokens,
+                                  int32_t head_dim, int32_t dtype, void* stream) {
+    P3D_REQUIRE(src.data && dst, "null pointer argument");
+    P3D_REQUIRE(dtype == P3D_F16 || dtype == P3D_BF16, "dtype must be fp16 or bf16");
+    P3D_REQUIRE(batch >= 1 && heads >= 1 && tokens >= 8 && tokens % 8 == 0, "tokens must be a multiple of 8");
+    P3D_REQUIRE(head_dim >= 8 && head_dim % 8 == 0, "head_dim must be a multiple of 8");
+    P3D_REQUIRE(view_ok(src, 2), "src rows must be 16-byte aligned");
+    P3D_REQUIRE(aligned16(dst), "dst must be 16-byte aligned");
+    P3D_REQUIRE((int64_t)batch * heads <= 65535, "batch * heads exceeds the launch grid");
+    TrDev d;
+    d.src = (const uint16_t*)src.data, d.sb = src.sb, d.sh = src.sh, d.sn = src.sn;
+    d.dst = (uint16_t*)dst, d.H = heads, d.N = tokens, d.D = head_dim;
+    const int64_t items = (int64_t)(tokens / 8) * (head_dim / 8);
+    k_transpose_rows<<<dim3((unsigned)cdiv(items, 256), (unsigned)(batch * heads)), 256, 0, as_stream(stream)>>>(d);
+    return check_launch("p3d_transpose_rows");
 }

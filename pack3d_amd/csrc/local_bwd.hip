@@ -190,6 +190,145 @@ __device__ __forceinline__ void trans_frags(const typename C::T_* Tb, int tps, i
         }
 }
 
+// dQ^T += K^T dS^T for chunk c of one plane: kf / vf are the chunk's K and V
+// row fragments (lane = key of the tile), tf the K^T fragments (A operand).
+template <typename C>
+__device__ __forceinline__ void dq_chunk(const typename C::Frag* kf, const typename C::Frag* vf,
+                                         const typename C::Frag* tf, const typename C::Frag* qf,
+                                         const typename C::Frag* df, bool zok, uint32_t kmask, float scale_log2,
+                                         float lse2, float delta, int& shift, f32x16* acc) {
+    typedef typename C::T_ T;
+    const f32x16 s = score_tile<C>(kf, qf);
+    const f32x16 dp = score_tile<C>(vf, df);
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const bool ok = zok && ((kmask >> r) & 1);
+        ds[r] = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], scale_log2, -lse2)) * (dp[r] - delta) : 0.f;
+    }
+    fit_fp16<C>(ds, shift, acc);
+#pragma unroll
+    for (int ks = 0; ks < C::KSTEPS; ++ks) {
+        const typename C::Frag pf = frag_from_p<T>(ds, ks);
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) acc[mb] = C::M::mfma(tf[mb * C::KSTEPS + ks], pf, acc[mb]);
+    }
+}
+
+// dK^T += q^T dS and dV^T += dO^T P for chunk c of one plane: qa / da are the
+// chunk's q and dO row fragments (lane = query of the tile), qt / dt the
+// transposed fragments (A operands); lse2s / dlts hold the plane's lse (log2
+// units, +inf where a position has no gradient) and Delta.
+template <typename C>
+__device__ __forceinline__ void dkv_chunk(const typename C::Frag* qa, const typename C::Frag* da,
+                                          const typename C::Frag* qt, const typename C::Frag* dt,
+                                          const typename C::Frag* kf, const typename C::Frag* vf, bool zok,
+                                          uint32_t qmask, float scale_log2, const float* lse2s, const float* dlts,
+                                          int wy, int wx, int c, int g, int& shift, f32x16* acck, f32x16* accv) {
+    typedef typename C::T_ T;
+    const f32x16 s = score_tile<C>(qa, kf);
+    const f32x16 dp = score_tile<C>(da, vf);
+    float p[16], ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int pos = chunk_pos(wy, wx, c, kperm<C::E, C::KS>(acc_row(r, g)));
+        const bool ok = zok && ((qmask >> r) & 1);
+        p[r] = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], scale_log2, -lse2s[pos])) : 0.f;
+        ds[r] = p[r] * (dp[r] - dlts[pos]);
+    }
+    fit_fp16<C>(ds, shift, acck);
+#pragma unroll
+    for (int ks = 0; ks < C::KSTEPS; ++ks) {
+        const typename C::Frag dsf = frag_from_p<T>(ds, ks);
+        const typename C::Frag pf = frag_from_p<T>(p, ks);
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb) {
+            acck[mb] = C::M::mfma(qt[mb * C::KSTEPS + ks], dsf, acck[mb]);
+            accv[mb] = C::M::mfma(dt[mb * C::KSTEPS + ks], pf, accv[mb]);
+        }
+    }
+}
+
+// Halo planes by the LDS DMA (16-bit types, head_dim <= 64).  Each plane's
+// rows of two tensors (K and V for dQ, q and dO for dK / dV) are copied into
+// one of two plane buffers while the previous plane is processed, in the
+// row-major layout of the register-staged kernels (row stride KSTR: D / 8
+// 16-byte slots and one spare, whose lanes fetch piece 0 of the same row
+// again).  The transposed A operands are read from those rows with
+// ds_read_b64_tr_b16, so nothing is staged transposed.  The packed row of
+// every halo position of the brick is looked up once into a table in LDS;
+// positions outside the grid take the row of the nearest grid position
+// (finite values, excluded by the stencil masks).  SIDE: each buffer also
+// holds the plane's lse (log2 units) and Delta, written from registers.
+template <typename C>
+constexpr bool kBwdPlaneDma = sizeof(typename C::T_) == 2 && C::D <= 64;
+
+template <typename C, bool SIDE>
+struct BwdPlaneDma {
+    typedef typename C::T_ T;
+    typedef typename C::Frag Frag;
+    static constexpr int EP = Piece<T>::N;
+    static constexpr int KROW = C::KSTR / EP;            // 16-byte slots per row
+    static constexpr int SLOTS = kPlaneKeys * KROW;      // slots of one tensor's plane
+    static constexpr int CH = (SLOTS + 63) / 64;         // copies per tensor
+    static constexpr int PER = (2 * CH + kWaves - 1) / kWaves;
+    static constexpr size_t REGION = (size_t)SLOTS * 16;
+    static constexpr size_t BUF = 2 * REGION + (SIDE ? 2 * kPlaneKeys * sizeof(float) : 0);
+    static constexpr int kMaxPlanes = 8;                 // 4 + 2 rz with rz <= 2
+    static constexpr size_t BYTES = 2 * BUF + (size_t)kMaxPlanes * kPlaneKeys * sizeof(int);
+    static_assert(C::KSTR % EP == 0 && C::KSTR > C::D, "rows need a spare slot");
+    // The copies address LDS through M0; the buffers stay inside the first
+    // 128 KB of the workgroup's allocation.
+    static_assert(2 * BUF <= 128 * 1024, "copy destinations below 128 KB");
+
+    // Packed rows of the halo positions of planes [0, planes) (z from Z0 - rz).
+    __device__ __forceinline__ static void fill_rows(const LbDev& a, int Z0, int Y0, int X0, int planes, int* rows) {
+        for (int i = threadIdx.x; i < planes * kPlaneKeys; i += blockDim.x) {
+            const int hz = i / kPlaneKeys, k = i - hz * kPlaneKeys, ky = k / kPlane, kx = k - ky * kPlane;
+            const int gz = min(max(Z0 - a.rz + hz, 0), a.Z - 1);
+            const int gy = min(max(Y0 - a.ry + ky, 0), a.Y - 1);
+            const int gx = min(max(X0 - a.rx + kx, 0), a.X - 1);
+            rows[i] = (int)packed_row(a, gz, gy, gx);
+        }
+    }
+
+    // Issue the copies of one plane (its rows at `rows`): rows of A into the
+    // first region of `buf`, rows of B into the second.
+    __device__ __forceinline__ static void copy(const T* A, int64_t asn, const T* B, int64_t bsn, const int* rows,
+                                                unsigned char* buf, int wave, int lane) {
+        const uint32_t lds0 = lds_address(buf);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int c = min(wave * PER + i, 2 * CH - 1);  // wave-uniform
+            const bool second = c >= CH;
+            const int first = min(64 * (second ? c - CH : c), SLOTS - 64);
+            const int slot = first + lane, key = slot / KROW, sl = slot - key * KROW;
+            const int64_t row = rows[key];
+            const int e = (sl < C::D / EP ? sl : 0) * EP;
+            const T* src = second ? B + row * bsn + e : A + row * asn + e;
+            dma_copy16(src, lds0 + (second ? (uint32_t)REGION : 0u) + (uint32_t)first * 16u);
+        }
+    }
+
+    // A-operand fragment of block mb / k-step of a chunk from plane rows:
+    // lane l holds channel 32 mb + l % 32 of the rows row0 .. row0 + 7
+    // (consecutive in x); channels past D are zero.
+    __device__ __forceinline__ static Frag tfrag(const T* rows, int row0, int mb, int lane) {
+        Frag f = tr_frag<T, Frag>(rows, row0, C::KSTR, 32 * mb, C::D - 16, lane);
+        if (32 * mb + 16 >= C::D && 32 * mb + 16 * ((lane >> 4) & 1) >= C::D) f = frag_fill<T>(0.f);
+        return f;
+    }
+
+    __device__ __forceinline__ static void tfrags(const T* rows, int wy, int wx, int c, int lane, Frag* f) {
+        const int g = lane >> 5;
+#pragma unroll
+        for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+            for (int ks = 0; ks < C::KSTEPS; ++ks)
+                f[mb * C::KSTEPS + ks] = tfrag(rows, chunk_pos(wy, wx, c, ks * C::KS + C::E * g), mb, lane);
+    }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(64 * kWaves) void k_local_dq_grid(LbDev a) {
     typedef Cfg<T, D> C;
@@ -251,21 +390,7 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dq_grid(LbDev a) {
             load_kfrags<C>(Kr + chunk_pos(wy, wx, c, kap) * C::KSTR + C::E * g, kf);
             load_kfrags<C>(Vr + chunk_pos(wy, wx, c, kap) * C::KSTR + C::E * g, vf);
             trans_frags<C>(Kt, TPS, wy, wx, c, lane, tf);
-            const f32x16 s = score_tile<C>(kf, qf);
-            const f32x16 dp = score_tile<C>(vf, df);
-            float ds[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const bool ok = zok && ((kmask[c] >> r) & 1);
-                ds[r] = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], a.scale_log2, -lse2)) * (dp[r] - delta) : 0.f;
-            }
-            fit_fp16<C>(ds, shift, acc);
-#pragma unroll
-            for (int ks = 0; ks < C::KSTEPS; ++ks) {
-                const typename C::Frag pf = frag_from_p<T>(ds, ks);
-#pragma unroll
-                for (int mb = 0; mb < C::MB; ++mb) acc[mb] = C::M::mfma(tf[mb * C::KSTEPS + ks], pf, acc[mb]);
-            }
+            dq_chunk<C>(kf, vf, tf, qf, df, zok, kmask[c], a.scale_log2, lse2, delta, shift, acc);
         }
     }
     if (!qok) return;
@@ -278,6 +403,106 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dq_grid(LbDev a) {
             const int c = 32 * mb + acc_row(r, g);
             if (c < D) dq[c] = acc[mb][r] * out_scale;
         }
+}
+
+// k_local_dq_grid with the planes copied by the LDS DMA (kBwdPlaneDma types).
+template <typename T, int D>
+__global__ __launch_bounds__(64 * kWaves) void k_local_dq_grid_dma(LbDev a) {
+    typedef Cfg<T, D> C;
+    typedef BwdPlaneDma<C, false> PD;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int* const rowtab = reinterpret_cast<int*>(smem + 2 * PD::BUF);
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, qi = lane & 31;
+    const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H, kvh = h / (a.H / a.G);
+    const int brick = xcd_brick(blockIdx.x, gridDim.x);
+    const int Z0 = 4 * (brick / (a.bricks_y * a.bricks_x));
+    const int Y0 = 8 * ((brick / a.bricks_x) % a.bricks_y);
+    const int X0 = 8 * (brick % a.bricks_x);
+    const int nb = wave >> 2, wy = (wave >> 1) & 1, wx = wave & 1;
+    const int qy = (qi >> 2) & 3, qx = qi & 3;
+    const int qz = 2 * nb + (qi >> 4);
+    const int planes = 4 + 2 * a.rz;
+    const T* KL = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
+    const T* VL = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
+    PD::fill_rows(a, Z0, Y0, X0, planes, rowtab);
+    __syncthreads();
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);
+    if ((unsigned)(Z0 - a.rz) < (unsigned)a.Z) PD::copy(KL, a.ksn, VL, a.vsn, rowtab, smem, uwave, lane);
+
+    const int gz = Z0 + qz, gy = Y0 + 4 * wy + qy, gx = X0 + 4 * wx + qx;
+    const bool qok = gz < a.Z && gy < a.Y && gx < a.X;
+    const int64_t qrow = qok ? packed_row(a, gz, gy, gx) : 0;
+    const int64_t qidx = (int64_t)bh * a.N + qrow;
+    typename C::Frag qf[C::NT], df[C::NT];
+    row_frags<C>(tp<T>(a.q) + b * a.qsb + h * a.qsh + qrow * a.qsn, qok, g, qf);
+    row_frags<C>(tp<T>(a.dol) + qidx * D, qok, g, df);
+    const float lse = qok ? a.lse[qidx] : -INFINITY;
+    const bool live = lse != -INFINITY;  // an all-masked row has no local gradient
+    const float lse2 = live ? lse * kLog2e : 0.f;
+    const float delta = qok ? a.delta[qidx] : 0.f;
+    f32x16 acc[C::MB];
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mb][r] = 0.f;
+    int shift = 0;
+    const uint32_t kmask[2] = {chunk_mask<C>(a, 0, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx),
+                               chunk_mask<C>(a, 1, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx)};
+    for (int hz = 0; hz < planes; ++hz) {
+        const int pz = Z0 - a.rz + hz;
+        // Plane hz has landed, and every wave is done with plane hz - 1,
+        // whose buffer takes the copy of plane hz + 1.
+        dma_wait();
+        __syncthreads();
+        if (hz + 1 < planes && (unsigned)(pz + 1) < (unsigned)a.Z)
+            PD::copy(KL, a.ksn, VL, a.vsn, rowtab + (hz + 1) * kPlaneKeys, smem + ((hz + 1) & 1) * PD::BUF, uwave,
+                     lane);
+        if ((unsigned)pz >= (unsigned)a.Z) continue;
+        // Column block nb holds query planes 2nb and 2nb + 1.
+        if (hz < 2 * nb || hz > 2 * nb + 1 + 2 * a.rz) continue;
+        const T* Kb = reinterpret_cast<const T*>(smem + (hz & 1) * PD::BUF);
+        const T* Vb = reinterpret_cast<const T*>(smem + (hz & 1) * PD::BUF + PD::REGION);
+        const bool zok = (unsigned)(hz - qz) <= (unsigned)(2 * a.rz) && live;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            if (4 * c >= 4 + 2 * a.ry) continue;
+            const int kap = kperm<C::E, C::KS>(qi);
+            typename C::Frag kf[C::NT], vf[C::NT], tf[C::MB * C::KSTEPS];
+            load_kfrags<C>(Kb + chunk_pos(wy, wx, c, kap) * C::KSTR + C::E * g, kf);
+            load_kfrags<C>(Vb + chunk_pos(wy, wx, c, kap) * C::KSTR + C::E * g, vf);
+            PD::tfrags(Kb, wy, wx, c, lane, tf);
+            dq_chunk<C>(kf, vf, tf, qf, df, zok, kmask[c], a.scale_log2, lse2, delta, shift, acc);
+        }
+    }
+    if (!qok) return;
+    float* dq = a.dq + qidx * D;
+    const float out_scale = ldexpf(a.scale, shift);
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int c = 32 * mb + acc_row(r, g);
+            if (c < D) dq[c] = acc[mb][r] * out_scale;
+        }
+}
+
+// lse (log2 units; +inf where the position has no gradient: outside the grid
+// or the halo, or an all-masked row) and Delta of halo position p of plane
+// pz for query head plane bh; rows: that plane's row table.
+__device__ __forceinline__ void plane_side(const LbDev& a, int64_t bh, int pz, int Y0, int X0, int p,
+                                           const int* rows, float& l2, float& dl) {
+    const int py = p / kPlane, px = p - py * kPlane;
+    const int qy = Y0 - a.ry + py, qx = X0 - a.rx + px;
+    const bool in = (unsigned)pz < (unsigned)a.Z && (unsigned)qy < (unsigned)a.Y && (unsigned)qx < (unsigned)a.X &&
+                    py < 8 + 2 * a.ry && px < 8 + 2 * a.rx;
+    l2 = INFINITY, dl = 0.f;
+    if (in) {
+        const int64_t qidx = bh * a.N + rows[p];
+        const float l = a.lse[qidx];
+        l2 = l == -INFINITY ? INFINITY : l * kLog2e;  // all-masked rows carry no gradient
+        dl = a.delta[qidx];
+    }
 }
 
 template <typename T, int D>
@@ -358,29 +583,130 @@ __global__ __launch_bounds__(64 * kWaves) void k_local_dkv_grid(LbDev a) {
                 load_kfrags<C>(Dr + chunk_pos(wy, wx, c, kap) * C::KSTR + C::E * g, da);
                 trans_frags<C>(Qt, TPS, wy, wx, c, lane, qt);
                 trans_frags<C>(Dt, TPS, wy, wx, c, lane, dt);
-                const f32x16 s = score_tile<C>(qa, kf);
-                const f32x16 dp = score_tile<C>(da, vf);
-                float p[16], ds[16];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int pos = chunk_pos(wy, wx, c, kperm<C::E, C::KS>(acc_row(r, g)));
-                    const bool ok = zok && ((qmask[c] >> r) & 1);
-                    p[r] = ok ? __builtin_amdgcn_exp2f(fmaf(s[r], a.scale_log2, -lse2s[pos])) : 0.f;
-                    ds[r] = p[r] * (dp[r] - dlts[pos]);
-                }
-                fit_fp16<C>(ds, shift, acck);
-#pragma unroll
-                for (int ks = 0; ks < C::KSTEPS; ++ks) {
-                    const typename C::Frag dsf = frag_from_p<T>(ds, ks);
-                    const typename C::Frag pf = frag_from_p<T>(p, ks);
-#pragma unroll
-                    for (int mb = 0; mb < C::MB; ++mb) {
-                        acck[mb] = C::M::mfma(qt[mb * C::KSTEPS + ks], dsf, acck[mb]);
-                        accv[mb] = C::M::mfma(dt[mb * C::KSTEPS + ks], pf, accv[mb]);
-                    }
-                }
+                dkv_chunk<C>(qa, da, qt, dt, kf, vf, zok, qmask[c], a.scale_log2, lse2s, dlts, wy, wx, c, g, shift,
+                             acck, accv);
             }
         }
+    }
+    if (!kok) return;
+    const int64_t kidx = (int64_t)bg * a.N + krow;
+    float* dk = a.dk + kidx * D;
+    T* dv = reinterpret_cast<T*>(a.dv) + b * a.dvsb + kvh * a.dvsh + (int64_t)krow * a.dvsn;
+    const float out_scale = ldexpf(a.scale, shift);
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int c = 32 * mb + acc_row(r, g);
+            if (c < D) {
+                dk[c] = acck[mb][r] * out_scale;
+                dv[c] = from_f32<T>(accv[mb][r]);
+            }
+        }
+}
+
+// k_local_dkv_grid with the planes copied by the LDS DMA (kBwdPlaneDma types).
+// The (query head, plane) steps of the kv group run as one sequence; a
+// step's lse / Delta are loaded into registers while the step before it is
+// processed and written into its buffer after that.
+template <typename T, int D>
+__global__ __launch_bounds__(64 * kWaves) void k_local_dkv_grid_dma(LbDev a) {
+    typedef Cfg<T, D> C;
+    typedef BwdPlaneDma<C, true> PD;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int* const rowtab = reinterpret_cast<int*>(smem + 2 * PD::BUF);
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5, ki = lane & 31;
+    const int bg = blockIdx.y, b = bg / a.G, kvh = bg % a.G, rep = a.H / a.G;
+    const int brick = xcd_brick(blockIdx.x, gridDim.x);
+    const int Z0 = 4 * (brick / (a.bricks_y * a.bricks_x));
+    const int Y0 = 8 * ((brick / a.bricks_x) % a.bricks_y);
+    const int X0 = 8 * (brick % a.bricks_x);
+    const int nb = wave >> 2, wy = (wave >> 1) & 1, wx = wave & 1;
+    const int ky = (ki >> 2) & 3, kx = ki & 3;
+    const int kz = 2 * nb + (ki >> 4);
+    const int planes = 4 + 2 * a.rz;
+    const int steps = rep * planes;
+    PD::fill_rows(a, Z0, Y0, X0, planes, rowtab);
+    __syncthreads();
+    const int uwave = __builtin_amdgcn_readfirstlane(wave);
+    const int h0 = kvh * rep;
+    // Step i: query head h0 + i / planes, plane i % planes.
+    auto copy_step = [&](int i) __attribute__((always_inline)) {
+        const int hh = i / planes, hz = i - hh * planes;
+        if ((unsigned)(Z0 - a.rz + hz) >= (unsigned)a.Z) return;
+        const int h = h0 + hh;
+        PD::copy(tp<T>(a.q) + b * a.qsb + h * a.qsh, a.qsn, tp<T>(a.dol) + ((int64_t)b * a.H + h) * a.N * D, D,
+                 rowtab + hz * kPlaneKeys, smem + (i & 1) * PD::BUF, uwave, lane);
+    };
+    auto side_step = [&](int i, float& l2, float& dl) __attribute__((always_inline)) {
+        const int hh = i / planes, hz = i - hh * planes;
+        l2 = INFINITY, dl = 0.f;
+        if (tid < kPlaneKeys)
+            plane_side(a, (int64_t)b * a.H + h0 + hh, Z0 - a.rz + hz, Y0, X0, tid, rowtab + hz * kPlaneKeys, l2, dl);
+    };
+    auto side_store = [&](int i, float l2, float dl) __attribute__((always_inline)) {
+        if (tid < kPlaneKeys) {
+            float* side = reinterpret_cast<float*>(smem + (i & 1) * PD::BUF + 2 * PD::REGION);
+            side[tid] = l2;
+            side[kPlaneKeys + tid] = dl;
+        }
+    };
+    {
+        float l2, dl;
+        side_step(0, l2, dl);
+        copy_step(0);
+        side_store(0, l2, dl);
+    }
+
+    const int gz = Z0 + kz, gy = Y0 + 4 * wy + ky, gx = X0 + 4 * wx + kx;
+    const bool kok = gz < a.Z && gy < a.Y && gx < a.X;
+    const int64_t krow = kok ? packed_row(a, gz, gy, gx) : 0;
+    typename C::Frag kf[C::NT], vf[C::NT];
+    row_frags<C>(tp<T>(a.kl) + b * a.ksb + kvh * a.ksh + krow * a.ksn, kok, g, kf);
+    row_frags<C>(tp<T>(a.vl) + b * a.vsb + kvh * a.vsh + krow * a.vsn, kok, g, vf);
+    f32x16 acck[C::MB], accv[C::MB];
+#pragma unroll
+    for (int mb = 0; mb < C::MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acck[mb][r] = accv[mb][r] = 0.f;
+    int shift = 0;
+    const uint32_t qmask[2] = {chunk_mask<C>(a, 0, g, ky, kx, Y0 + 4 * wy, X0 + 4 * wx),
+                               chunk_mask<C>(a, 1, g, ky, kx, Y0 + 4 * wy, X0 + 4 * wx)};
+    for (int i = 0; i < steps; ++i) {
+        const int hz = i % planes;
+        const int pz = Z0 - a.rz + hz;
+        // Step i's copies and side values have landed, and every wave is done
+        // with step i - 1, whose buffer takes step i + 1.
+        dma_wait();
+        __syncthreads();
+        const bool more = i + 1 < steps;
+        float l2n = INFINITY, dln = 0.f;
+        if (more) {
+            side_step(i + 1, l2n, dln);
+            copy_step(i + 1);
+        }
+        if ((unsigned)pz < (unsigned)a.Z && hz >= 2 * nb && hz <= 2 * nb + 1 + 2 * a.rz) {
+            const unsigned char* buf = smem + (i & 1) * PD::BUF;
+            const T* Qb = reinterpret_cast<const T*>(buf);
+            const T* Db = reinterpret_cast<const T*>(buf + PD::REGION);
+            const float* lse2s = reinterpret_cast<const float*>(buf + 2 * PD::REGION);
+            const float* dlts = lse2s + kPlaneKeys;
+            const bool zok = (unsigned)(hz - kz) <= (unsigned)(2 * a.rz);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                if (4 * c >= 4 + 2 * a.ry) continue;
+                const int kap = kperm<C::E, C::KS>(ki);
+                typename C::Frag qa[C::NT], da[C::NT], qt[C::MB * C::KSTEPS], dt[C::MB * C::KSTEPS];
+                load_kfrags<C>(Qb + chunk_pos(wy, wx, c, kap) * C::KSTR + C::E * g, qa);
+                load_kfrags<C>(Db + chunk_pos(wy, wx, c, kap) * C::KSTR + C::E * g, da);
+                PD::tfrags(Qb, wy, wx, c, lane, qt);
+                PD::tfrags(Db, wy, wx, c, lane, dt);
+                dkv_chunk<C>(qa, da, qt, dt, kf, vf, zok, qmask[c], a.scale_log2, lse2s, dlts, wy, wx, c, g, shift,
+                             acck, accv);
+            }
+        }
+        if (more) side_store(i + 1, l2n, dln);
     }
     if (!kok) return;
     const int64_t kidx = (int64_t)bg * a.N + krow;
@@ -414,11 +740,19 @@ size_t lds_dkv_grid() {
 
 template <typename T, int D>
 int launch_t(const LbDev& d, hipStream_t s) {
-    const size_t l1 = lds_dq_grid<T, D>(), l2 = lds_dkv_grid<T, D>();
-    if (l1 > 160 * 1024 || l2 > 160 * 1024) return fail(P3D_EUNSUPPORTED, "p3d_local_bwd_grid: planes exceed LDS");
+    typedef Cfg<T, D> C;
     const int bricks = (int)(cdiv(d.Z, 4) * d.bricks_y * d.bricks_x);
-    k_local_dq_grid<T, D><<<dim3(bricks, d.B * d.H), 64 * kWaves, l1, s>>>(d);
-    k_local_dkv_grid<T, D><<<dim3(bricks, d.B * d.G), 64 * kWaves, l2, s>>>(d);
+    if constexpr (kBwdPlaneDma<C>) {
+        constexpr size_t l1 = BwdPlaneDma<C, false>::BYTES, l2 = BwdPlaneDma<C, true>::BYTES;
+        static_assert(l1 <= 160 * 1024 && l2 <= 160 * 1024, "plane buffers within LDS");
+        k_local_dq_grid_dma<T, D><<<dim3(bricks, d.B * d.H), 64 * kWaves, l1, s>>>(d);
+        k_local_dkv_grid_dma<T, D><<<dim3(bricks, d.B * d.G), 64 * kWaves, l2, s>>>(d);
+    } else {
+        const size_t l1 = lds_dq_grid<T, D>(), l2 = lds_dkv_grid<T, D>();
+        if (l1 > 160 * 1024 || l2 > 160 * 1024) return fail(P3D_EUNSUPPORTED, "p3d_local_bwd_grid: planes exceed LDS");
+        k_local_dq_grid<T, D><<<dim3(bricks, d.B * d.H), 64 * kWaves, l1, s>>>(d);
+        k_local_dkv_grid<T, D><<<dim3(bricks, d.B * d.G), 64 * kWaves, l2, s>>>(d);
+    }
     return P3D_OK;
 }
 

@@ -33,7 +33,7 @@ def _compare(got, exp, dtype, what):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(37, 16, 2, 4, 2, 4, 3), (131, 64, 1, 8, 2, 16, 2), (19, 32, 1, 2, 2, 3, 1),
-                                   (21, 128, 1, 2, 1, 4, 4), (67, 48, 1, 4, 4, 8, 1)])
+                                   (21, 128, 1, 2, 1, 4, 4), (67, 48, 1, 4, 4, 8, 1), (136, 48, 2, 4, 2, 8, 2)])
 def test_every_gradient_custom_graph(gpu, dtype, shape):
     print(f"backward custom {shape} {dtype}", flush=True)
     inputs, nb, blocks, pool = make_case(*shape, dtype=dtype)
@@ -47,6 +47,23 @@ def test_every_gradient_custom_graph(gpu, dtype, shape):
     got = torch.autograd.grad(y, xs, up.to(gpu))
     exp = torch.autograd.grad(e, rs, up)
     _compare(got, exp, dtype, f"custom {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("b,h,n,d", [(1, 1, 8, 8), (2, 3, 136, 48), (1, 4, 64, 128)])
+def test_transpose_rows(gpu, dtype, b, h, n, d):
+    """p3d_transpose_rows (the transposed q / dO_G copies of the summary dK/dV
+    pass) is an exact transpose, also from a token-major strided view."""
+    print(f"transpose_rows b{b} h{h} n{n} d{d} {dtype}", flush=True)
+    from pack3d_amd import _lib
+    x = torch.randn(b, n, h, d, generator=torch.Generator().manual_seed(n + d)).to(gpu, dtype)
+    src = x.permute(0, 2, 1, 3)  # [B, H, N, d] view, row stride H d
+    out = torch.full((b * h * d * n,), float("nan"), dtype=dtype, device=gpu)
+    _lib.call("p3d_transpose_rows", _lib.view(src), out.data_ptr(), b, h, n, d, _lib.DTYPES[dtype],
+              _lib.stream_of(gpu))
+    torch.cuda.synchronize()
+    exp = src.transpose(2, 3).reshape(-1)
+    assert torch.equal(out.view(torch.int16), exp.contiguous().view(torch.int16))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -184,7 +201,7 @@ def _compare_one(name, a, e, dtype):
 from tests.test_gpu_forward import GRIDS  # noqa: E402
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("shape,block,radius,kind,heads,kv_heads,d", GRIDS)
 def test_every_gradient_grid_shapes(gpu, dtype, shape, block, radius, kind, heads, kv_heads, d):
     """Complete-grid layouts of every radius pattern and partial bricks (the

@@ -75,6 +75,12 @@ def test_entry_points_reject_bad_arguments_before_launch():
             _lib.call("p3d_weight_grad", 16, out_f, 16, in_f, 16, 16, 100, out_f, in_f, 1, bf16, None)
     with pytest.raises(RuntimeError, match="null pointer"):
         _lib.call("p3d_weight_grad", None, 8, 16, 32, 16, 16, 100, 8, 32, 1, bf16, None)
+    # Transposed copies: 16-bit types and token counts a multiple of 8 only.
+    src = _lib.View(16, 0, 0, 64)
+    for n, d, dt, msg in ((12, 64, bf16, "multiple of 8"), (16, 64, _lib.P3D_F32, "fp16 or bf16"),
+                          (16, 12, bf16, "head_dim")):
+        with pytest.raises(RuntimeError, match=msg):
+            _lib.call("p3d_transpose_rows", src, 16, 1, 1, n, d, dt, None)
 
 
 def test_import_without_gpu_and_no_oracle_import():

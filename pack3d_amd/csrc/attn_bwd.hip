@@ -316,47 +316,100 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_global_dq(BwdDev a) {
     zero_padding_rows<C>(lds + S::SIZE + 2 * SK * C::KSTR, S::TGS, SK);
     const DqDma<C, SK> dma;
     dma.copy(a, bg, 0, lds);
+
+    // The wave's reference point m = the largest lse (log2 units) of its live
+    // queries.  The score MFMAs start from -m (one 16-register accumulator
+    // for both blocks), so 2^(s - m) <= 1, lse bounding every score of its
+    // query, and P = 2^(s - m) c with c = 2^(m - lse) per query, which folds
+    // into dP - Delta as one fma: dS = 2^(s - m) (c dP - c Delta), two VALU
+    // operations and an exponential per score instead of three and one.
+    // When a live query's lse lies more than 64 below m, terms that matter
+    // could underflow, and the wave takes the per-query path instead.
+    // Only 16-bit types up to head_dim 48 have the registers for both paths
+    // (wider ones and fp32 keep the per-query path, which already fills them).
+    constexpr bool kFast = sizeof(T) == 2 && D <= 48;
+    float mw = 0.f, cq[2] = {0.f, 0.f}, cd[2] = {0.f, 0.f};
+    bool fast = false;
+    if constexpr (kFast) {
+        mw = -INFINITY;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+            if (qok[nb]) mw = fmaxf(mw, lse2[nb]);
+        mw = wave_max(mw);
+        if (mw == -INFINITY) mw = 0.f;  // no live query in the wave
+        bool spread = false;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) spread |= qok[nb] && mw - lse2[nb] > 64.f;
+        fast = __builtin_amdgcn_ballot_w64(spread) == 0;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            cq[nb] = qok[nb] ? __builtin_amdgcn_exp2f(mw - lse2[nb]) : 0.f;
+            cd[nb] = -cq[nb] * delta[nb];
+        }
+    }
     dma_wait();
     __syncthreads();
-    int buf = 0;
-    for (int base = 0; base < a.M; base += SK) {
-        const int next = base + SK;
-        // The other buffer held the previous stage, which every wave finished
-        // before the last barrier.
-        if (next < a.M) dma.copy(a, bg, next, lds + (buf ^ 1) * S::SIZE);
-        const T* cur = lds + buf * S::SIZE;
+
+    // The stage loop, with dS formed as described above (FAST) or per query.
+    auto sweep = [&](auto mode) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(mode)::value;
+        f32x16 minit;
 #pragma unroll
-        for (int tt = 0; tt < SK / 32; ++tt) {
-            const int first = base + 32 * tt;
-            if (first >= a.M) break;
-            typename C::Frag kf[C::NT], vf[C::NT], tf[C::MB * C::KSTEPS];
-            load_kfrags<C>(cur + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, kf);
-            load_kfrags<C>(cur + SK * C::KSTR + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, vf);
-            load_vfrags<C, true>(cur + 2 * SK * C::KSTR, S::TGS, 32 * tt, lane, tf);
+        for (int r = 0; r < 16; ++r) minit[r] = -mw;
+        int buf = 0;
+        for (int base = 0; base < a.M; base += SK) {
+            const int next = base + SK;
+            // The other buffer held the previous stage, which every wave finished
+            // before the last barrier.
+            if (next < a.M) dma.copy(a, bg, next, lds + (buf ^ 1) * S::SIZE);
+            const T* cur = lds + buf * S::SIZE;
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb) {
-                const f32x16 s = score_tile<C>(kf, qf[nb]);
-                const f32x16 dp = score_tile<C>(vf, df[nb]);
-                float ds[16];
+            for (int tt = 0; tt < SK / 32; ++tt) {
+                const int first = base + 32 * tt;
+                if (first >= a.M) break;
+                typename C::Frag kf[C::NT], vf[C::NT], tf[C::MB * C::KSTEPS];
+                load_kfrags<C>(cur + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, kf);
+                load_kfrags<C>(cur + SK * C::KSTR + (32 * tt + kperm<C::E, C::KS>(qi)) * C::KSTR + C::E * g, vf);
+                load_vfrags<C, true>(cur + 2 * SK * C::KSTR, S::TGS, 32 * tt, lane, tf);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) ds[r] = __builtin_amdgcn_exp2f(s[r] - lse2[nb]) * (dp[r] - delta[nb]);
-                if (first + 32 > a.M) {  // the last tile: summaries past M contribute nothing
+                for (int nb = 0; nb < 2; ++nb) {
+                    f32x16 s;
+                    if constexpr (FAST)
+                        s = score_tile<C>(kf, qf[nb], minit);
+                    else
+                        s = score_tile<C>(kf, qf[nb]);
+                    const f32x16 dp = score_tile<C>(vf, df[nb]);
+                    float ds[16];
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        if (first + kperm<C::E, C::KS>(acc_row(r, g)) >= a.M) ds[r] = 0.f;
-                }
+                    for (int r = 0; r < 16; ++r) {
+                        if constexpr (FAST)
+                            ds[r] = __builtin_amdgcn_exp2f(s[r]) * fmaf(dp[r], cq[nb], cd[nb]);
+                        else
+                            ds[r] = __builtin_amdgcn_exp2f(s[r] - lse2[nb]) * (dp[r] - delta[nb]);
+                    }
+                    if (first + 32 > a.M) {  // the last tile: summaries past M contribute nothing
 #pragma unroll
-                for (int ks = 0; ks < C::KSTEPS; ++ks) {
-                    const typename C::Frag pf = frag_from_p<T>(ds, ks);
+                        for (int r = 0; r < 16; ++r)
+                            if (first + kperm<C::E, C::KS>(acc_row(r, g)) >= a.M) ds[r] = 0.f;
+                    }
 #pragma unroll
-                    for (int mb = 0; mb < C::MB; ++mb)
-                        acc[nb][mb] = C::M::mfma(tf[mb * C::KSTEPS + ks], pf, acc[nb][mb]);
+                    for (int ks = 0; ks < C::KSTEPS; ++ks) {
+                        const typename C::Frag pf = frag_from_p<T>(ds, ks);
+#pragma unroll
+                        for (int mb = 0; mb < C::MB; ++mb)
+                            acc[nb][mb] = C::M::mfma(tf[mb * C::KSTEPS + ks], pf, acc[nb][mb]);
+                    }
                 }
             }
+            dma_wait();
+            __syncthreads();
+            buf ^= 1;
         }
-        dma_wait();
-        __syncthreads();
-        buf ^= 1;
+    };
+    if (kFast && fast) {
+        if constexpr (kFast) sweep(std::true_type{});
+    } else {
+        sweep(std::false_type{});
     }
     // One summary: P = 1 and dS = 0 exactly (kernels.py:198-199), so dQ_G = 0.
     const float out_scale = a.M > 1 ? kLn2 : 0.f;

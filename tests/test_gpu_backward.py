@@ -88,6 +88,35 @@ def test_every_gradient_grid_rope_fused(gpu, dtype, kind, kv_heads):
     _compare(got, exp, dtype, f"grid {kind}")
 
 
+@pytest.mark.parametrize("spread", [False, True])
+def test_summary_dq_reference_point_paths(gpu, spread):
+    """The summary dQ pass forms dS against one reference point per wave (the
+    largest lse of its 64 queries) unless a query's lse lies more than 64
+    log2 units below it.  spread=True scales the first query of every wave
+    by 200, which puts its summary lse 35-97 log2 units above the rest of
+    the wave (computed with the oracle's pooling): some waves take the
+    per-query path, the others the reference point near its limit.  Every
+    gradient against the oracle."""
+    dtype = torch.bfloat16
+    print(f"backward dq reference point spread={spread}", flush=True)
+    inputs, nb, blocks, pool = make_case(n=256, d=48, b=1, h=2, g=1, volume=8, pool=1, dtype=torch.float32, seed=7)
+    if spread:
+        q = inputs[0].clone()
+        q[:, :, ::64] *= 200.0
+        inputs = (q,) + tuple(inputs[1:])
+    inputs = tuple(t.to(dtype) for t in inputs)
+    og = ref.prepare_geometry(nb, blocks, pool)
+    hg = p3d.prepare_geometry(nb.to(gpu), blocks.to(gpu), pool)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    rs = [t.detach().clone().requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, hg, temperature=0.7)
+    e = ref.pack3d_reference(*rs, og, temperature=0.7)
+    up = torch.randn(e.shape, generator=torch.Generator().manual_seed(3)).to(dtype)
+    got = torch.autograd.grad(y, xs, up.to(gpu))
+    exp = torch.autograd.grad(e, rs, up)
+    _compare(got, exp, dtype, f"dq reference point spread={spread}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_singleton_summary_has_no_query_or_key_gradient(gpu, dtype):
     """One token, one summary: the local row is empty and attention to a single

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 16
+#define P3D_ABI_VERSION 17
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -330,6 +330,20 @@ int p3d_out_residual(const void* y, const void* wo, const void* x, void* out, in
  * batch < 65536. */
 int p3d_copy_rows(p3d_view src, p3d_view dst, int64_t batch, int32_t heads, int64_t tokens, int32_t head_dim,
                   int32_t dtype, void* stream);
+
+/* Input gradient of the layer's three input projections in 16-bit training
+ * (the backward of attention.py:64-67,85 with respect to the normalised
+ * tokens; torch's autograd computes it as three products dq Wq, dkv Wkv,
+ * dgl Wg and adds them): dx = dq Wq + dkv Wkv + dg Wg as one contraction over
+ * the concatenated features, summed in fp32 and rounded once to dtype.
+ * dq [rows, q_out], dkv [rows, kv_out], dg [rows, g_out] with row strides in
+ * elements (multiples of 8, 16-byte aligned rows); wt = [Wq; Wkv; Wg]^T as a
+ * contiguous [dim][k_pad] matrix whose columns past q_out + kv_out + g_out
+ * are zero, k_pad a multiple of 64; dx [rows, dim] contiguous.  q_out, kv_out,
+ * g_out positive multiples of 8; dim 64, 96, 128, 192 or 256; fp16 / bf16. */
+int p3d_input_grad(const void* dq, int64_t dq_stride, int32_t q_out, const void* dkv, int64_t dkv_stride,
+                   int32_t kv_out, const void* dg, int64_t dg_stride, int32_t g_out, const void* wt, int32_t k_pad,
+                   void* dx, int64_t rows, int32_t dim, int32_t dtype, void* stream);
 
 /* Weight gradient of a linear map y = x W^T (the W part of the backward of
  * the layer's to_q, to_kv, gate and to_out nn.Linear maps, attention.py:64-67,

@@ -46,6 +46,33 @@ def weight_grad_supported(out_features, in_features):
     return out_features >= 8 and out_features % 8 == 0 and in_features % 32 == 0 and 32 <= in_features <= 256
 
 
+INPUT_GRAD_DIMS = (64, 96, 128, 192, 256)
+
+
+def input_grad(dys, ws):
+    """dq Wq + dkv Wkv + dgl Wg for the three 16-bit gradients dys [rows, *]
+    and the weights ws [*, dim] of the same type, as one contraction summed in
+    fp32 (``p3d_input_grad``); None where the kernel does not take the shapes
+    (the caller then runs the three products)."""
+    if any(dy is None for dy in dys):
+        return None
+    dt, rows, dim = ws[0].dtype, dys[0].shape[0], ws[0].shape[1]
+    outs = [w.shape[0] for w in ws]
+    if (dt not in (torch.float16, torch.bfloat16) or dim not in INPUT_GRAD_DIMS or any(o % 8 for o in outs)
+            or any(dy.dtype != dt or dy.shape != (rows, o) or dy.stride(1) != 1 or dy.stride(0) % 8
+                   or dy.data_ptr() % 16 for dy, o in zip(dys, outs))):
+        return None
+    k = sum(outs)
+    k_pad = -(-k // 64) * 64
+    wt = torch.zeros(dim, k_pad, dtype=dt, device=ws[0].device)
+    wt[:, :k] = torch.cat(ws, 0).t()
+    dx = torch.empty(rows, dim, dtype=dt, device=ws[0].device)
+    _lib.call("p3d_input_grad", dys[0].data_ptr(), dys[0].stride(0), outs[0], dys[1].data_ptr(), dys[1].stride(0),
+              outs[1], dys[2].data_ptr(), dys[2].stride(0), outs[2], wt.data_ptr(), k_pad, dx.data_ptr(), rows, dim,
+              _lib.DTYPES[dt], _lib.stream_of(dx.device))
+    return dx
+
+
 def weight_grad(dy, x):
     """dW = dy^T x in fp32 for dy [rows, out], x [rows, in] of one 16-bit type
     (``p3d_weight_grad``; torch's product in fp32 where the kernel does not
@@ -167,18 +194,22 @@ class InputProjections(torch.autograd.Function):
         # products are summed in fp32 as autograd would; for a 16-bit x the
         # GEMMs accumulate into one buffer of that type.
         wide = x_dt == torch.float32
-        dx = torch.zeros(x16.shape, dtype=torch.float32, device=x16.device) if wide else None
+        dys = [None if dy is None else _rows(dy).to(x16.dtype) for dy in (dq, dkv, dgl)]
+        # One kernel for the three products where it takes the shapes (16-bit x).
+        dx = None if wide else input_grad(dys, (wq, wkv, wg))
+        fused = dx is not None
+        if wide:
+            dx = torch.zeros(x16.shape, dtype=torch.float32, device=x16.device)
         grads = []
-        for dy, w, w_dt in ((dq, wq, wq_dt), (dkv, wkv, wkv_dt), (dgl, wg, wg_dt)):
+        for dy, w, w_dt in zip(dys, (wq, wkv, wg), (wq_dt, wkv_dt, wg_dt)):
             if dy is None:
                 grads.append(None)
                 continue
-            dy = _rows(dy).to(x16.dtype)
             if wide:
                 dx.add_(torch.mm(dy, w))
             elif dx is None:
                 dx = torch.mm(dy, w)
-            else:
+            elif not fused:
                 dx.addmm_(dy, w)  # in place: no copy of dx into a new result
             grads.append(weight_grad(dy, x16).to(w_dt))
         if dx is None:

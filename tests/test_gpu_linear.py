@@ -44,6 +44,49 @@ def test_weight_grad_matches_fp32_product(gpu, dtype, rows, out_f, in_f, splits)
     assert err < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,dim,outs", [(37, 192, (192, 768, 8)), (1000, 64, (64, 256, 16)),
+                                           (4099, 96, (96, 384, 8)), (5000, 128, (128, 512, 8)),
+                                           (3001, 256, (256, 1024, 8)), (262144, 192, (192, 768, 8))])
+def test_input_grad_matches_fp32_products(gpu, dtype, rows, dim, outs):
+    """p3d_input_grad (dq Wq + dkv Wkv + dg Wg as one contraction) against
+    the three products in fp32 on the same 16-bit inputs: one rounding of the
+    fp32 sum, so every element within half a unit in the last place of the
+    16-bit type plus the fp32 summation-order slack.  dq and dkv are column
+    ranges of one wider buffer (row strides past the rows, as the layer's
+    gradient layout can give); ragged row counts; every supported width and
+    the c4 shape."""
+    print(f"input grad {rows}x{dim} {outs} {dtype}", flush=True)
+    gen = torch.Generator(device=gpu).manual_seed(rows + dim)
+    qo, kvo, go = outs
+    wide = torch.randn(rows, qo + kvo + 16, device=gpu, generator=gen).to(dtype)
+    dq, dkv = wide[:, :qo], wide[:, qo:qo + kvo]
+    dg = torch.randn(rows, go, device=gpu, generator=gen).to(dtype)
+    ws = [(torch.randn(o, dim, device=gpu, generator=gen) / math.sqrt(dim)).to(dtype) for o in outs]
+    got = linear.input_grad([dq, dkv, dg], ws)
+    assert got is not None and got.dtype == dtype and got.shape == (rows, dim)
+    ref = sum(torch.mm(a.float(), w.float()) for a, w in zip((dq, dkv, dg), ws))
+    scale = sum(torch.mm(a.float().abs(), w.float().abs()) for a, w in zip((dq, dkv, dg), ws))
+    ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    excess = ((got.float() - ref).abs() - ulp * ref.abs() - 1e-5 * scale).max().item()
+    print(f"  excess={excess:.3g}", flush=True)
+    assert excess <= 0
+
+
+def test_input_grad_declines_unsupported_shapes(gpu):
+    """Widths and feature counts the kernel does not take go back to the
+    three products (None), and the kernel rejects them before launching."""
+    dt = torch.bfloat16
+    dys = [torch.zeros(64, o, device=gpu, dtype=dt) for o in (48, 192, 8)]
+    ws = [torch.zeros(o, 48, device=gpu, dtype=dt) for o in (48, 192, 8)]
+    assert linear.input_grad(dys, ws) is None  # dim 48
+    dys = [torch.zeros(64, o, device=gpu, dtype=dt) for o in (64, 256, 4)]
+    ws = [torch.zeros(o, 64, device=gpu, dtype=dt) for o in (64, 256, 4)]
+    assert linear.input_grad(dys, ws) is None  # 4 gate features
+    with pytest.raises(RuntimeError, match="dim must be"):
+        _lib.call("p3d_input_grad", 16, 64, 64, 16, 256, 256, 16, 8, 8, 16, 384, 16, 64, 48, _lib.DTYPES[dt], None)
+
+
 def test_weight_grad_strided_rows_and_determinism(gpu):
     """Row strides wider than the rows (column slices of wider tensors, as the
     layer's projections are) and bit-identical repeats."""

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 17
+#define P3D_ABI_VERSION 18
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -358,6 +358,16 @@ int p3d_input_grad(const void* dq, int64_t dq_stride, int32_t q_out, const void*
 int p3d_weight_grad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float* dw, float* workspace,
                     int64_t rows, int32_t out_features, int32_t in_features, int32_t splits, int32_t dtype,
                     void* stream);
+
+/* p3d_weight_grad of three linear maps that share their input x (the
+ * layer's to_q, to_kv and gate, attention.py:64-67,85) in one pass over x:
+ * dw [out0 + out1 + out2, in_features] fp32 holds dW of dy0, then of dy1,
+ * then of dy2, each dy with its own row stride.  Same rules as
+ * p3d_weight_grad; the out counts positive multiples of 8. */
+int p3d_weight_grad3(const void* dy0, int64_t ld0, int32_t out0, const void* dy1, int64_t ld1, int32_t out1,
+                     const void* dy2, int64_t ld2, int32_t out2, const void* x, int64_t ldx, float* dw,
+                     float* workspace, int64_t rows, int32_t in_features, int32_t splits, int32_t dtype,
+                     void* stream);
 
 /* ---- backward (replaces kernels.py:313-356, autograd.py:19-28) --------- */
 

@@ -25,7 +25,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 17  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 18  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -109,6 +109,8 @@ SIGNATURES = {
     "p3d_copy_rows": ([View, View, c_int64, c_int32, c_int64, c_int32, c_int32, _P], c_int32),
     "p3d_input_grad": ([_P, c_int64, c_int32, _P, c_int64, c_int32, _P, c_int64, c_int32, _P, c_int32, _P, c_int64,
                         c_int32, c_int32, _P], c_int32),
+    "p3d_weight_grad3": ([_P, c_int64, c_int32, _P, c_int64, c_int32, _P, c_int64, c_int32, _P, c_int64, _P, _P,
+                          c_int64, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_weight_grad": ([_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_mix_bwd": ([ctypes.POINTER(BwdArgs), _P], c_int32),
     "p3d_local_bwd_indexed": ([ctypes.POINTER(BwdArgs), _P, c_int32, _P, c_int32, _P], c_int32),

@@ -55,12 +55,22 @@ __device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* tile, int stri
 template <int IT>
 constexpr int wgrad_stage_elems() { return kWgTok * (tile_stride(kWgRows) + tile_stride(32 * IT)); }
 
+// dy as up to three column blocks of output rows: rows [0, end[0]) from
+// src[0], [end[0], end[1]) from src[1], [end[1], O) from src[2], each with its
+// own row stride (a single dy has end[0] = end[1] = O).
+template <typename T>
+struct WgSrc {
+    const T* src[3];
+    int64_t ld[3];
+    int end[2];
+};
+
 // Partial dW of token range [blockIdx.y * per, + per) for output rows
 // [blockIdx.x * 256, + 256), written to part[blockIdx.y][o][i].  Two stages
 // of dynamic LDS (2 * wgrad_stage_elems<IT>() elements).
 template <typename T, int IT>
-__global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(const T* dy, int64_t ldy, const T* x, int64_t ldx,
-                                                        float* part, int64_t rows, int O, int64_t per) {
+__global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x, int64_t ldx, float* part,
+                                                        int64_t rows, int O, int64_t per) {
     typedef Mma<T> M;
     constexpr int I = 32 * IT;
     constexpr int SA = tile_stride(kWgRows), SB = tile_stride(I);
@@ -82,8 +92,11 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(const T* dy, int64_t ld
         for (int i = 0; i < PA; ++i) {
             const int p = tid + i * 64 * kWgWaves, r = p / (kWgRows / 8), c = (p % (kWgRows / 8)) * 8;
             const int64_t n = t0 + r;
+            const int o = ob + c;  // 8 rows of one source (the blocks are multiples of 8)
+            const int sel = o < dy.end[0] ? 0 : (o < dy.end[1] ? 1 : 2);
+            const int o_src = o - (sel == 0 ? 0 : dy.end[sel - 1]);
             ra[i] = u32x4{0, 0, 0, 0};
-            if (n < n1 && ob + c < O) ra[i] = *reinterpret_cast<const u32x4*>(dy + n * ldy + ob + c);
+            if (n < n1 && o < O) ra[i] = *reinterpret_cast<const u32x4*>(dy.src[sel] + n * dy.ld[sel] + o_src);
         }
 #pragma unroll
         for (int i = 0; i < PB; ++i) {
@@ -170,8 +183,8 @@ __global__ __launch_bounds__(kRedElems * kRedGroups) void k_wgrad_reduce(const f
 }
 
 template <typename T>
-int launch_wgrad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float* dw, float* part, int64_t rows, int O,
-                 int I, int splits, hipStream_t s) {
+int launch_wgrad(const WgSrc<T>& dy, const void* x, int64_t ldx, float* dw, float* part, int64_t rows, int O, int I,
+                 int splits, hipStream_t s) {
     const int64_t per = cdiv(cdiv(rows, splits), kWgTok) * kWgTok;
     const int used = (int)cdiv(rows, per);
     const dim3 grid((unsigned)cdiv(O, kWgRows), (unsigned)used);
@@ -179,7 +192,7 @@ int launch_wgrad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float*
 #define CASE(IT)                                                                                                  \
     case IT:                                                                                                      \
         k_wgrad<T, IT><<<grid, 64 * kWgWaves, 2 * wgrad_stage_elems<IT>() * sizeof(T), s>>>(                      \
-            (const T*)dy, ldy, (const T*)x, ldx, part, rows, O, per);                                             \
+            dy, (const T*)x, ldx, part, rows, O, per);                                                            \
         break;
         CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
 #undef CASE
@@ -208,8 +221,41 @@ extern "C" int p3d_weight_grad(const void* dy, int64_t ldy, const void* x, int64
                 "row strides must cover the rows and keep 16-byte alignment");
     P3D_REQUIRE(aligned16(dy) && aligned16(x), "dy and x must be 16-byte aligned");
     P3D_REQUIRE(cdiv(out_features, kWgRows) < 65536 && splits < 65536, "grid too large");
-    return dtype == P3D_F16 ? launch_wgrad<_Float16>(dy, ldy, x, ldx, dw, workspace, rows, out_features, in_features,
-                                                     splits, as_stream(stream))
-                            : launch_wgrad<__bf16>(dy, ldy, x, ldx, dw, workspace, rows, out_features, in_features,
-                                                   splits, as_stream(stream));
+    if (dtype == P3D_F16) {
+        const WgSrc<_Float16> src{{(const _Float16*)dy, nullptr, nullptr}, {ldy, 0, 0}, {out_features, out_features}};
+        return launch_wgrad<_Float16>(src, x, ldx, dw, workspace, rows, out_features, in_features, splits,
+                                      as_stream(stream));
+    }
+    const WgSrc<__bf16> src{{(const __bf16*)dy, nullptr, nullptr}, {ldy, 0, 0}, {out_features, out_features}};
+    return launch_wgrad<__bf16>(src, x, ldx, dw, workspace, rows, out_features, in_features, splits,
+                                as_stream(stream));
+}
+
+extern "C" int p3d_weight_grad3(const void* dy0, int64_t ld0, int32_t out0, const void* dy1, int64_t ld1,
+                                int32_t out1, const void* dy2, int64_t ld2, int32_t out2, const void* x, int64_t ldx,
+                                float* dw, float* workspace, int64_t rows, int32_t in_features, int32_t splits,
+                                int32_t dtype, void* stream) {
+    P3D_REQUIRE(dy0 && dy1 && dy2 && x && dw && workspace, "null pointer argument");
+    P3D_REQUIRE(dtype == P3D_F16 || dtype == P3D_BF16, "dtype must be fp16 or bf16");
+    P3D_REQUIRE(rows >= 1 && splits >= 1, "need at least one row and one split");
+    P3D_REQUIRE(out0 >= 8 && out1 >= 8 && out2 >= 8 && out0 % 8 == 0 && out1 % 8 == 0 && out2 % 8 == 0 &&
+                    (int64_t)out0 + out1 + out2 < (1 << 24),
+                "out features must be positive multiples of 8");
+    P3D_REQUIRE(in_features >= 32 && in_features % 32 == 0 && in_features <= 256,
+                "in_features must be a multiple of 32, at most 256");
+    P3D_REQUIRE(ld0 >= out0 && ld1 >= out1 && ld2 >= out2 && ld0 % 8 == 0 && ld1 % 8 == 0 && ld2 % 8 == 0 &&
+                    ldx >= in_features && ldx % 8 == 0,
+                "row strides must cover the rows and keep 16-byte alignment");
+    P3D_REQUIRE(aligned16(dy0) && aligned16(dy1) && aligned16(dy2) && aligned16(x), "dy and x must be 16-byte aligned");
+    const int O = out0 + out1 + out2;
+    P3D_REQUIRE(cdiv(O, kWgRows) < 65536 && splits < 65536, "grid too large");
+    if (dtype == P3D_F16) {
+        const WgSrc<_Float16> src{{(const _Float16*)dy0, (const _Float16*)dy1, (const _Float16*)dy2},
+                                  {ld0, ld1, ld2},
+                                  {out0, out0 + out1}};
+        return launch_wgrad<_Float16>(src, x, ldx, dw, workspace, rows, O, in_features, splits, as_stream(stream));
+    }
+    const WgSrc<__bf16> src{{(const __bf16*)dy0, (const __bf16*)dy1, (const __bf16*)dy2}, {ld0, ld1, ld2},
+                            {out0, out0 + out1}};
+    return launch_wgrad<__bf16>(src, x, ldx, dw, workspace, rows, O, in_features, splits, as_stream(stream));
 }

@@ -94,6 +94,29 @@ def weight_grad(dy, x):
     return dw
 
 
+def weight_grads3(dys, x):
+    """dW of three linear maps sharing the input x: [dy0^T x; dy1^T x;
+    dy2^T x] in fp32 from one pass over x (``p3d_weight_grad3``), as three
+    tensors; None where the kernel does not take the shapes (the caller
+    then takes them one at a time)."""
+    rows, in_f = x.shape
+    outs = [dy.shape[1] for dy in dys]
+    dt = x.dtype
+    if (dt not in (torch.float16, torch.bfloat16) or not all(weight_grad_supported(o, in_f) for o in outs)
+            or x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16
+            or any(dy.dtype != dt or dy.shape[0] != rows or dy.stride(1) != 1 or dy.stride(0) % 8
+                   or dy.data_ptr() % 16 for dy in dys)):
+        return None
+    total = sum(outs)
+    splits = splits_for(rows, total)
+    dw = torch.empty(total, in_f, dtype=torch.float32, device=x.device)
+    work = torch.empty(splits, total, in_f, dtype=torch.float32, device=x.device)
+    _lib.call("p3d_weight_grad3", dys[0].data_ptr(), dys[0].stride(0), outs[0], dys[1].data_ptr(), dys[1].stride(0),
+              outs[1], dys[2].data_ptr(), dys[2].stride(0), outs[2], x.data_ptr(), x.stride(0), dw.data_ptr(),
+              work.data_ptr(), rows, in_f, splits, _lib.DTYPES[dt], _lib.stream_of(x.device))
+    return torch.split(dw, outs, 0)
+
+
 def _rows(t):
     return t.reshape(-1, t.shape[-1])
 
@@ -200,8 +223,10 @@ class InputProjections(torch.autograd.Function):
         fused = dx is not None
         if wide:
             dx = torch.zeros(x16.shape, dtype=torch.float32, device=x16.device)
+        # The three weight gradients from one pass over x16 where the kernel takes them.
+        dws = None if any(dy is None for dy in dys) else weight_grads3(dys, x16)
         grads = []
-        for dy, w, w_dt in zip(dys, (wq, wkv, wg), (wq_dt, wkv_dt, wg_dt)):
+        for i, (dy, w, w_dt) in enumerate(zip(dys, (wq, wkv, wg), (wq_dt, wkv_dt, wg_dt))):
             if dy is None:
                 grads.append(None)
                 continue
@@ -211,7 +236,7 @@ class InputProjections(torch.autograd.Function):
                 dx = torch.mm(dy, w)
             elif not fused:
                 dx.addmm_(dy, w)  # in place: no copy of dx into a new result
-            grads.append(weight_grad(dy, x16).to(w_dt))
+            grads.append((weight_grad(dy, x16) if dws is None else dws[i]).to(w_dt))
         if dx is None:
             dx = torch.zeros(x16.shape, dtype=x16.dtype, device=x16.device)
         dbg = None if dgl is None else _rows(dgl).float().sum(0).to(bg_dt)

@@ -87,6 +87,28 @@ def test_input_grad_declines_unsupported_shapes(gpu):
         _lib.call("p3d_input_grad", 16, 64, 64, 16, 256, 256, 16, 8, 8, 16, 384, 16, 64, 48, _lib.DTYPES[dt], None)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,in_f,outs", [(37, 192, (192, 768, 8)), (4099, 96, (96, 384, 8)),
+                                            (262144, 192, (192, 768, 8))])
+def test_weight_grads3_match_fp32_products(gpu, dtype, rows, in_f, outs):
+    """p3d_weight_grad3 (three dW sharing x from one pass) against the fp32
+    products dy^T x of the same 16-bit inputs; two of the dy are column
+    ranges of one wider buffer (row strides past the rows, a gap between
+    them), the third a separate tensor; ragged and c4 row counts."""
+    print(f"weight grads3 {rows}x{in_f} {outs} {dtype}", flush=True)
+    gen = torch.Generator(device=gpu).manual_seed(rows + in_f)
+    qo, kvo, go = outs
+    wide = torch.randn(rows, qo + kvo + 24, device=gpu, generator=gen).to(dtype)
+    dys = [wide[:, :qo], wide[:, qo + 8:qo + 8 + kvo], torch.randn(rows, go, device=gpu, generator=gen).to(dtype)]
+    x = torch.randn(rows, in_f, device=gpu, generator=gen).to(dtype)
+    got = linear.weight_grads3(dys, x)
+    assert got is not None
+    for dy, dw in zip(dys, got):
+        err = rel_l2(dw, _reference(dy, x))
+        print(f"  rel_l2={err:.3g}", flush=True)
+        assert err < 1e-5
+
+
 def test_weight_grad_strided_rows_and_determinism(gpu):
     """Row strides wider than the rows (column slices of wider tensors, as the
     layer's projections are) and bit-identical repeats."""
@@ -141,7 +163,10 @@ def test_layer_training_gradients_match_torch_linear(gpu, dtype):
         y_h, dx_h, g_h = run(True)
     finally:
         linear._lib.call = real
-    assert calls.count("p3d_weight_grad") == 4, calls
+    # to_out's weight gradient alone; to_q / to_kv / gate share one pass over
+    # the tokens, and their input gradients one contraction.
+    assert calls.count("p3d_weight_grad") == 1 and calls.count("p3d_weight_grad3") == 1, calls
+    assert calls.count("p3d_input_grad") == 1, calls
     y_t, dx_t, g_t = run(False)
     assert rel_l2(y_h, y_t) < 1e-2
     assert rel_l2(dx_h, dx_t) < 1e-2

@@ -703,10 +703,29 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
         if (count > 0) {
             const float inv = 1.f / (float)count;
             for (int c = lane; c < D; c += 64) {
+                // The split partials in groups of 8 loads issued together, then
+                // added in split order (the same sums as one at a time, without
+                // a memory round trip per split).
+                const float* pk = bd.dsk_part + (bg * a.Mp + m) * D + c;
+                const float* pv = bd.dsv_part + (bg * a.Mp + m) * D + c;
                 float sk = 0.f, sv = 0.f;
-                for (int sp = 0; sp < bd.splits; ++sp) {
-                    sk += bd.dsk_part[sp * slice + (bg * a.Mp + m) * D + c];
-                    sv += bd.dsv_part[sp * slice + (bg * a.Mp + m) * D + c];
+                int sp = 0;
+                for (; sp + 8 <= bd.splits; sp += 8) {
+                    float k8[8], v8[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        k8[i] = pk[(sp + i) * slice];
+                        v8[i] = pv[(sp + i) * slice];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        sk += k8[i];
+                        sv += v8[i];
+                    }
+                }
+                for (; sp < bd.splits; ++sp) {
+                    sk += pk[sp * slice];
+                    sv += pv[sp * slice];
                 }
                 gk[c] = sk * inv;
                 gv[c] = sv * inv;

@@ -178,13 +178,18 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     const __amdgpu_buffer_rsrc_t qrsrc = buffer_rsrc(reinterpret_cast<T*>(a.q) + tok0 * a.q_out, qbytes);
     const __amdgpu_buffer_rsrc_t kvrsrc = buffer_rsrc(reinterpret_cast<T*>(a.kv) + tok0 * a.kv_out, kvbytes);
     settle_loads(wreg, xf);
-    for (int ob = 0; ob < nblocks; ++ob) {
+    // The GEMM of block ob into one accumulator set.
+    auto gemm = [&](int ob) __attribute__((always_inline)) -> f32x16 {
         const T* wb = &wbuf[ob & 1][t * WS + 8 * g];
         f32x16 d;
 #pragma unroll
         for (int r = 0; r < 16; ++r) d[r] = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) d = M::mfma(*reinterpret_cast<const Frag*>(wb + 16 * ks), xf[ks], d);
+        return d;
+    };
+    // The outputs of block ob from its accumulators.
+    auto epilogue = [&](int ob, const f32x16& d) __attribute__((always_inline)) {
         {
             // q / kv outputs of the block through the tile: row t, columns
             // acc_row(4 qd, g) .. +3, then 16-byte pieces (token tt, outputs
@@ -231,11 +236,44 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
                 }
             }
         }
-        // Unconditional (a stage after the last block fills a buffer no
-        // block reads), so that every block issues the same loads.
+    };
+    // Unconditional (a stage after the last block fills a buffer no block
+    // reads), so that every block issues the same loads.
+    auto advance = [&](int ob) __attribute__((always_inline)) {
         stage((ob + 1) & 1);
         fetch(min(ob + 2, nblocks - 1));
         __syncthreads();
+    };
+    if constexpr (KS != 12 && KS != 16) {
+        // One block at a time (the second accumulator set below would spill
+        // at these widths).
+        for (int ob = 0; ob < nblocks; ++ob) {
+            epilogue(ob, gemm(ob));
+            advance(ob);
+        }
+        return;
+    }
+    // Software-pipelined by one block: block ob's MFMAs are issued before
+    // block ob - 1's epilogue, which then runs under them.  The staged
+    // weights of block ob + 1 go into the buffer block ob - 1 read, whose
+    // readers all passed the barrier that ended the step before.
+    f32x16 d0 = gemm(0), d1;
+    advance(0);
+    int ob = 1;
+    for (; ob + 1 < nblocks; ob += 2) {
+        d1 = gemm(ob);
+        epilogue(ob - 1, d0);
+        advance(ob);
+        d0 = gemm(ob + 1);
+        epilogue(ob, d1);
+        advance(ob + 1);
+    }
+    if (ob < nblocks) {
+        d1 = gemm(ob);
+        epilogue(ob - 1, d0);
+        epilogue(ob, d1);
+    } else {
+        epilogue(ob - 1, d0);
     }
 }
 

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define P3D_ABI_VERSION 18
+#define P3D_ABI_VERSION 19
 
 enum p3d_status { P3D_OK = 0, P3D_EINVAL = 1, P3D_EHIP = 2, P3D_EUNSUPPORTED = 3 };
 enum p3d_dtype { P3D_F32 = 0, P3D_F16 = 1, P3D_BF16 = 2 };
@@ -289,6 +289,18 @@ typedef struct p3d_project_args {
 } p3d_project_args;
 
 int p3d_project(const p3d_project_args* args, void* stream);
+
+/* The three input projections of tokens that are already normalised: the
+ * to_q, to_kv and gate nn.Linear calls of attention.py:64-67,85 in 16-bit
+ * training, where the LayerNorm output is its own tensor (kept for the
+ * backward).  q = x Wq^T, kv = x Wkv^T and the gate logits x Wg^T +
+ * gate_bias, written as [rows, 2 heads] to `gate`; each output accumulated in
+ * fp32 and rounded once to dtype, as torch.mm / torch.addmm of the 16-bit
+ * operands (the summation order differs, so values can differ in the last
+ * bit).  ln_weight, ln_bias, ln_dtype and eps are not read; every other
+ * argument and limit is p3d_project's.  Replaces the three GEMMs of the
+ * training layer's input projections with one pass over x. */
+int p3d_project_linear(const p3d_project_args* args, void* stream);
 
 /* The projections of p3d_project with the summary pooling (compression.py:
  * 28-44, the pooling p3d_pool_fwd performs) fused in, for the no-grad

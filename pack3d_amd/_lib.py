@@ -25,7 +25,7 @@ class View(ctypes.Structure):
     _fields_ = [("data", c_void_p), ("sb", c_int64), ("sh", c_int64), ("sn", c_int64)]
 
 
-ABI_VERSION = 18  # P3D_ABI_VERSION in include/pack3d_hip.h
+ABI_VERSION = 19  # P3D_ABI_VERSION in include/pack3d_hip.h
 
 
 class Rope(ctypes.Structure):
@@ -100,6 +100,7 @@ SIGNATURES = {
                    c_int32),
     "p3d_layer_norm": ([_P, _P, _P, c_int32, _P, c_int64, c_int32, c_int32, c_float, _P], c_int32),
     "p3d_project": ([ctypes.POINTER(ProjectArgs), _P], c_int32),
+    "p3d_project_linear": ([ctypes.POINTER(ProjectArgs), _P], c_int32),
     "p3d_project_pool": ([ctypes.POINTER(ProjectArgs), ctypes.POINTER(PoolArgs), c_int32, _P], c_int32),
     "p3d_out_residual": ([_P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32, _P], c_int32),
     "p3d_layer_norm_train": ([_P, _P, _P, c_int32, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_float,

@@ -107,9 +107,14 @@ __device__ __forceinline__ void layer_norm_math(const ProjDev& a, const float* l
 
 // Waves per SIMD: 4 up to dim 128, 3 at dim 192 (the 168 registers that
 // leaves hold the GEMM without spilling; at 4 it spilled 16), else 2.
-template <typename T, int KS>
+// LIN: x holds tokens already normalised (no LayerNorm: the loaded half rows
+// are the B fragments), and the gate block writes its logits x Wg^T + bias,
+// rounded once, as [rows, 2 heads] instead of the pair softmax (one
+// workgroup per CU either way at dim 192, so LIN takes the register budget of
+// two waves per SIMD there).
+template <typename T, int KS, bool LIN>
 __global__ __launch_bounds__(64 * kProjWaves)
-__attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_project(ProjDev a) {
+__attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 && !LIN ? 3 : 2)))) void k_project(ProjDev a) {
     typedef Mma<T> M;
     typedef typename M::Frag Frag;
     constexpr int DIM = 16 * KS;
@@ -128,10 +133,11 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     constexpr bool kEarlyRows = KS <= 16;
     u32x4 xraw[KS];
     if constexpr (kEarlyRows) layer_norm_load<T, KS>(a, tok, live, g, xraw);
-    for (int c = threadIdx.x; c < DIM; c += blockDim.x) {
-        lw[c] = load_any(a.ln_w, c, a.ln_dtype);
-        lb[c] = load_any(a.ln_b, c, a.ln_dtype);
-    }
+    if constexpr (!LIN)
+        for (int c = threadIdx.x; c < DIM; c += blockDim.x) {
+            lw[c] = load_any(a.ln_w, c, a.ln_dtype);
+            lb[c] = load_any(a.ln_b, c, a.ln_dtype);
+        }
     const int gbase = a.q_out + a.kv_out, nout = gbase + 2 * a.heads;
     const int nblocks = (nout + 31) / 32;
     // Weight row o of the concatenation [Wq; Wkv; Wg].
@@ -170,7 +176,12 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
     // ---- LayerNorm of the lane's half row (channels 16 ks + 8 g + j)
     Frag xf[KS];
     if constexpr (!kEarlyRows) layer_norm_load<T, KS>(a, tok, live, g, xraw);
-    layer_norm_math<T, KS>(a, lw, lb, g, xraw, xf);
+    if constexpr (LIN) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) xf[ks] = __builtin_bit_cast(Frag, xraw[ks]);
+    } else {
+        layer_norm_math<T, KS>(a, lw, lb, g, xraw, xf);
+    }
 
     // ---- D = W X^T, 32 outputs at a time
     T* go = reinterpret_cast<T*>(a.gate) + tok * a.heads;
@@ -229,9 +240,15 @@ __attribute__((amdgpu_waves_per_eu(KS <= 8 ? 4 : (KS <= 12 ? 3 : 2)))) void k_pr
                             to_f32(from_f32<T>(v[2 * p] + load_any(a.gate_bias, j, a.gate_bias_dtype)));
                         const float l1 =
                             to_f32(from_f32<T>(v[2 * p + 1] + load_any(a.gate_bias, j + 1, a.gate_bias_dtype)));
-                        const float m = fmaxf(l0, l1);
-                        const float e0 = expf(l0 - m), e1 = expf(l1 - m);
-                        go[j / 2] = from_f32<T>(e1 / (e0 + e1));
+                        if constexpr (LIN) {
+                            T* gl = reinterpret_cast<T*>(a.gate) + tok * 2 * a.heads + j;
+                            gl[0] = from_f32<T>(l0);
+                            gl[1] = from_f32<T>(l1);
+                        } else {
+                            const float m = fmaxf(l0, l1);
+                            const float e0 = expf(l0 - m), e1 = expf(l1 - m);
+                            go[j / 2] = from_f32<T>(e1 / (e0 + e1));
+                        }
                     }
                 }
             }
@@ -833,19 +850,19 @@ void k_out_residual(const T* __restrict__ y, const T* __restrict__ wo, const R* 
     }
 }
 
-template <typename T>
+template <typename T, bool LIN>
 int launch_project(const ProjDev& d, hipStream_t s) {
     const unsigned blocks = (unsigned)cdiv(cdiv(d.rows, 32), kProjWaves);
     switch (d.dim) {
 #define CASE(DIM)                                                                     \
     case DIM:                                                                         \
-        k_project<T, DIM / 16><<<blocks, 64 * kProjWaves, 0, s>>>(d);                 \
+        k_project<T, DIM / 16, LIN><<<blocks, 64 * kProjWaves, 0, s>>>(d);            \
         break;
         CASE(64) CASE(96) CASE(128) CASE(192) CASE(256) CASE(384) CASE(512)
 #undef CASE
         default: return fail(P3D_EUNSUPPORTED, "dim must be one of 64, 96, 128, 192, 256, 384, 512");
     }
-    return check_launch("p3d_project");
+    return check_launch(LIN ? "p3d_project_linear" : "p3d_project");
 }
 
 template <typename T, typename R>
@@ -910,13 +927,15 @@ extern "C" int p3d_out_residual(const void* y, const void* wo, const void* x, vo
 
 namespace {
 
-// Validates the projection arguments and fills the kernels' argument block.
-int project_dev(const p3d_project_args& a, ProjDev& d) {
+// Validates the projection arguments and fills the kernels' argument block
+// (linear: no LayerNorm, whose parameters are then not read).
+int project_dev(const p3d_project_args& a, ProjDev& d, bool linear = false) {
     P3D_REQUIRE(a.dtype == P3D_F16 || a.dtype == P3D_BF16, "dtype must be fp16 or bf16");
-    P3D_REQUIRE(a.ln_dtype >= P3D_F32 && a.ln_dtype <= P3D_BF16 && a.gate_bias_dtype >= P3D_F32 &&
+    P3D_REQUIRE((linear || (a.ln_dtype >= P3D_F32 && a.ln_dtype <= P3D_BF16)) && a.gate_bias_dtype >= P3D_F32 &&
                     a.gate_bias_dtype <= P3D_BF16,
                 "unknown parameter dtype");
-    P3D_REQUIRE(a.x && a.ln_weight && a.ln_bias && a.wq && a.wkv && a.wg && a.gate_bias && a.q && a.kv && a.gate,
+    P3D_REQUIRE(a.x && (linear || (a.ln_weight && a.ln_bias)) && a.wq && a.wkv && a.wg && a.gate_bias && a.q &&
+                    a.kv && a.gate,
                 "null pointer argument");
     P3D_REQUIRE(a.rows >= 1 && a.heads >= 1, "empty projection problem");
     P3D_REQUIRE(a.dim >= 16 && a.dim <= kProjMaxDim && a.dim % 16 == 0, "dim must be a multiple of 16, at most 512");
@@ -954,7 +973,15 @@ extern "C" int p3d_project(const p3d_project_args* args, void* stream) {
     ProjDev d;
     if (int rc = project_dev(*args, d)) return rc;
     hipStream_t s = as_stream(stream);
-    return args->dtype == P3D_F16 ? launch_project<_Float16>(d, s) : launch_project<__bf16>(d, s);
+    return args->dtype == P3D_F16 ? launch_project<_Float16, false>(d, s) : launch_project<__bf16, false>(d, s);
+}
+
+extern "C" int p3d_project_linear(const p3d_project_args* args, void* stream) {
+    P3D_REQUIRE(args, "null args");
+    ProjDev d;
+    if (int rc = project_dev(*args, d, true)) return rc;
+    hipStream_t s = as_stream(stream);
+    return args->dtype == P3D_F16 ? launch_project<_Float16, true>(d, s) : launch_project<__bf16, true>(d, s);
 }
 
 extern "C" int p3d_project_pool(const p3d_project_args* args, const p3d_pool_args* pool, int32_t rotate_kl,

@@ -4,8 +4,10 @@ gradients from the HIP kernel ``p3d_weight_grad``.
 For y = x W^T the weight gradient dW = dy^T x contracts over every token
 (262,144 at 64^3) into a small matrix; the library GEMM runs it with a
 handful of workgroups.  ``p3d_weight_grad`` splits the tokens over the whole
-GPU and sums fp32 partials in a fixed order.  The forward products and the
-input gradients stay torch GEMMs.  These functions replace the to_q, to_kv,
+GPU and sums fp32 partials in a fixed order.  The three input projections
+run as one kernel over the normalised tokens (``p3d_project_linear``), their
+input gradient as one contraction (``p3d_input_grad``); the output
+projection's products stay torch GEMMs.  These functions replace the to_q, to_kv,
 gate (attention.py:64-67,85 of amilworks/Pack3D) and to_out + residual
 (attention.py:89) steps of ``PACK3DAttention.forward`` when it runs in a
 16-bit compute type with autograd active; weight gradients are accumulated
@@ -71,6 +73,35 @@ def input_grad(dys, ws):
               outs[1], dys[2].data_ptr(), dys[2].stride(0), outs[2], wt.data_ptr(), k_pad, dx.data_ptr(), rows, dim,
               _lib.DTYPES[dt], _lib.stream_of(dx.device))
     return dx
+
+
+PROJECT_DIMS = (64, 96, 128, 192, 256, 384, 512)
+
+
+def project_linear(x16, ws, bg):
+    """(x Wq^T, x Wkv^T, x Wg^T + bg) for x16 [rows, dim] and the weights ws
+    [*, dim] of one 16-bit type, from one pass over x16 (``p3d_project_linear``:
+    each output summed in fp32 and rounded once, as the torch products); None
+    where the kernel does not take the shapes (the caller then runs the three
+    products)."""
+    dt, (rows, dim) = x16.dtype, x16.shape
+    q_out, kv_out, g_out = (w.shape[0] for w in ws)
+    if (dt not in (torch.float16, torch.bfloat16) or dim not in PROJECT_DIMS or q_out % 16 or kv_out % 16
+            or g_out % 2 or not x16.is_contiguous() or x16.data_ptr() % 16
+            or any(w.dtype != dt or w.shape[1] != dim or not w.is_contiguous() or w.data_ptr() % 16 for w in ws)
+            or bg.numel() != g_out):
+        return None
+    bg = bg.to(dt).contiguous()  # the bias in dt, as torch.addmm(bg.to(dt), ...) adds it
+    q = torch.empty(rows, q_out, dtype=dt, device=x16.device)
+    kv = torch.empty(rows, kv_out, dtype=dt, device=x16.device)
+    gl = torch.empty(rows, g_out, dtype=dt, device=x16.device)
+    args = _lib.ProjectArgs(x=x16.data_ptr(), ln_weight=None, ln_bias=None, wq=ws[0].data_ptr(),
+                            wkv=ws[1].data_ptr(), wg=ws[2].data_ptr(), gate_bias=bg.data_ptr(), q=q.data_ptr(),
+                            kv=kv.data_ptr(), gate=gl.data_ptr(), rows=rows, dim=dim, q_out=q_out, kv_out=kv_out,
+                            heads=g_out // 2, dtype=_lib.DTYPES[dt], ln_dtype=_lib.DTYPES[dt],
+                            gate_bias_dtype=_lib.DTYPES[bg.dtype], eps=0.0)
+    _lib.call("p3d_project_linear", args, _lib.stream_of(x16.device))
+    return q, kv, gl
 
 
 def weight_grad(dy, x):
@@ -201,9 +232,13 @@ class InputProjections(torch.autograd.Function):
     def forward(ctx, x, wq, wkv, wg, bg, dt):
         x16 = _rows(x).to(dt).contiguous()
         ws = [w.to(dt) for w in (wq, wkv, wg)]
-        q = torch.mm(x16, ws[0].t())
-        kv = torch.mm(x16, ws[1].t())
-        gl = torch.addmm(bg.to(dt), x16, ws[2].t())
+        made = project_linear(x16, ws, bg)
+        if made is not None:
+            q, kv, gl = made
+        else:
+            q = torch.mm(x16, ws[0].t())
+            kv = torch.mm(x16, ws[1].t())
+            gl = torch.addmm(bg.to(dt), x16, ws[2].t())
         ctx.save_for_backward(x16, *ws)
         ctx.meta = (x.shape, x.dtype, wq.dtype, wkv.dtype, wg.dtype, bg.dtype)
         lead = x.shape[:-1]

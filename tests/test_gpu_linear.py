@@ -166,7 +166,7 @@ def test_layer_training_gradients_match_torch_linear(gpu, dtype):
     # to_out's weight gradient alone; to_q / to_kv / gate share one pass over
     # the tokens, and their input gradients one contraction.
     assert calls.count("p3d_weight_grad") == 1 and calls.count("p3d_weight_grad3") == 1, calls
-    assert calls.count("p3d_input_grad") == 1, calls
+    assert calls.count("p3d_input_grad") == 1 and calls.count("p3d_project_linear") == 1, calls
     y_t, dx_t, g_t = run(False)
     assert rel_l2(y_h, y_t) < 1e-2
     assert rel_l2(dx_h, dx_t) < 1e-2
@@ -174,6 +174,54 @@ def test_layer_training_gradients_match_torch_linear(gpu, dtype):
         err = rel_l2(g_h[k], g_t[k])
         print(f"  {k}: rel_l2={err:.3g}", flush=True)
         assert err < 1e-2, (k, err)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim,q_out,kv_out,g_out,rows", [(192, 192, 768, 8, 1003), (64, 64, 128, 4, 77),
+                                                         (96, 48, 64, 6, 300), (256, 128, 512, 4, 129),
+                                                         (512, 256, 256, 2, 65), (128, 32, 96, 16, 2048)])
+def test_project_linear_matches_fp32_products(gpu, dtype, dim, q_out, kv_out, g_out, rows):
+    """p3d_project_linear (the training layer's three input projections in one
+    pass) against the products of the same 16-bit operands in fp32, rounded
+    once to the 16-bit type (what torch.mm / torch.addmm compute up to the
+    order of the fp32 sums): every value within one rounding step of the
+    output.  Ragged row counts; blocks of 32 outputs that straddle q / kv and
+    kv / gate (q_out 48, g_out 6); a gate bias in fp32 that the layer rounds
+    to the compute type first, as torch.addmm(bg.to(dt), ...) does."""
+    print(f"project linear {dim} {q_out}/{kv_out}/{g_out} rows={rows} {dtype}", flush=True)
+    gen = torch.Generator(device=gpu).manual_seed(dim + rows)
+    x = (torch.randn(rows, dim, device=gpu, generator=gen) * 1.5).to(dtype)
+    ws = [(torch.randn(o, dim, device=gpu, generator=gen) / dim ** 0.5).to(dtype) for o in (q_out, kv_out, g_out)]
+    bg = torch.randn(g_out, device=gpu, generator=gen)
+    got = linear.project_linear(x, ws, bg)
+    assert got is not None
+    bias = bg.to(dtype).float()
+    exp = [x.float() @ ws[0].float().t(), x.float() @ ws[1].float().t(), x.float() @ ws[2].float().t() + bias]
+    tol = {torch.bfloat16: 2 ** -8, torch.float16: 2 ** -11}[dtype]
+    for name, g_, e_ in zip(("q", "kv", "gate"), got, exp):
+        assert g_.shape == e_.shape and g_.dtype == dtype, name
+        g32 = g_.float()
+        bound = tol * e_.abs() * 1.01 + 1e-6
+        assert ((g32 - e_).abs() <= bound).all(), (name, float((g32 - e_).abs().max()))
+        # almost every value is the correctly rounded fp32 product
+        assert float((g32 == e_.to(dtype).float()).float().mean()) > 0.98, name
+
+
+def test_project_linear_declines_unsupported_shapes():
+    """Shapes the kernel does not take go back to the torch products (None)
+    before anything is launched: a width outside its list, q_out not a
+    multiple of 16, an odd gate width, fp32."""
+    x = torch.zeros(4, 80, dtype=torch.bfloat16)
+    ws = [torch.zeros(o, 80, dtype=torch.bfloat16) for o in (32, 64, 2)]
+    assert linear.project_linear(x, ws, torch.zeros(2)) is None
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    ws = [torch.zeros(o, 64, dtype=torch.bfloat16) for o in (24, 64, 2)]
+    assert linear.project_linear(x, ws, torch.zeros(2)) is None
+    ws = [torch.zeros(o, 64, dtype=torch.bfloat16) for o in (32, 64, 3)]
+    assert linear.project_linear(x, ws, torch.zeros(3)) is None
+    x32 = torch.zeros(4, 64)
+    ws32 = [torch.zeros(o, 64) for o in (32, 64, 2)]
+    assert linear.project_linear(x32, ws32, torch.zeros(2)) is None
 
 
 @pytest.mark.parametrize("x_dtype,y_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float16),

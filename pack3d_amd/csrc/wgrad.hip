@@ -7,10 +7,13 @@
 // fixed order (deterministic).
 //
 // A workgroup owns 256 output rows (8 waves x 32) and a token range, taken
-// 32 tokens per stage.  A stage of dy [32 tokens x 256 rows] and of x [32
+// TOK tokens per stage.  A stage of dy [TOK tokens x 256 rows] and of x [TOK
 // tokens x I] is loaded with 16-byte row pieces (the next stage in flight
 // while the current one is multiplied) and stored row-major in LDS.  The
-// MFMA operands need 8 consecutive tokens of one column per lane; they come
+// pass is bound by the bytes in flight per CU: from I = 128 on, one
+// workgroup fits per CU and its stages take 64 tokens (32-token stages ran
+// 15% slower at I = 192); narrower x keeps 32-token stages and several
+// workgroups per CU.  The MFMA operands need 8 consecutive tokens of one column per lane; they come
 // out of the row-major tiles through ds_read_b64_tr_b16, two 8-byte
 // transposed reads per fragment, so nothing is transposed on the way in.
 // Each wave then multiplies its 32 x 16-token A fragment with the I / 32
@@ -22,7 +25,10 @@ namespace {
 
 constexpr int kWgWaves = 8;
 constexpr int kWgRows = 32 * kWgWaves;  // output rows per workgroup
-constexpr int kWgTok = 32;              // tokens per stage
+// Tokens per stage for x of 32 IT columns.
+template <int IT>
+constexpr int wg_tok() { return IT >= 4 ? 64 : 32; }
+constexpr int kWgTokMax = 64;
 
 // Row stride (elements of a 16-bit type) of an LDS tile w elements wide: the
 // stride in dwords is 16 mod 32, so the four consecutive rows that a 16-lane
@@ -53,7 +59,7 @@ __device__ __forceinline__ typename Mma<T>::Frag frag_tr(const T* tile, int stri
 }
 
 template <int IT>
-constexpr int wgrad_stage_elems() { return kWgTok * (tile_stride(kWgRows) + tile_stride(32 * IT)); }
+constexpr int wgrad_stage_elems() { return wg_tok<IT>() * (tile_stride(kWgRows) + tile_stride(32 * IT)); }
 
 // dy as up to three column blocks of output rows: rows [0, end[0]) from
 // src[0], [end[0], end[1]) from src[1], [end[1], O) from src[2], each with its
@@ -75,6 +81,7 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x
     constexpr int I = 32 * IT;
     constexpr int SA = tile_stride(kWgRows), SB = tile_stride(I);
     constexpr int STAGE = wgrad_stage_elems<IT>();         // elements
+    constexpr int kWgTok = wg_tok<IT>();
     constexpr int PA = kWgTok * (kWgRows / 8) / (64 * kWgWaves);            // dy pieces per thread
     constexpr int BP = kWgTok * (I / 8);                                     // x pieces per stage
     constexpr int PB = (BP + 64 * kWgWaves - 1) / (64 * kWgWaves);           // x pieces per thread
@@ -185,7 +192,7 @@ __global__ __launch_bounds__(kRedElems * kRedGroups) void k_wgrad_reduce(const f
 template <typename T>
 int launch_wgrad(const WgSrc<T>& dy, const void* x, int64_t ldx, float* dw, float* part, int64_t rows, int O, int I,
                  int splits, hipStream_t s) {
-    const int64_t per = cdiv(cdiv(rows, splits), kWgTok) * kWgTok;
+    const int64_t per = cdiv(cdiv(rows, splits), kWgTokMax) * kWgTokMax;
     const int used = (int)cdiv(rows, per);
     const dim3 grid((unsigned)cdiv(O, kWgRows), (unsigned)used);
     switch (I / 32) {

@@ -366,7 +366,8 @@ int p3d_input_grad(const void* dq, int64_t dq_stride, int32_t q_out, const void*
  * aligned rows).  The rows are split into `splits` ranges whose fp32
  * partials go to workspace [splits, out_features, in_features] and are then
  * summed in order (deterministic).  out_features a positive multiple of 8;
- * in_features a multiple of 32, at most 256. */
+ * in_features a multiple of 32 up to 256, or a multiple of 256 up to 2048
+ * (taken in column blocks of 256, dy read once per block). */
 int p3d_weight_grad(const void* dy, int64_t ldy, const void* x, int64_t ldx, float* dw, float* workspace,
                     int64_t rows, int32_t out_features, int32_t in_features, int32_t splits, int32_t dtype,
                     void* stream);

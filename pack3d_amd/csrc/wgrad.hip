@@ -29,6 +29,7 @@ constexpr int kWgRows = 32 * kWgWaves;  // output rows per workgroup
 template <int IT>
 constexpr int wg_tok() { return IT >= 4 ? 64 : 32; }
 constexpr int kWgTokMax = 64;
+constexpr int kWgMaxCols = 256;  // input columns per workgroup
 
 // Row stride (elements of a 16-bit type) of an LDS tile w elements wide: the
 // stride in dwords is 16 mod 32, so the four consecutive rows that a 16-lane
@@ -72,11 +73,12 @@ struct WgSrc {
 };
 
 // Partial dW of token range [blockIdx.y * per, + per) for output rows
-// [blockIdx.x * 256, + 256), written to part[blockIdx.y][o][i].  Two stages
-// of dynamic LDS (2 * wgrad_stage_elems<IT>() elements).
+// [blockIdx.x * 256, + 256) and input columns [blockIdx.z * I, + I) of
+// I_total, written to part[blockIdx.y][o][blockIdx.z * I + i].  Two stages of
+// dynamic LDS (2 * wgrad_stage_elems<IT>() elements).
 template <typename T, int IT>
 __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x, int64_t ldx, float* part,
-                                                        int64_t rows, int O, int64_t per) {
+                                                        int64_t rows, int O, int64_t per, int I_total) {
     typedef Mma<T> M;
     constexpr int I = 32 * IT;
     constexpr int SA = tile_stride(kWgRows), SB = tile_stride(I);
@@ -91,6 +93,7 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
     const int ob = blockIdx.x * kWgRows;
     const int64_t n0 = (int64_t)blockIdx.y * per, n1 = min(rows, n0 + per);
+    x += (int64_t)blockIdx.z * I;  // this workgroup's input columns
     const bool active = ob + 32 * wave < O;  // wave-uniform
 
     u32x4 ra[PA], rb[PB];
@@ -157,13 +160,13 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x
     }
     if (!active) return;
     // D row acc_row(r, g) is output row ob + 32 wave + that; column lane % 32 of tile t is input 32 t + lane % 32.
-    float* out = part + (int64_t)blockIdx.y * O * I;
+    float* out = part + (int64_t)blockIdx.y * O * I_total + (int64_t)blockIdx.z * I;
 #pragma unroll
     for (int t = 0; t < IT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int o = ob + 32 * wave + acc_row(r, g);
-            if (o < O) out[(int64_t)o * I + 32 * t + (lane & 31)] = acc[t][r];
+            if (o < O) out[(int64_t)o * I_total + 32 * t + (lane & 31)] = acc[t][r];
         }
 }
 
@@ -189,17 +192,26 @@ __global__ __launch_bounds__(kRedElems * kRedGroups) void k_wgrad_reduce(const f
     }
 }
 
+// Input widths the kernel takes: a multiple of 32 up to 256 (one column
+// block), or a multiple of 256 up to 2048 (column blocks of 256).
+inline bool wgrad_cols_ok(int I) {
+    return (I >= 32 && I % 32 == 0 && I <= kWgMaxCols) || (I > kWgMaxCols && I % kWgMaxCols == 0 && I <= 2048);
+}
+
 template <typename T>
 int launch_wgrad(const WgSrc<T>& dy, const void* x, int64_t ldx, float* dw, float* part, int64_t rows, int O, int I,
                  int splits, hipStream_t s) {
     const int64_t per = cdiv(cdiv(rows, splits), kWgTokMax) * kWgTokMax;
     const int used = (int)cdiv(rows, per);
-    const dim3 grid((unsigned)cdiv(O, kWgRows), (unsigned)used);
-    switch (I / 32) {
+    // Past 256 input columns the columns go to blocks of 256 (grid z), each
+    // with its own accumulators; dy is read once per block.
+    const int cbs = I > kWgMaxCols ? I / kWgMaxCols : 1, Ib = I / cbs;
+    const dim3 grid((unsigned)cdiv(O, kWgRows), (unsigned)used, (unsigned)cbs);
+    switch (Ib / 32) {
 #define CASE(IT)                                                                                                  \
     case IT:                                                                                                      \
         k_wgrad<T, IT><<<grid, 64 * kWgWaves, 2 * wgrad_stage_elems<IT>() * sizeof(T), s>>>(                      \
-            dy, (const T*)x, ldx, part, rows, O, per);                                                            \
+            dy, (const T*)x, ldx, part, rows, O, per, I);                                                         \
         break;
         CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
 #undef CASE
@@ -222,8 +234,8 @@ extern "C" int p3d_weight_grad(const void* dy, int64_t ldy, const void* x, int64
     P3D_REQUIRE(dtype == P3D_F16 || dtype == P3D_BF16, "dtype must be fp16 or bf16");
     P3D_REQUIRE(rows >= 1 && splits >= 1, "need at least one row and one split");
     P3D_REQUIRE(out_features >= 8 && out_features % 8 == 0, "out_features must be a positive multiple of 8");
-    P3D_REQUIRE(in_features >= 32 && in_features % 32 == 0 && in_features <= 256,
-                "in_features must be a multiple of 32, at most 256");
+    P3D_REQUIRE(wgrad_cols_ok(in_features),
+                "in_features must be a multiple of 32 up to 256, or a multiple of 256 up to 2048");
     P3D_REQUIRE(ldy >= out_features && ldy % 8 == 0 && ldx >= in_features && ldx % 8 == 0,
                 "row strides must cover the rows and keep 16-byte alignment");
     P3D_REQUIRE(aligned16(dy) && aligned16(x), "dy and x must be 16-byte aligned");
@@ -248,8 +260,8 @@ extern "C" int p3d_weight_grad3(const void* dy0, int64_t ld0, int32_t out0, cons
     P3D_REQUIRE(out0 >= 8 && out1 >= 8 && out2 >= 8 && out0 % 8 == 0 && out1 % 8 == 0 && out2 % 8 == 0 &&
                     (int64_t)out0 + out1 + out2 < (1 << 24),
                 "out features must be positive multiples of 8");
-    P3D_REQUIRE(in_features >= 32 && in_features % 32 == 0 && in_features <= 256,
-                "in_features must be a multiple of 32, at most 256");
+    P3D_REQUIRE(wgrad_cols_ok(in_features),
+                "in_features must be a multiple of 32 up to 256, or a multiple of 256 up to 2048");
     P3D_REQUIRE(ld0 >= out0 && ld1 >= out1 && ld2 >= out2 && ld0 % 8 == 0 && ld1 % 8 == 0 && ld2 % 8 == 0 &&
                     ldx >= in_features && ldx % 8 == 0,
                 "row strides must cover the rows and keep 16-byte alignment");

@@ -45,7 +45,9 @@ def compute_dtype(x):
 
 
 def weight_grad_supported(out_features, in_features):
-    return out_features >= 8 and out_features % 8 == 0 and in_features % 32 == 0 and 32 <= in_features <= 256
+    cols_ok = (in_features % 32 == 0 and 32 <= in_features <= 256) or (
+        in_features % 256 == 0 and 256 < in_features <= 2048)
+    return out_features >= 8 and out_features % 8 == 0 and cols_ok
 
 
 INPUT_GRAD_DIMS = (64, 96, 128, 192, 256)

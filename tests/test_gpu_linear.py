@@ -26,11 +26,15 @@ def _reference(dy, x):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,out_f,in_f,splits", [(37, 8, 192, 1), (1000, 200, 32, 3), (4099, 136, 256, 7),
-                                                    (70000, 384, 192, 33), (262144, 192, 192, 128)])
+                                                    (70000, 384, 192, 33), (262144, 192, 192, 128),
+                                                    (3001, 264, 512, 5), (777, 40, 1024, 2),
+                                                    (262144, 512, 512, 52)])
 def test_weight_grad_matches_fp32_product(gpu, dtype, rows, out_f, in_f, splits):
-    """Ragged row counts (not multiples of the 32-token stage or of the
-    split), output widths that leave part of a 128-row workgroup idle, every
-    split count from one to the c4 setting, and the c4 size itself."""
+    """Ragged row counts (not multiples of the token stage or of the split),
+    output widths that leave part of a 256-row workgroup idle, every split
+    count from one to the c4 setting, the c4 size itself, and inputs wider
+    than 256 columns (column blocks of 256; 512 at 262,144 rows is the
+    allen15 preset's to_out)."""
     print(f"weight grad {rows}x{out_f}x{in_f} s{splits} {dtype}", flush=True)
     gen = torch.Generator(device=gpu).manual_seed(rows + out_f)
     dy = torch.randn(rows, out_f, device=gpu, generator=gen).to(dtype)
@@ -101,6 +105,25 @@ def test_weight_grads3_match_fp32_products(gpu, dtype, rows, in_f, outs):
     wide = torch.randn(rows, qo + kvo + 24, device=gpu, generator=gen).to(dtype)
     dys = [wide[:, :qo], wide[:, qo + 8:qo + 8 + kvo], torch.randn(rows, go, device=gpu, generator=gen).to(dtype)]
     x = torch.randn(rows, in_f, device=gpu, generator=gen).to(dtype)
+    got = linear.weight_grads3(dys, x)
+    assert got is not None
+    for dy, dw in zip(dys, got):
+        err = rel_l2(dw, _reference(dy, x))
+        print(f"  rel_l2={err:.3g}", flush=True)
+        assert err < 1e-5
+
+
+@pytest.mark.parametrize("rows,in_f,outs", [(4099, 512, (512, 512, 16)), (1000, 768, (64, 128, 8))])
+def test_weight_grads3_wide_inputs(gpu, rows, in_f, outs):
+    """p3d_weight_grad3 over inputs wider than 256 columns (the allen15
+    preset's dim 512: to_q 512, to_kv 512, gate 16 outputs) against the fp32
+    products, with dy as column slices of one wider buffer."""
+    print(f"weight grads3 wide {rows}x{in_f} {outs}", flush=True)
+    gen = torch.Generator(device=gpu).manual_seed(rows + in_f)
+    qo, kvo, go = outs
+    wide = torch.randn(rows, qo + kvo + 24, device=gpu, generator=gen).to(torch.bfloat16)
+    dys = [wide[:, :qo], wide[:, qo + 8:qo + 8 + kvo], torch.randn(rows, go, device=gpu, generator=gen).to(torch.bfloat16)]
+    x = torch.randn(rows, in_f, device=gpu, generator=gen).to(torch.bfloat16)
     got = linear.weight_grads3(dys, x)
     assert got is not None
     for dy, dw in zip(dys, got):

@@ -70,7 +70,8 @@ def test_entry_points_reject_bad_arguments_before_launch():
         _lib.call("p3d_attn_fwd_grid", args, None)
     # Weight gradient: widths the kernel does not take (never dereferenced).
     bf16 = _lib.DTYPES[torch.bfloat16]
-    for out_f, in_f, msg in ((12, 192, "out_features"), (8, 48, "in_features"), (8, 288, "in_features")):
+    for out_f, in_f, msg in ((12, 192, "out_features"), (8, 48, "in_features"), (8, 288, "in_features"),
+                             (8, 2304, "in_features")):
         with pytest.raises(RuntimeError, match=msg):
             _lib.call("p3d_weight_grad", 16, out_f, 16, in_f, 16, 16, 100, out_f, in_f, 1, bf16, None)
     with pytest.raises(RuntimeError, match="null pointer"):

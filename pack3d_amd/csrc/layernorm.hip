@@ -173,14 +173,24 @@ __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const voi
 // g = dy * w, dx = rstd (g - mean(g) - xhat mean(g xhat)) per row, and the
 // affine gradients dw = sum_rows dy xhat, db = sum_rows dy.  Blocks stride
 // over the rows; each writes its fp32 partial sums of dw and db to
-// part[block][0 / 1][dim], summed by the caller.  PPL: pieces per lane
-// (ceil(dim / EP / 8)), which sizes the per-lane arrays.
-template <typename TD, typename TI, typename TO, int PPL>
+// part[block][0 / 1][dim], summed by the caller.  LPR lanes share a row (8,
+// or 32 for rows of more than 32 pieces, whose per-lane arrays would
+// otherwise hold a wave to one per SIMD); PPL: pieces per lane
+// (ceil(dim / EP / LPR)), which sizes the per-lane arrays.
+template <typename TD, typename TI, typename TO, int PPL, int LPR>
 __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* dres, const TI* x, const void* w,
                                                         int param_dtype, const float* mean_in, const float* rstd_in,
                                                         TO* dx, float* part, int64_t rows, int dim, int parts) {
     constexpr int EP = Piece<TI>::N;
+    constexpr int kLanesPerRow = LPR;
     constexpr int GROUPS = 256 / kLanesPerRow;
+    // Sum over the row's lanes.
+    auto row_sum = [](float v) __attribute__((always_inline)) {
+        v = group8_sum(v);
+        if constexpr (LPR >= 16) v += __shfl_xor(v, 8);
+        if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
+        return v;
+    };
     __shared__ __align__(16) float lw[kMaxDim];
     __shared__ float red[2][kMaxDim];
     for (int c = threadIdx.x; c < dim; c += blockDim.x) {
@@ -218,7 +228,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* 
                 }
             }
         }
-        const float mg = group8_sum(sg) / (float)dim, mgx = group8_sum(sgx) / (float)dim;
+        const float mg = row_sum(sg) / (float)dim, mgx = row_sum(sgx) / (float)dim;
 #pragma unroll
         for (int i = 0; i < PPL; ++i) {
             const int p = sub + kLanesPerRow * i;
@@ -283,7 +293,8 @@ int dispatch_ln_train(const void* x, const void* w, const void* b, int pdt, void
 template <typename TD, typename TI, typename TO>
 int launch_ln_bwd(const void* dy, const void* dres, const void* x, const void* w, int pdt, const float* mean,
                   const float* rstd, void* dx, float* part, int64_t rows, int dim, int parts, hipStream_t s) {
-    const int ppl = (int)cdiv(dim / Piece<TI>::N, kLanesPerRow);
+    const int pieces = dim / Piece<TI>::N;
+    const int ppl = (int)cdiv(pieces, kLanesPerRow);
     // At most one round of resident blocks: the blocks stride over the rows,
     // and a partly filled second round would leave most of the GPU idle.
     int dev = 0, cus = 0;
@@ -295,15 +306,31 @@ int launch_ln_bwd(const void* dy, const void* dres, const void* x, const void* w
         const int64_t resident = (int64_t)(cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1);
         return (unsigned)(parts < resident ? parts : resident);
     };
-    switch (ppl) {
+    if (ppl > 4) {
+        // 32 lanes per row: 2 pieces per lane (up to 64 pieces).
+        switch ((int)cdiv(pieces, 32)) {
 #define CASE(P)                                                                                                  \
     case P:                                                                                                      \
-        k_layer_norm_bwd<TD, TI, TO, P>                                                                          \
-            <<<grid_for(reinterpret_cast<const void*>(k_layer_norm_bwd<TD, TI, TO, P>)), 256, 0, s>>>(          \
+        k_layer_norm_bwd<TD, TI, TO, P, 32>                                                                      \
+            <<<grid_for(reinterpret_cast<const void*>(k_layer_norm_bwd<TD, TI, TO, P, 32>)), 256, 0, s>>>(      \
                 (const TD*)dy, (const TO*)dres, (const TI*)x, w, pdt, mean, rstd, (TO*)dx, part, rows, dim,      \
                 parts);                                                                                          \
         break;
-        CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
+            CASE(2)
+#undef CASE
+            default: return fail(P3D_EUNSUPPORTED, "dim too large for the LayerNorm backward");
+        }
+        return check_launch("p3d_layer_norm_bwd");
+    }
+    switch (ppl) {
+#define CASE(P)                                                                                                  \
+    case P:                                                                                                      \
+        k_layer_norm_bwd<TD, TI, TO, P, 8>                                                                       \
+            <<<grid_for(reinterpret_cast<const void*>(k_layer_norm_bwd<TD, TI, TO, P, 8>)), 256, 0, s>>>(       \
+                (const TD*)dy, (const TO*)dres, (const TI*)x, w, pdt, mean, rstd, (TO*)dx, part, rows, dim,      \
+                parts);                                                                                          \
+        break;
+        CASE(1) CASE(2) CASE(3) CASE(4)
 #undef CASE
         default: return fail(P3D_EUNSUPPORTED, "dim too large for the LayerNorm backward");
     }

@@ -11,8 +11,10 @@ A step is one layer forward (LayerNorm, projections, gate, fused core,
 to_out, residual) under torch.inference_mode with every input resident in
 HBM.  The layer's output is checked against the oracle layer before the line
 is printed (a failed check raises).  The same line carries the c4 layer
-forward + backward with its summary-backward kernels, and the
-incremental peak of allocated bytes of both.  Prints one JSON line.
+forward + backward with its summary-backward kernels, the
+incremental peak of allocated bytes of both, and the reference benchmark's
+own headline preset (allen15, inference and forward + backward) beside the
+medians the reference publishes for it.  Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -407,6 +409,67 @@ def gather_probe():
 C4_SHAPE = (32, 128, 64)
 
 
+# The reference benchmark's own headline preset (benchmarks/attention.py:84-87
+# of amilworks/Pack3D, "allen15") on its published 32 x 128 x 64 grid, and
+# the reference's published medians for it on one H200 with its Triton backend
+# (benchmarks/results/h200_vision_2026-11-18.md:7-14, raster, bf16).
+ALLEN15 = dict(dim=512, heads=8, kv_heads=2, head_dim=64, block=(1, 4, 4), pool_size=16, layout="raster_block",
+               radius=1, grid=(32, 128, 64))
+ALLEN15_H200_MS = {"inference": 4.644, "forward_backward": 15.098}
+
+
+def bench_allen15(warmup=5, iterations=20):
+    """The reference harness's two modes on its allen15 preset (bf16 model and
+    input, seed 31, batch 1): inference under inference_mode, and forward +
+    backward of y.float().square().mean() to the input and every parameter
+    with the gradients cleared first (benchmarks/attention.py:14-22); median
+    of `iterations` synchronised steps each, as that harness reports."""
+    import statistics
+
+    import pack3d_amd as p3d
+
+    c = ALLEN15
+    dev = torch.device("cuda:0")
+    torch.manual_seed(31)
+    model = p3d.PACK3DAttention(c["dim"], heads=c["heads"], kv_heads=c["kv_heads"], head_dim=c["head_dim"],
+                                block_volume=math.prod(c["block"])).to(dev, torch.bfloat16)
+    layout = p3d.build_layout(c["grid"], c["block"], radius=c["radius"], pool_size=c["pool_size"],
+                              layout=c["layout"], device=dev)
+    n = math.prod(c["grid"])
+    x = torch.randn(1, n, c["dim"], device=dev, dtype=torch.bfloat16, requires_grad=True)
+
+    def inference():
+        with torch.inference_mode():
+            model(x, layout)
+
+    def forward_backward():
+        model.zero_grad(set_to_none=True)
+        x.grad = None
+        model(x, layout).float().square().mean().backward()
+
+    out = {"workload": "the reference benchmark's allen15 preset: dim 512, 8 / 2 heads, head_dim 64, (1, 4, 4) "
+                       "blocks, pool 16, raster, radius 1, 32 x 128 x 64 (262,144 tokens), batch 1, bf16",
+           "warmup": warmup, "iterations": iterations}
+    for name, step in (("inference", inference), ("forward_backward", forward_backward)):
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(iterations):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            times.append(1000.0 * (time.perf_counter() - t0))
+        ms = statistics.median(times)
+        out[f"{name}_ms"] = round(ms, 4)
+        out[f"{name}_reference_h200_ms"] = ALLEN15_H200_MS[name]
+        out[f"{name}_speedup_vs_reference_h200"] = round(ALLEN15_H200_MS[name] / ms, 3)
+    del model, layout, x
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_c4(steps, warmup, kernels=False):
     """c4: layer forward + backward on 32 x 128 x 64
     (262,144 tokens), batch 1, raster, bf16 autocast, upstream gradient N(0, 1).
@@ -560,6 +623,8 @@ def main():
                    help="only run the launch sequence that the HBM traffic counters are collected over")
     p.add_argument("--gather-probe", action="store_true",
                    help="only run the launch sequence the indexed-gather and rotation counters are collected over")
+    p.add_argument("--no-presets", action="store_true",
+                   help="skip the reference benchmark's allen15 preset (reported beside the c2 line)")
     p.add_argument("--c4", action="store_true",
                    help="time the c4 layer forward + backward instead (one JSON line of its own)")
     p.add_argument("--probe-rates", action="store_true",
@@ -600,6 +665,7 @@ def main():
     # so that the c2 steps right after it are timed at those clocks rather
     # than on the ramp of a freshly started process.
     c4 = bench_c4(a.c4_steps, a.c4_warmup, kernels=True)
+    allen15 = None if a.no_presets else bench_allen15()
 
     with torch.inference_mode():
         for _ in range(a.warmup):
@@ -711,6 +777,7 @@ def main():
                        "incremental_peak_allocated_bytes": c4["config"]["incremental_peak_allocated_bytes"]},
         "roofline_global_dq": c4["roofline_global_dq"],
         "roofline_global_dkv": c4["roofline_global_dkv"],
+        "reference_preset_allen15": allen15,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -352,7 +352,9 @@ int p3d_copy_rows(p3d_view src, p3d_view dst, int64_t batch, int32_t heads, int6
  * elements (multiples of 8, 16-byte aligned rows); wt = [Wq; Wkv; Wg]^T as a
  * contiguous [dim][k_pad] matrix whose columns past q_out + kv_out + g_out
  * are zero, k_pad a multiple of 64; dx [rows, dim] contiguous.  q_out, kv_out,
- * g_out positive multiples of 8; dim 64, 96, 128, 192 or 256; fp16 / bf16. */
+ * g_out positive multiples of 8; dim 64, 96, 128, 192, 256, 384 or 512 (the
+ * last two in two channel halves, the gradients read once per half); fp16 /
+ * bf16. */
 int p3d_input_grad(const void* dq, int64_t dq_stride, int32_t q_out, const void* dkv, int64_t dkv_stride,
                    int32_t kv_out, const void* dg, int64_t dg_stride, int32_t g_out, const void* wt, int32_t k_pad,
                    void* dx, int64_t rows, int32_t dim, int32_t dtype, void* stream);

@@ -14,7 +14,10 @@
 // 32 cb + acc_row(r, l / 32) of token l % 32.  Each wave keeps all of its
 // token tile's channel blocks (CB = NB; WT = NB / CB waves per tile is 1 for
 // every width taken: split over two waves, each tile's dY rows were read twice
-// and the pass took 25% longer) for the whole contraction.  The result goes
+// and the pass took 25% longer) for the whole contraction.  Widths past 256
+// (384, 512) go to two channel halves on grid y, each workgroup computing one
+// half (its W^T rows, its dx columns), so dY is read once per half; the
+// registers of a whole 512-channel row would not fit.  The result goes
 // through the wave's LDS tile and leaves as 16-byte row pieces, rounded once
 // from the fp32 sum.
 #include "attn_common.hpp"
@@ -31,8 +34,9 @@ struct IgDev {
     int q_out, kv_out, k_end;   // feature ranges [0, q_out), [q_out, q_out + kv_out), [.., k_end)
     const char* wt;             // [dim][k_pad]
     int k_pad;
-    char* dx;                   // [rows][dim]
+    char* dx;                   // [rows][ldx]
     int64_t rows;
+    int ldx;                    // dx row stride (elements): the whole width
 };
 
 template <typename T>
@@ -68,7 +72,8 @@ __global__ __launch_bounds__(64 * kIgWaves, 2) void k_input_grad(IgDev a) {
     const int64_t tok0 = ((int64_t)blockIdx.x * TILES + tile) * 32;
     const int64_t trow = min(tok0 + t, a.rows - 1);  // dead lanes read the last row, their outputs are dropped
     const int chunks = a.k_pad / kIgChunk;
-    const T* wt = tp<T>(a.wt);
+    // This workgroup's channel half (grid y): W^T rows and dx columns from DIM * blockIdx.y.
+    const T* wt = tp<T>(a.wt) + (int64_t)blockIdx.y * DIM * a.k_pad;
 
     // W^T chunk c: rows = channels, 64 features each.
     u32x4 wreg[PPT];
@@ -149,7 +154,7 @@ __global__ __launch_bounds__(64 * kIgWaves, 2) void k_input_grad(IgDev a) {
     // +3, then 16-byte pieces (token tt, channels 8 pp .. +7), four lanes per
     // token.
     T* tl = otile[wave];
-    T* dx = reinterpret_cast<T*>(a.dx);
+    T* dx = reinterpret_cast<T*>(a.dx) + (int64_t)blockIdx.y * DIM;
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
 #pragma unroll
@@ -163,28 +168,30 @@ __global__ __launch_bounds__(64 * kIgWaves, 2) void k_input_grad(IgDev a) {
             const int tt = 16 * i + (lane >> 2), pp = lane & 3;
             const u32x4 piece = *reinterpret_cast<const u32x4*>(tl + tt * OS + 8 * pp);
             if (tok0 + tt < a.rows)
-                *reinterpret_cast<u32x4*>(dx + (tok0 + tt) * DIM + 32 * (cb0 + cb) + 8 * pp) = piece;
+                *reinterpret_cast<u32x4*>(dx + (tok0 + tt) * a.ldx + 32 * (cb0 + cb) + 8 * pp) = piece;
         }
         wave_lds_sync();  // the next block's tile writes follow these reads
     }
 }
 
 template <typename T, int NB, int CB>
-void launch_ig(const IgDev& d, hipStream_t s) {
+void launch_ig(const IgDev& d, int halves, hipStream_t s) {
     constexpr int TILES = kIgWaves / (NB / CB);
     const int64_t blocks = cdiv(d.rows, 32 * TILES);
-    k_input_grad<T, NB, CB><<<(unsigned)blocks, 64 * kIgWaves, 0, s>>>(d);
+    k_input_grad<T, NB, CB><<<dim3((unsigned)blocks, (unsigned)halves), 64 * kIgWaves, 0, s>>>(d);
 }
 
 template <typename T>
 int dispatch_ig(const IgDev& d, int dim, hipStream_t s) {
     switch (dim) {
-        case 64: launch_ig<T, 2, 2>(d, s); break;
-        case 96: launch_ig<T, 3, 3>(d, s); break;
-        case 128: launch_ig<T, 4, 4>(d, s); break;
-        case 192: launch_ig<T, 6, 6>(d, s); break;
-        case 256: launch_ig<T, 8, 8>(d, s); break;
-        default: return fail(P3D_EUNSUPPORTED, "p3d_input_grad: dim must be 64, 96, 128, 192 or 256");
+        case 64: launch_ig<T, 2, 2>(d, 1, s); break;
+        case 96: launch_ig<T, 3, 3>(d, 1, s); break;
+        case 128: launch_ig<T, 4, 4>(d, 1, s); break;
+        case 192: launch_ig<T, 6, 6>(d, 1, s); break;
+        case 256: launch_ig<T, 8, 8>(d, 1, s); break;
+        case 384: launch_ig<T, 6, 6>(d, 2, s); break;
+        case 512: launch_ig<T, 8, 8>(d, 2, s); break;
+        default: return fail(P3D_EUNSUPPORTED, "p3d_input_grad: dim must be 64, 96, 128, 192, 256, 384 or 512");
     }
     return P3D_OK;
 }
@@ -214,7 +221,7 @@ extern "C" int p3d_input_grad(const void* dq, int64_t dq_stride, int32_t q_out, 
     d.dq = (const char*)dq, d.dkv = (const char*)dkv, d.dg = (const char*)dg;
     d.dq_s = dq_stride, d.dkv_s = dkv_stride, d.dg_s = dg_stride;
     d.q_out = q_out, d.kv_out = kv_out, d.k_end = (int)k_end;
-    d.wt = (const char*)wt, d.k_pad = k_pad, d.dx = (char*)dx, d.rows = rows;
+    d.wt = (const char*)wt, d.k_pad = k_pad, d.dx = (char*)dx, d.rows = rows, d.ldx = dim;
     hipStream_t s = as_stream(stream);
     const int rc = dtype == P3D_F16 ? dispatch_ig<_Float16>(d, dim, s) : dispatch_ig<__bf16>(d, dim, s);
     if (rc != P3D_OK) return rc;

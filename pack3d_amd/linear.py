@@ -50,7 +50,7 @@ def weight_grad_supported(out_features, in_features):
     return out_features >= 8 and out_features % 8 == 0 and cols_ok
 
 
-INPUT_GRAD_DIMS = (64, 96, 128, 192, 256)
+INPUT_GRAD_DIMS = (64, 96, 128, 192, 256, 384, 512)
 
 
 def input_grad(dys, ws):

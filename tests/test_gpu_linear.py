@@ -51,7 +51,8 @@ def test_weight_grad_matches_fp32_product(gpu, dtype, rows, out_f, in_f, splits)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("rows,dim,outs", [(37, 192, (192, 768, 8)), (1000, 64, (64, 256, 16)),
                                            (4099, 96, (96, 384, 8)), (5000, 128, (128, 512, 8)),
-                                           (3001, 256, (256, 1024, 8)), (262144, 192, (192, 768, 8))])
+                                           (3001, 256, (256, 1024, 8)), (262144, 192, (192, 768, 8)),
+                                           (2049, 384, (384, 384, 24)), (4100, 512, (512, 512, 16))])
 def test_input_grad_matches_fp32_products(gpu, dtype, rows, dim, outs):
     """p3d_input_grad (dq Wq + dkv Wkv + dg Wg as one contraction) against
     the three products in fp32 on the same 16-bit inputs: one rounding of the

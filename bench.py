@@ -13,8 +13,8 @@ HBM.  The layer's output is checked against the oracle layer before the line
 is printed (a failed check raises).  The same line carries the c4 layer
 forward + backward with its summary-backward kernels, the
 incremental peak of allocated bytes of both, and the reference benchmark's
-own headline preset (allen15, inference and forward + backward) beside the
-medians the reference publishes for it.  Prints one JSON line.
+own presets (allen15 and small, inference and forward + backward) beside the
+medians the reference publishes for them.  Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -409,17 +409,28 @@ def gather_probe():
 C4_SHAPE = (32, 128, 64)
 
 
-# The reference benchmark's own headline preset (benchmarks/attention.py:84-87
-# of amilworks/Pack3D, "allen15") on its published 32 x 128 x 64 grid, and
-# the reference's published medians for it on one H200 with its Triton backend
-# (benchmarks/results/h200_vision_2026-11-18.md:7-14, raster, bf16).
-ALLEN15 = dict(dim=512, heads=8, kv_heads=2, head_dim=64, block=(1, 4, 4), pool_size=16, layout="raster_block",
-               radius=1, grid=(32, 128, 64))
-ALLEN15_H200_MS = {"inference": 4.644, "forward_backward": 15.098}
+# The reference benchmark's own presets (benchmarks/attention.py:84-91 of
+# amilworks/Pack3D) on the grids of its published table, and the medians it
+# publishes for them on one H200 with its Triton backend, bf16
+# (benchmarks/results/h200_vision_2026-11-18.md:7-14: "Raster, allen15" and
+# "Small Morton block").
+PRESETS = {
+    "allen15": dict(dim=512, heads=8, kv_heads=2, head_dim=64, block=(1, 4, 4), pool_size=16,
+                    layout="raster_block", radius=1, grid=(32, 128, 64),
+                    h200_ms={"inference": 4.644, "forward_backward": 15.098},
+                    workload="the reference benchmark's allen15 preset: dim 512, 8 / 2 heads, head_dim 64, "
+                             "(1, 4, 4) blocks, pool 16, raster, radius 1, 32 x 128 x 64 (262,144 tokens), "
+                             "batch 1, bf16"),
+    "small": dict(dim=64, heads=4, kv_heads=2, head_dim=16, block=(2, 2, 2), pool_size=4,
+                  layout="native_block_morton", radius=1, grid=(16, 16, 16),
+                  h200_ms={"inference": 0.568, "forward_backward": 4.051},
+                  workload="the reference benchmark's small preset: dim 64, 4 / 2 heads, head_dim 16, "
+                           "(2, 2, 2) blocks, pool 4, Morton, radius 1, 16 x 16 x 16 (4,096 tokens), batch 1, bf16"),
+}
 
 
-def bench_allen15(warmup=5, iterations=20):
-    """The reference harness's two modes on its allen15 preset (bf16 model and
+def bench_preset(name, warmup=5, iterations=20):
+    """The reference harness's two modes on one of its presets (bf16 model and
     input, seed 31, batch 1): inference under inference_mode, and forward +
     backward of y.float().square().mean() to the input and every parameter
     with the gradients cleared first (benchmarks/attention.py:14-22); median
@@ -428,7 +439,7 @@ def bench_allen15(warmup=5, iterations=20):
 
     import pack3d_amd as p3d
 
-    c = ALLEN15
+    c = PRESETS[name]
     dev = torch.device("cuda:0")
     torch.manual_seed(31)
     model = p3d.PACK3DAttention(c["dim"], heads=c["heads"], kv_heads=c["kv_heads"], head_dim=c["head_dim"],
@@ -447,10 +458,8 @@ def bench_allen15(warmup=5, iterations=20):
         x.grad = None
         model(x, layout).float().square().mean().backward()
 
-    out = {"workload": "the reference benchmark's allen15 preset: dim 512, 8 / 2 heads, head_dim 64, (1, 4, 4) "
-                       "blocks, pool 16, raster, radius 1, 32 x 128 x 64 (262,144 tokens), batch 1, bf16",
-           "warmup": warmup, "iterations": iterations}
-    for name, step in (("inference", inference), ("forward_backward", forward_backward)):
+    out = {"workload": c["workload"], "warmup": warmup, "iterations": iterations}
+    for mode, step in (("inference", inference), ("forward_backward", forward_backward)):
         for _ in range(warmup):
             step()
         torch.cuda.synchronize()
@@ -462,9 +471,9 @@ def bench_allen15(warmup=5, iterations=20):
             torch.cuda.synchronize()
             times.append(1000.0 * (time.perf_counter() - t0))
         ms = statistics.median(times)
-        out[f"{name}_ms"] = round(ms, 4)
-        out[f"{name}_reference_h200_ms"] = ALLEN15_H200_MS[name]
-        out[f"{name}_speedup_vs_reference_h200"] = round(ALLEN15_H200_MS[name] / ms, 3)
+        out[f"{mode}_ms"] = round(ms, 4)
+        out[f"{mode}_reference_h200_ms"] = c["h200_ms"][mode]
+        out[f"{mode}_speedup_vs_reference_h200"] = round(c["h200_ms"][mode] / ms, 3)
     del model, layout, x
     torch.cuda.empty_cache()
     return out
@@ -624,7 +633,7 @@ def main():
     p.add_argument("--gather-probe", action="store_true",
                    help="only run the launch sequence the indexed-gather and rotation counters are collected over")
     p.add_argument("--no-presets", action="store_true",
-                   help="skip the reference benchmark's allen15 preset (reported beside the c2 line)")
+                   help="skip the reference benchmark's presets (allen15, small; reported beside the c2 line)")
     p.add_argument("--c4", action="store_true",
                    help="time the c4 layer forward + backward instead (one JSON line of its own)")
     p.add_argument("--probe-rates", action="store_true",
@@ -665,7 +674,7 @@ def main():
     # so that the c2 steps right after it are timed at those clocks rather
     # than on the ramp of a freshly started process.
     c4 = bench_c4(a.c4_steps, a.c4_warmup, kernels=True)
-    allen15 = None if a.no_presets else bench_allen15()
+    presets = None if a.no_presets else {name: bench_preset(name) for name in PRESETS}
 
     with torch.inference_mode():
         for _ in range(a.warmup):
@@ -777,7 +786,7 @@ def main():
                        "incremental_peak_allocated_bytes": c4["config"]["incremental_peak_allocated_bytes"]},
         "roofline_global_dq": c4["roofline_global_dq"],
         "roofline_global_dkv": c4["roofline_global_dkv"],
-        "reference_preset_allen15": allen15,
+        "reference_presets": presets,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -64,6 +64,17 @@ __device__ __forceinline__ void layer_norm_load(const ProjDev& a, int64_t tok, b
     for (int ks = 0; ks < KS; ++ks) raw[ks] = *reinterpret_cast<const u32x4*>(xr + 16 * ks);
 }
 
+// An empty asm that claims to rewrite the pieces, so values derived from them
+// before it are derived again after it instead of being kept in registers.
+template <int KS>
+__device__ __forceinline__ void renew_pieces(const u32x4 (&raw)[KS]) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        u32x4& r = const_cast<u32x4&>(raw[ks]);
+        asm volatile("" : "+v"(r.x), "+v"(r.y), "+v"(r.z), "+v"(r.w));
+    }
+}
+
 // LayerNorm of the half rows `raw` (layer_norm_load) into the B fragments of
 // the projection GEMM: normalised in fp32 (statistics shared with lane l ^
 // 32, which holds the other half of the row) and rounded to the storage type
@@ -81,6 +92,10 @@ __device__ __forceinline__ void layer_norm_math(const ProjDev& a, const float* l
         for (int j = 0; j < 8; ++j) sum += to_f32(v[j]);
     }
     const float mean = (sum + lane_xor32(sum)) / (float)DIM;
+    // Past 256 channels the row's fp32 values from one pass are not kept
+    // for the next (the compiler held all 256 of them besides the 128
+    // registers of the row and spilled): each pass converts the pieces again.
+    if constexpr (KS > 16) renew_pieces(raw);
     float sq = 0.f;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -92,6 +107,7 @@ __device__ __forceinline__ void layer_norm_math(const ProjDev& a, const float* l
         }
     }
     const float rstd = 1.f / sqrtf((sq + lane_xor32(sq)) / (float)DIM + a.eps);
+    if constexpr (KS > 16) renew_pieces(raw);
     // Explicit fused multiply-adds: every kernel that normalises through here
     // rounds the same way, whatever the compiler contracts elsewhere.
 #pragma unroll

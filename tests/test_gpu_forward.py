@@ -272,7 +272,7 @@ def test_layer_norm_kernel_matches_torch(gpu, dtype, dim):
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("dim,heads,kv_heads,d", [(192, 4, 4, 48), (64, 2, 1, 32), (128, 4, 2, 16), (256, 2, 2, 64),
-                                                (96, 3, 1, 16)])
+                                                (96, 3, 1, 16), (512, 8, 2, 64)])
 def test_fused_projections_match_torch(gpu, dtype, dim, heads, kv_heads, d):
     """p3d_project against the separate torch ops it replaces (LayerNorm, the
     three linear maps, the gate softmax), with random LayerNorm affine and

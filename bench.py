@@ -12,9 +12,9 @@ to_out, residual) under torch.inference_mode with every input resident in
 HBM.  The layer's output is checked against the oracle layer before the line
 is printed (a failed check raises).  The same line carries the c4 layer
 forward + backward with its summary-backward kernels, the
-incremental peak of allocated bytes of both, and the reference benchmark's
-own presets (allen15 and small, inference and forward + backward) beside the
-medians the reference publishes for them.  Prints one JSON line.
+incremental peak of allocated bytes of both, and every row of the
+reference's own published table of whole-layer latencies (inference and
+forward + backward) beside the medians it publishes.  Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -409,74 +409,89 @@ def gather_probe():
 C4_SHAPE = (32, 128, 64)
 
 
-# The reference benchmark's own presets (benchmarks/attention.py:84-91 of
-# amilworks/Pack3D) on the grids of its published table, and the medians it
-# publishes for them on one H200 with its Triton backend, bf16
-# (benchmarks/results/h200_vision_2026-11-18.md:7-14: "Raster, allen15" and
-# "Small Morton block").
-PRESETS = {
-    "allen15": dict(dim=512, heads=8, kv_heads=2, head_dim=64, block=(1, 4, 4), pool_size=16,
-                    layout="raster_block", radius=1, grid=(32, 128, 64),
-                    h200_ms={"inference": 4.644, "forward_backward": 15.098},
-                    workload="the reference benchmark's allen15 preset: dim 512, 8 / 2 heads, head_dim 64, "
-                             "(1, 4, 4) blocks, pool 16, raster, radius 1, 32 x 128 x 64 (262,144 tokens), "
-                             "batch 1, bf16"),
-    "small": dict(dim=64, heads=4, kv_heads=2, head_dim=16, block=(2, 2, 2), pool_size=4,
-                  layout="native_block_morton", radius=1, grid=(16, 16, 16),
-                  h200_ms={"inference": 0.568, "forward_backward": 4.051},
-                  workload="the reference benchmark's small preset: dim 64, 4 / 2 heads, head_dim 16, "
-                           "(2, 2, 2) blocks, pool 4, Morton, radius 1, 16 x 16 x 16 (4,096 tokens), batch 1, bf16"),
-}
+# Every row of the reference's published table of whole-layer latencies
+# (benchmarks/results/h200_vision_2026-11-18.md:7-14 of amilworks/Pack3D: its
+# Triton backend on one H200), with the workload of each row as
+# benchmarks/vision.py:33-42,62-77 builds it: name, grid, layout, repack,
+# precision, batch, small preset, and the published inference and forward +
+# backward medians (ms).
+VISION_ROWS = (
+    ("Raster volume", (32, 128, 64), "raster_block", None, "BF16", 1, False, 4.644, 15.098),
+    ("Morton volume", (32, 128, 64), "native_block_morton", None, "BF16", 1, False, 4.638, 15.316),
+    ("Raster volume", (32, 128, 64), "raster_block", None, "FP16", 1, False, 4.655, 15.915),
+    ("Morton to raster", (16, 64, 64), "native_block_morton", "raster", "BF16", 1, False, 1.044, 4.105),
+    ("Morton to random", (16, 64, 64), "native_block_morton", "random", "BF16", 1, False, 1.054, 4.023),
+    ("Raster volume", (16, 64, 64), "raster_block", None, "BF16 autocast", 1, False, 1.276, 4.266),
+    ("Image slices", (1, 128, 128), "raster_block", None, "BF16", 2, False, 0.746, 3.306),
+    ("Small Morton block", (16, 16, 16), "native_block_morton", None, "BF16", 1, True, 0.568, 4.051),
+)
 
 
-def bench_preset(name, warmup=5, iterations=20):
-    """The reference harness's two modes on one of its presets (bf16 model and
-    input, seed 31, batch 1): inference under inference_mode, and forward +
-    backward of y.float().square().mean() to the input and every parameter
-    with the gradients cleared first (benchmarks/attention.py:14-22); median
-    of `iterations` synchronised steps each, as that harness reports."""
+def bench_vision_table(warmups=7, repeats=31):
+    """The rows of VISION_ROWS under the protocol of benchmarks/vision.py:
+    seed 205 (repack seed 17); dim 512, 8 / 2 heads, head_dim 64, (1, 4, 4)
+    blocks, pool 16 (the small row: dim 64, 4 / 2 heads, head_dim 16, (2, 2, 2)
+    blocks, pool 4); radius (0, 1, 1) on single-slice grids, else 1; the model
+    and input in the named dtype (fp32 under bf16 autocast for the autocast
+    row); inference under inference_mode; forward + backward as
+    forward(x).backward(dy) with a preallocated dy, the gradients cleared
+    outside the timed region; synchronised wall time per step, the median of
+    `repeats` steps after `warmups`."""
     import statistics
+    from contextlib import nullcontext
 
     import pack3d_amd as p3d
 
-    c = PRESETS[name]
     dev = torch.device("cuda:0")
-    torch.manual_seed(31)
-    model = p3d.PACK3DAttention(c["dim"], heads=c["heads"], kv_heads=c["kv_heads"], head_dim=c["head_dim"],
-                                block_volume=math.prod(c["block"])).to(dev, torch.bfloat16)
-    layout = p3d.build_layout(c["grid"], c["block"], radius=c["radius"], pool_size=c["pool_size"],
-                              layout=c["layout"], device=dev)
-    n = math.prod(c["grid"])
-    x = torch.randn(1, n, c["dim"], device=dev, dtype=torch.bfloat16, requires_grad=True)
+    rows = []
+    for name, grid, order, repack, prec, batch, small, ref_inf, ref_fb in VISION_ROWS:
+        torch.manual_seed(205)
+        if small:
+            dim, heads, groups, head_dim, block, pool = 64, 4, 2, 16, (2, 2, 2), 4
+        else:
+            dim, heads, groups, head_dim, block, pool = 512, 8, 2, 64, (1, 4, 4), 16
+        dtype = {"BF16": torch.bfloat16, "FP16": torch.float16, "BF16 autocast": torch.float32}[prec]
+        radius = (0, 1, 1) if grid[0] == 1 else (1, 1, 1)
+        layout = p3d.build_layout(grid, block, radius=radius, pool_size=pool, layout=order)
+        if repack == "raster":
+            layout = layout.repack(layout.order.argsort())
+        elif repack == "random":
+            layout = layout.repack(torch.randperm(len(layout.order), generator=torch.Generator().manual_seed(17)))
+        layout = layout.to(dev)
+        model = p3d.PACK3DAttention(dim, heads=heads, kv_heads=groups, head_dim=head_dim,
+                                    block_volume=math.prod(block)).to(dev, dtype)
+        x = torch.randn(batch, math.prod(grid), dim, device=dev, dtype=dtype, requires_grad=True)
+        dy = torch.randn_like(x)
 
-    def inference():
-        with torch.inference_mode():
-            model(x, layout)
+        def forward():
+            amp = torch.autocast("cuda", torch.bfloat16) if prec == "BF16 autocast" else nullcontext()
+            with amp:
+                return model(x, layout)
 
-    def forward_backward():
-        model.zero_grad(set_to_none=True)
-        x.grad = None
-        model(x, layout).float().square().mean().backward()
-
-    out = {"workload": c["workload"], "warmup": warmup, "iterations": iterations}
-    for mode, step in (("inference", inference), ("forward_backward", forward_backward)):
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
-        times = []
-        for _ in range(iterations):
+        row = {"workload": name, "batch": batch, "grid": list(grid), "precision": prec}
+        for mode, ref in (("inference", ref_inf), ("forward_backward", ref_fb)):
+            times = []
             torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            step()
-            torch.cuda.synchronize()
-            times.append(1000.0 * (time.perf_counter() - t0))
-        ms = statistics.median(times)
-        out[f"{mode}_ms"] = round(ms, 4)
-        out[f"{mode}_reference_h200_ms"] = c["h200_ms"][mode]
-        out[f"{mode}_speedup_vs_reference_h200"] = round(c["h200_ms"][mode] / ms, 3)
-    del model, layout, x
-    torch.cuda.empty_cache()
-    return out
+            for it in range(warmups + repeats):
+                start = time.perf_counter()
+                if mode == "inference":
+                    with torch.inference_mode():
+                        forward()
+                else:
+                    forward().backward(dy)
+                torch.cuda.synchronize()
+                if it >= warmups:
+                    times.append(1000.0 * (time.perf_counter() - start))
+                model.zero_grad(set_to_none=True)
+                x.grad = None
+            ms = statistics.median(times)
+            row[f"{mode}_ms"] = round(ms, 4)
+            row[f"{mode}_reference_h200_ms"] = ref
+            row[f"{mode}_speedup_vs_reference_h200"] = round(ref / ms, 3)
+        rows.append(row)
+        del model, x, dy, layout
+        torch.cuda.empty_cache()
+    return rows
 
 
 def bench_c4(steps, warmup, kernels=False):
@@ -633,7 +648,7 @@ def main():
     p.add_argument("--gather-probe", action="store_true",
                    help="only run the launch sequence the indexed-gather and rotation counters are collected over")
     p.add_argument("--no-presets", action="store_true",
-                   help="skip the reference benchmark's presets (allen15, small; reported beside the c2 line)")
+                   help="skip the rows of the reference's published latency table (reported beside the c2 line)")
     p.add_argument("--c4", action="store_true",
                    help="time the c4 layer forward + backward instead (one JSON line of its own)")
     p.add_argument("--probe-rates", action="store_true",
@@ -674,7 +689,7 @@ def main():
     # so that the c2 steps right after it are timed at those clocks rather
     # than on the ramp of a freshly started process.
     c4 = bench_c4(a.c4_steps, a.c4_warmup, kernels=True)
-    presets = None if a.no_presets else {name: bench_preset(name) for name in PRESETS}
+    vision = None if a.no_presets else bench_vision_table()
 
     with torch.inference_mode():
         for _ in range(a.warmup):
@@ -786,7 +801,7 @@ def main():
                        "incremental_peak_allocated_bytes": c4["config"]["incremental_peak_allocated_bytes"]},
         "roofline_global_dq": c4["roofline_global_dq"],
         "roofline_global_dkv": c4["roofline_global_dkv"],
-        "reference_presets": presets,
+        "reference_vision_table": vision,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

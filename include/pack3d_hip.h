@@ -231,7 +231,7 @@ int p3d_rotate(p3d_view x, p3d_view y, int32_t batch, int32_t heads, int32_t tok
 /* nn.LayerNorm over the last dimension of x [rows, dim] (contiguous, dtype):
  * y = (x - mean) / sqrt(var + eps) * weight + bias, statistics in fp32,
  * weight / bias [dim] of param_dtype.  dim must be a multiple of the 16-byte
- * piece and at most 64 pieces. */
+ * piece and at most 512. */
 int p3d_layer_norm(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
                    int64_t rows, int32_t dim, int32_t dtype, float eps, void* stream);
 
@@ -242,7 +242,7 @@ int p3d_layer_norm(const void* x, const void* weight, const void* bias, int32_t 
  * backward.  x_copy (may be NULL): x rounded to y_dtype [rows, dim], the
  * residual operand of the layer's output product under autocast
  * (attention.py:89), written from the same read of x.  dim a multiple of
- * x's 16-byte piece, at most 64 pieces. */
+ * x's 16-byte piece, at most 512. */
 int p3d_layer_norm_train(const void* x, const void* weight, const void* bias, int32_t param_dtype, void* y,
                          void* x_copy, float* mean, float* rstd, int64_t rows, int32_t dim, int32_t x_dtype,
                          int32_t y_dtype, float eps, void* stream);

@@ -7,15 +7,17 @@ to_q, to_kv, the gate map and its softmax run as one kernel
 (``p3d_project``); on layouts whose fine blocks are consecutive 64-token runs
 with pool_size 1 (this package's ``build_layout``) that kernel also pools the
 summaries from the kg / vg values it computes (``p3d_project_pool``), and kg /
-vg never reach memory; with autograd active in fp16 / bf16 the linear maps are
-``linear.InputProjections`` / ``linear.OutputResidual`` (torch GEMMs forward,
-weight gradients from ``p3d_weight_grad``); for fp32 models they are the
-torch modules (LayerNorm on the HIP kernel when no gradient is needed).  The
+vg never reach memory.  With autograd active in fp16 / bf16, and under
+autocast, LayerNorm is ``linear.LayerNormTrain`` and the linear maps are
+``linear.InputProjections`` (``p3d_project_linear``) and
+``linear.OutputResidual`` / ``OutputResidualWide``, with weight gradients from
+``p3d_weight_grad``; for fp32 models without autocast they are the torch
+modules (LayerNorm on the HIP kernel when no gradient is needed).  The
 rotation, pooling, local and global attention and their fusion run in
 ``libpack3d_hip.so``, and so does ``x + to_out(y)`` in the no-grad fp16 /
-bf16 forward (``p3d_out_residual``; otherwise one GEMM with the residual as
-its C operand).  The projections are consumed as strided views, without
-copies.
+bf16 forward and under autocast over an fp32 input (``p3d_out_residual``;
+otherwise one GEMM with the residual as its C operand).  The projections are
+consumed as strided views, without copies.
 """
 from __future__ import annotations
 
@@ -35,16 +37,16 @@ from .rope import axial_rope, balanced_pairs, packed_rope
 def layer_norm(norm: nn.LayerNorm, x):
     """``norm(x)`` on the HIP LayerNorm kernel when no gradient is needed.
 
-    With autograd active (training, autocast) the differentiable torch op
-    runs instead; shapes the kernel does not take (a channel count that is
-    not a whole number of 16-byte pieces, or above 64 pieces) do too.
+    With autograd active the differentiable torch op runs instead; shapes
+    the kernel does not take (a channel count that is not a whole number of
+    16-byte pieces, or above 512) do too.
     """
     dim = x.shape[-1]
     dtypes = _lib.DTYPES
     ep = 16 // x.element_size()
     usable = (x.is_cuda and x.dtype in dtypes and norm.weight is not None and norm.bias is not None
               and norm.weight.dtype == norm.bias.dtype and norm.weight.dtype in dtypes
-              and dim % ep == 0 and dim // ep <= 64 and len(norm.normalized_shape) == 1)
+              and dim % ep == 0 and dim <= 512 and len(norm.normalized_shape) == 1)
     if not usable or (torch.is_grad_enabled() and (x.requires_grad or norm.weight.requires_grad
                                                    or norm.bias.requires_grad)):
         return norm(x)
@@ -297,13 +299,15 @@ class PACK3DAttention(nn.Module):
     def _hip_linear(self, x):
         """Whether the linear maps run as InputProjections / OutputResidual
         (weight gradients from p3d_weight_grad) and LayerNorm as LayerNormTrain:
-        autograd active, a CUDA input and a 16-bit compute type, the gate with a
-        bias, and no hooks or parametrisations on the linear modules that the
+        autograd active, or autocast on (the no-grad forward under autocast,
+        whose fp32 parameters or input the fused projection kernel does not
+        take); a CUDA input and a 16-bit compute type, the gate with a bias,
+        and no hooks or parametrisations on the linear modules that the
         functions would skip."""
         mods = (self.to_q, self.to_kv, self.gate, self.to_out)
         params = [m.weight for m in mods] + [self.gate.bias]
-        return (torch.is_grad_enabled() and x.is_cuda and compute_dtype(x) is not None
-                and (x.requires_grad or any(p.requires_grad for p in params))
+        grad = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in params))
+        return ((grad or torch.is_autocast_enabled("cuda")) and x.is_cuda and compute_dtype(x) is not None
                 and self.gate.bias is not None and self.to_q.bias is None and self.to_kv.bias is None
                 and self.to_out.bias is None
                 and all(type(m) is nn.Linear and not m._forward_hooks and not m._forward_pre_hooks for m in mods))

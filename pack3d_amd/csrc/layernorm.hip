@@ -4,10 +4,12 @@
 // registers: mean, then the biased variance of the centred values), output
 // (x - mean) / sqrt(var + eps) * w + b rounded to the storage type.
 //
-// Eight lanes share a row; lane j of the group holds the 16-byte pieces j,
-// j + 8, ... of the row, so a wave covers 8 rows and every load and store is
-// a full 16 bytes.  The affine weight and bias are staged in LDS as fp32 once
-// per block; the row sums reduce over the 8 lanes through DPP.
+// LPR lanes share a row (8, or 16 for rows of more than 64 pieces: fp32
+// rows of 384 or 512 channels); lane j of the group holds the 16-byte pieces
+// j, j + LPR, ... of the row, so a wave covers 64 / LPR rows and every load
+// and store is a full 16 bytes.  The affine weight and bias are staged in LDS
+// as fp32 once per block; the row sums reduce over the 8-lane groups through
+// DPP, then across groups by lane shuffles.
 #include "common.hpp"
 
 namespace p3d {
@@ -16,6 +18,7 @@ namespace {
 constexpr int kLanesPerRow = 8;
 constexpr int kMaxPiecesPerLane = 8;
 constexpr int kMaxDim = 512;
+constexpr int kMaxPieces = 128;  // fp32 rows of 512 channels
 
 // Sum over the 8-lane group: lanes l ^ 1, l ^ 2 (quad_perm), then l ^ 7
 // within 8 (row_half_mirror).
@@ -25,10 +28,23 @@ __device__ __forceinline__ float group8_sum(float x) {
     return x + dpp_move<0x141>(x);
 }
 
-template <typename T>
+// Sum over the LPR lanes of a row (LPR 8, 16 or 32, aligned groups).
+template <int LPR>
+__device__ __forceinline__ float lanes_sum(float x) {
+    x = group8_sum(x);
+    if constexpr (LPR >= 16) x += __shfl_xor(x, 8);
+    if constexpr (LPR >= 32) x += __shfl_xor(x, 16);
+    return x;
+}
+
+// Lanes per row of the forward kernels: 8, or 16 past 64 pieces.
+__host__ __device__ constexpr int fwd_lanes(int pieces) { return pieces > 64 ? 16 : 8; }
+
+template <typename T, int LPR>
 __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, const void* b, int param_dtype,
                                                     T* y, int64_t rows, int dim, float eps) {
     constexpr int EP = Piece<T>::N;
+    constexpr int kLanesPerRow = LPR;
     __shared__ __align__(16) float lw[kMaxDim], lb[kMaxDim];
     for (int c = threadIdx.x; c < dim; c += blockDim.x) {
         lw[c] = load_any(w, c, param_dtype);
@@ -51,7 +67,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, c
             for (int e = 0; e < EP; ++e) sum += v[i][e];
         }
     }
-    const float mean = group8_sum(sum) / (float)dim;
+    const float mean = lanes_sum<LPR>(sum) / (float)dim;
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxPiecesPerLane; ++i) {
@@ -63,7 +79,7 @@ __global__ __launch_bounds__(256) void k_layer_norm(const T* x, const void* w, c
                 sq += c * c;
             }
     }
-    const float rstd = 1.f / sqrtf(group8_sum(sq) / (float)dim + eps);
+    const float rstd = 1.f / sqrtf(lanes_sum<LPR>(sq) / (float)dim + eps);
     __syncthreads();
     if (!live) return;
 #pragma unroll
@@ -108,11 +124,12 @@ __device__ __forceinline__ void store_n(T* p, const float (&in)[N]) {
     *reinterpret_cast<typename Vec<T, N>::type*>(p) = v;
 }
 
-template <typename TI, typename TO>
+template <typename TI, typename TO, int LPR>
 __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const void* w, const void* b, int param_dtype,
                                                           TO* y, TO* x_copy, float* mean_out, float* rstd_out,
                                                           int64_t rows, int dim, float eps) {
     constexpr int EP = Piece<TI>::N;
+    constexpr int kLanesPerRow = LPR;
     __shared__ __align__(16) float lw[kMaxDim], lb[kMaxDim];
     for (int c = threadIdx.x; c < dim; c += blockDim.x) {
         lw[c] = load_any(w, c, param_dtype);
@@ -134,7 +151,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const voi
             for (int e = 0; e < EP; ++e) sum += v[i][e];
         }
     }
-    const float mean = group8_sum(sum) / (float)dim;
+    const float mean = lanes_sum<LPR>(sum) / (float)dim;
     float sq = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxPiecesPerLane; ++i) {
@@ -146,7 +163,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_train(const TI* x, const voi
                 sq += c * c;
             }
     }
-    const float rstd = 1.f / sqrtf(group8_sum(sq) / (float)dim + eps);
+    const float rstd = 1.f / sqrtf(lanes_sum<LPR>(sq) / (float)dim + eps);
     __syncthreads();
     if (!live) return;
     if (sub == 0) {
@@ -184,13 +201,6 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* 
     constexpr int EP = Piece<TI>::N;
     constexpr int kLanesPerRow = LPR;
     constexpr int GROUPS = 256 / kLanesPerRow;
-    // Sum over the row's lanes.
-    auto row_sum = [](float v) __attribute__((always_inline)) {
-        v = group8_sum(v);
-        if constexpr (LPR >= 16) v += __shfl_xor(v, 8);
-        if constexpr (LPR >= 32) v += __shfl_xor(v, 16);
-        return v;
-    };
     __shared__ __align__(16) float lw[kMaxDim];
     __shared__ float red[2][kMaxDim];
     for (int c = threadIdx.x; c < dim; c += blockDim.x) {
@@ -228,7 +238,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* 
                 }
             }
         }
-        const float mg = row_sum(sg) / (float)dim, mgx = row_sum(sgx) / (float)dim;
+        const float mg = lanes_sum<LPR>(sg) / (float)dim, mgx = lanes_sum<LPR>(sgx) / (float)dim;
 #pragma unroll
         for (int i = 0; i < PPL; ++i) {
             const int p = sub + kLanesPerRow * i;
@@ -274,9 +284,15 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* 
 template <typename TI, typename TO>
 int launch_ln_train(const void* x, const void* w, const void* b, int pdt, void* y, void* xc, float* mean, float* rstd,
                     int64_t rows, int dim, float eps, hipStream_t s) {
-    const unsigned blocks = (unsigned)cdiv(rows * kLanesPerRow, 256);
-    k_layer_norm_train<TI, TO><<<blocks, 256, 0, s>>>((const TI*)x, w, b, pdt, (TO*)y, (TO*)xc, mean, rstd, rows, dim,
-                                                      eps);
+    if (fwd_lanes(dim / Piece<TI>::N) == 16) {
+        const unsigned blocks = (unsigned)cdiv(rows * 16, 256);
+        k_layer_norm_train<TI, TO, 16><<<blocks, 256, 0, s>>>((const TI*)x, w, b, pdt, (TO*)y, (TO*)xc, mean, rstd,
+                                                              rows, dim, eps);
+    } else {
+        const unsigned blocks = (unsigned)cdiv(rows * 8, 256);
+        k_layer_norm_train<TI, TO, 8><<<blocks, 256, 0, s>>>((const TI*)x, w, b, pdt, (TO*)y, (TO*)xc, mean, rstd,
+                                                             rows, dim, eps);
+    }
     return check_launch("p3d_layer_norm_train");
 }
 
@@ -307,7 +323,7 @@ int launch_ln_bwd(const void* dy, const void* dres, const void* x, const void* w
         return (unsigned)(parts < resident ? parts : resident);
     };
     if (ppl > 4) {
-        // 32 lanes per row: 2 pieces per lane (up to 64 pieces).
+        // 32 lanes per row: up to 4 pieces per lane (128 pieces).
         switch ((int)cdiv(pieces, 32)) {
 #define CASE(P)                                                                                                  \
     case P:                                                                                                      \
@@ -316,7 +332,7 @@ int launch_ln_bwd(const void* dy, const void* dres, const void* x, const void* w
                 (const TD*)dy, (const TO*)dres, (const TI*)x, w, pdt, mean, rstd, (TO*)dx, part, rows, dim,      \
                 parts);                                                                                          \
         break;
-            CASE(2)
+            CASE(2) CASE(3) CASE(4)
 #undef CASE
             default: return fail(P3D_EUNSUPPORTED, "dim too large for the LayerNorm backward");
         }
@@ -381,25 +397,27 @@ extern "C" int p3d_layer_norm(const void* x, const void* weight, const void* bia
     P3D_REQUIRE(dtype >= P3D_F32 && dtype <= P3D_BF16 && param_dtype >= P3D_F32 && param_dtype <= P3D_BF16,
                 "unknown dtype");
     const int ep = 16 / dtype_size(dtype);
-    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kLanesPerRow * kMaxPiecesPerLane && dim <= kMaxDim,
-                "dim must be a multiple of the 16-byte piece, at most 64 pieces and 512 channels");
+    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kMaxPieces && dim <= kMaxDim,
+                "dim must be a multiple of the 16-byte piece and at most 512 channels");
     P3D_REQUIRE(rows >= 1, "need at least one row");
     P3D_REQUIRE(((uintptr_t)x % 16) == 0 && ((uintptr_t)y % 16) == 0, "x and y must be 16-byte aligned");
-    const int64_t threads = rows * kLanesPerRow;
-    const unsigned blocks = (unsigned)cdiv(threads, 256);
     hipStream_t s = as_stream(stream);
     switch (dtype) {
         case P3D_F32:
-            k_layer_norm<float><<<blocks, 256, 0, s>>>((const float*)x, weight, bias, param_dtype, (float*)y, rows,
-                                                       dim, eps);
+            if (fwd_lanes(dim / ep) == 16)
+                k_layer_norm<float, 16><<<(unsigned)cdiv(rows * 16, 256), 256, 0, s>>>(
+                    (const float*)x, weight, bias, param_dtype, (float*)y, rows, dim, eps);
+            else
+                k_layer_norm<float, 8><<<(unsigned)cdiv(rows * 8, 256), 256, 0, s>>>(
+                    (const float*)x, weight, bias, param_dtype, (float*)y, rows, dim, eps);
             break;
         case P3D_F16:
-            k_layer_norm<_Float16><<<blocks, 256, 0, s>>>((const _Float16*)x, weight, bias, param_dtype,
-                                                          (_Float16*)y, rows, dim, eps);
+            k_layer_norm<_Float16, 8><<<(unsigned)cdiv(rows * 8, 256), 256, 0, s>>>(
+                (const _Float16*)x, weight, bias, param_dtype, (_Float16*)y, rows, dim, eps);
             break;
         default:
-            k_layer_norm<__bf16><<<blocks, 256, 0, s>>>((const __bf16*)x, weight, bias, param_dtype, (__bf16*)y,
-                                                        rows, dim, eps);
+            k_layer_norm<__bf16, 8><<<(unsigned)cdiv(rows * 8, 256), 256, 0, s>>>(
+                (const __bf16*)x, weight, bias, param_dtype, (__bf16*)y, rows, dim, eps);
             break;
     }
     return check_launch("p3d_layer_norm");
@@ -413,8 +431,8 @@ extern "C" int p3d_layer_norm_train(const void* x, const void* weight, const voi
                     param_dtype >= P3D_F32 && param_dtype <= P3D_BF16,
                 "unknown dtype");
     const int ep = 16 / dtype_size(x_dtype);
-    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kLanesPerRow * kMaxPiecesPerLane && dim <= kMaxDim,
-                "dim must be a multiple of the 16-byte piece of x, at most 64 pieces and 512 channels");
+    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kMaxPieces && dim <= kMaxDim,
+                "dim must be a multiple of the 16-byte piece of x and at most 512 channels");
     P3D_REQUIRE(rows >= 1, "need at least one row");
     P3D_REQUIRE(aligned16(x) && aligned16(y), "x and y must be 16-byte aligned");
     P3D_REQUIRE(!x_copy || aligned16(x_copy), "x_copy must be 16-byte aligned");
@@ -438,8 +456,8 @@ extern "C" int p3d_layer_norm_bwd(const void* dy, const void* dres, const void* 
                     dx_dtype >= P3D_F32 && dx_dtype <= P3D_BF16 && param_dtype >= P3D_F32 && param_dtype <= P3D_BF16,
                 "unknown dtype");
     const int ep = 16 / dtype_size(x_dtype);
-    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kLanesPerRow * kMaxPiecesPerLane && dim <= kMaxDim,
-                "dim must be a multiple of the 16-byte piece of x, at most 64 pieces and 512 channels");
+    P3D_REQUIRE(dim >= ep && dim % ep == 0 && dim / ep <= kMaxPieces && dim <= kMaxDim,
+                "dim must be a multiple of the 16-byte piece of x and at most 512 channels");
     P3D_REQUIRE(rows >= 1 && parts >= 1 && parts < 65536, "need at least one row and one part");
     P3D_REQUIRE(aligned16(dy) && aligned16(x) && aligned16(dx), "dy, x and dx must be 16-byte aligned");
     P3D_REQUIRE(!dres || aligned16(dres), "dres must be 16-byte aligned");

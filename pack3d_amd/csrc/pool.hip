@@ -920,16 +920,19 @@ void launch_pool_t(const PoolDev& d, hipStream_t s) {
     const bool tab_lds = d.table_entries * 8 <= kTableLdsBytes;
     const size_t tab_bytes = tab_lds ? (size_t)((d.table_entries * 2 + 3) & ~3) * 4 : 0;
     const size_t fixed = C::FIXED + tab_bytes;
-    const int waves = (int)std::min<size_t>(C::MAX_WAVES, (160 * 1024 - fixed) / C::WAVE_BYTES);
-    const size_t smem = fixed + (size_t)C::WAVE_BYTES * waves;
     int dev = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const int64_t items = (int64_t)d.B * d.G * d.Mp;
+    int waves = (int)std::min<size_t>(C::MAX_WAVES, (160 * 1024 - fixed) / C::WAVE_BYTES);
+    // Few items (long summaries: pool_size 16 gives 16 fine blocks each):
+    // fewer waves per block, so that the blocks reach every compute unit.
+    while (waves > 1 && cdiv(items, waves) < cus) waves >>= 1;
+    const size_t smem = fixed + (size_t)C::WAVE_BYTES * waves;
     if (tab_lds)
         (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_fwd<T, D, true>, 64 * waves, smem);
     else
         (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_fwd<T, D, false>, 64 * waves, smem);
-    const int64_t items = (int64_t)d.B * d.G * d.Mp;
     const int64_t resident = (int64_t)std::max(1, cus) * std::max(1, per_cu);
     const int64_t needed = cdiv(items, waves);
     // Equal shares: the fewest rounds that cover every item, spread evenly.
@@ -1010,11 +1013,12 @@ void launch_pool_bwd_t(const PoolDev& d, const PoolBwdDev& bd, int64_t items, hi
     const size_t tab_bytes = tab_lds ? (size_t)((d.table_entries * 2 + 3) & ~3) * 4 : 0;
     const size_t fixed = (size_t)(D / 2) * 16 + (size_t)D * 4 + 64 * 4;
     const size_t per_wave = (size_t)(2 * 64 * PoolCfg<T, D>::RD + 2 * D + 64) * 4;
-    const int waves = pool_waves(fixed + tab_bytes, per_wave);
-    const size_t smem = fixed + tab_bytes + per_wave * waves;
     int dev = 0, cus = 0, per_cu = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    int waves = pool_waves(fixed + tab_bytes, per_wave);
+    while (waves > 1 && cdiv(items, waves) < cus) waves >>= 1;  // as in the forward
+    const size_t smem = fixed + tab_bytes + per_wave * waves;
     if (tab_lds)
         (void)hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_pool_bwd<T, D, true>, 64 * waves, smem);
     else

@@ -73,12 +73,14 @@ struct WgSrc {
 };
 
 // Partial dW of token range [blockIdx.y * per, + per) for output rows
-// [blockIdx.x * 256, + 256) and input columns [blockIdx.z * I, + I) of
-// I_total, written to part[blockIdx.y][o][blockIdx.z * I + i].  Two stages of
-// dynamic LDS (2 * wgrad_stage_elems<IT>() elements).
+// [blockIdx.x * rpb, + rpb) (rpb a multiple of 32, at most 256: the rows are
+// spread evenly over the row blocks, so that a last block of a few rows does
+// not cost a whole workgroup's pass) and input columns [blockIdx.z * I, + I)
+// of I_total, written to part[blockIdx.y][o][blockIdx.z * I + i].  Two
+// stages of dynamic LDS (2 * wgrad_stage_elems<IT>() elements).
 template <typename T, int IT>
 __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x, int64_t ldx, float* part,
-                                                        int64_t rows, int O, int64_t per, int I_total) {
+                                                        int64_t rows, int O, int rpb, int64_t per, int I_total) {
     typedef Mma<T> M;
     constexpr int I = 32 * IT;
     constexpr int SA = tile_stride(kWgRows), SB = tile_stride(I);
@@ -91,10 +93,10 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x
     extern __shared__ __align__(16) unsigned char wg_smem[];
     T* lds = reinterpret_cast<T*>(wg_smem);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 5;
-    const int ob = blockIdx.x * kWgRows;
+    const int ob = blockIdx.x * rpb;
     const int64_t n0 = (int64_t)blockIdx.y * per, n1 = min(rows, n0 + per);
     x += (int64_t)blockIdx.z * I;  // this workgroup's input columns
-    const bool active = ob + 32 * wave < O;  // wave-uniform
+    const bool active = 32 * wave < rpb && ob + 32 * wave < O;  // wave-uniform
 
     u32x4 ra[PA], rb[PB];
     auto fetch = [&](int64_t t0) __attribute__((always_inline)) {
@@ -106,7 +108,8 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x
             const int sel = o < dy.end[0] ? 0 : (o < dy.end[1] ? 1 : 2);
             const int o_src = o - (sel == 0 ? 0 : dy.end[sel - 1]);
             ra[i] = u32x4{0, 0, 0, 0};
-            if (n < n1 && o < O) ra[i] = *reinterpret_cast<const u32x4*>(dy.src[sel] + n * dy.ld[sel] + o_src);
+            if (n < n1 && c < rpb && o < O)
+                ra[i] = *reinterpret_cast<const u32x4*>(dy.src[sel] + n * dy.ld[sel] + o_src);
         }
 #pragma unroll
         for (int i = 0; i < PB; ++i) {
@@ -143,8 +146,8 @@ __global__ __launch_bounds__(64 * kWgWaves) void k_wgrad(WgSrc<T> dy, const T* x
             const bool more = t0 + kWgTok < n1;
             if (more) fetch(t0 + kWgTok);
             const T* cur = lds + buf * STAGE;
-            // Waves past the last output row multiply the zero columns of the
-            // dy tile: no branch around the MFMAs, whose accumulators would
+            // Waves past the block's last output row multiply the zero columns
+            // of the dy tile: no branch around the MFMAs, whose accumulators would
             // otherwise be copied between register files at the join.
 #pragma unroll
             for (int ks = 0; ks < kWgTok / 16; ++ks) {
@@ -206,12 +209,13 @@ int launch_wgrad(const WgSrc<T>& dy, const void* x, int64_t ldx, float* dw, floa
     // Past 256 input columns the columns go to blocks of 256 (grid z), each
     // with its own accumulators; dy is read once per block.
     const int cbs = I > kWgMaxCols ? I / kWgMaxCols : 1, Ib = I / cbs;
-    const dim3 grid((unsigned)cdiv(O, kWgRows), (unsigned)used, (unsigned)cbs);
+    const int nrb = (int)cdiv(O, kWgRows), rpb = 32 * (int)cdiv(cdiv(O, nrb), 32);
+    const dim3 grid((unsigned)nrb, (unsigned)used, (unsigned)cbs);
     switch (Ib / 32) {
 #define CASE(IT)                                                                                                  \
     case IT:                                                                                                      \
         k_wgrad<T, IT><<<grid, 64 * kWgWaves, 2 * wgrad_stage_elems<IT>() * sizeof(T), s>>>(                      \
-            dy, (const T*)x, ldx, part, rows, O, per, I);                                                         \
+            dy, (const T*)x, ldx, part, rows, O, rpb, per, I);                                                         \
         break;
         CASE(1) CASE(2) CASE(3) CASE(4) CASE(5) CASE(6) CASE(7) CASE(8)
 #undef CASE

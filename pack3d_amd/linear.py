@@ -19,18 +19,22 @@ import torch
 
 from . import _lib
 
-# The kernel's workgroups own 256 output rows and a range of rows of dy / x;
-# splits are chosen for about WORKGROUPS workgroups in all (one per compute
-# unit), with at least MIN_ROWS_PER_SPLIT rows each.  The fp32 partials
-# ([splits, out, in]) stay below half of the bytes of dy and x at 64^3.
+# The kernel's workgroups own up to 256 output rows, up to 256 input columns
+# and a range of rows of dy / x; splits are chosen for at most WORKGROUPS
+# workgroups in all (one per compute unit: from 128 input columns on, one
+# workgroup fills a compute unit's LDS, and a second round for a few
+# workgroups would double the pass), with at least MIN_ROWS_PER_SPLIT rows
+# each.  The fp32 partials ([splits, out, in]) stay below half of the bytes
+# of dy and x at 64^3.
 WG_ROWS = 256
+WG_COLS = 256
 WORKGROUPS = 256
 MIN_ROWS_PER_SPLIT = 512
 
 
-def splits_for(rows, out_features):
-    blocks = -(-out_features // WG_ROWS)
-    return max(1, min(-(-WORKGROUPS // blocks), rows // MIN_ROWS_PER_SPLIT))
+def splits_for(rows, out_features, in_features):
+    blocks = -(-out_features // WG_ROWS) * max(1, in_features // WG_COLS)
+    return max(1, min(max(1, WORKGROUPS // blocks), rows // MIN_ROWS_PER_SPLIT))
 
 
 def compute_dtype(x):
@@ -119,7 +123,7 @@ def weight_grad(dy, x):
     x = x if x.stride(1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()
     if dy.data_ptr() % 16 or x.data_ptr() % 16:
         dy, x = dy.clone(), x.clone()
-    splits = splits_for(rows, out_f)
+    splits = splits_for(rows, out_f, in_f)
     dw = torch.empty(out_f, in_f, dtype=torch.float32, device=dy.device)
     work = torch.empty(splits, out_f, in_f, dtype=torch.float32, device=dy.device)
     _lib.call("p3d_weight_grad", dy.data_ptr(), dy.stride(0), x.data_ptr(), x.stride(0), dw.data_ptr(),
@@ -141,7 +145,7 @@ def weight_grads3(dys, x):
                    or dy.data_ptr() % 16 for dy in dys)):
         return None
     total = sum(outs)
-    splits = splits_for(rows, total)
+    splits = splits_for(rows, total, in_f)
     dw = torch.empty(total, in_f, dtype=torch.float32, device=x.device)
     work = torch.empty(splits, total, in_f, dtype=torch.float32, device=x.device)
     _lib.call("p3d_weight_grad3", dys[0].data_ptr(), dys[0].stride(0), outs[0], dys[1].data_ptr(), dys[1].stride(0),
@@ -161,7 +165,7 @@ def layer_norm_train_supported(norm, x):
     return (x.dtype in _lib.DTYPES and norm.weight is not None and norm.bias is not None
             and norm.weight.dtype in _lib.DTYPES and norm.bias.dtype in _lib.DTYPES
             and norm.weight.dtype == norm.bias.dtype and tuple(norm.normalized_shape) == (dim,)
-            and dim % ep == 0 and dim // ep <= 64 and dim <= 512
+            and dim % ep == 0 and dim <= 512
             and not norm._forward_hooks and not norm._forward_pre_hooks)
 
 

@@ -250,7 +250,7 @@ def test_project_linear_declines_unsupported_shapes():
 
 @pytest.mark.parametrize("x_dtype,y_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float16),
                                               (torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32)])
-@pytest.mark.parametrize("rows,dim", [(1, 192), (1003, 192), (517, 64), (300, 512)])
+@pytest.mark.parametrize("rows,dim", [(1, 192), (1003, 192), (517, 64), (300, 512), (777, 384), (4099, 512)])
 @pytest.mark.parametrize("residual", [False, True, "pass"])
 def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, rows, dim, residual):
     """LayerNormTrain against torch.layer_norm in fp64 on the same inputs: the
@@ -259,8 +259,6 @@ def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, ro
     is x cast to the output type (bit-exact), and its gradient is added to
     dx.  With the pass-through: x itself, its gradient (in x's type) added
     to dx."""
-    if dim // (16 // torch.tensor([], dtype=x_dtype).element_size()) > 64:
-        pytest.skip("more than 64 pieces per row")
     print(f"layer norm train {rows}x{dim} {x_dtype}->{y_dtype} residual={residual}", flush=True)
     gen = torch.Generator(device=gpu).manual_seed(rows + dim)
     x = (torch.randn(rows, dim, device=gpu, generator=gen) * 2 + 0.5).to(x_dtype)
@@ -373,8 +371,11 @@ def test_layer_autocast_keeps_the_wide_residual(gpu, grad):
             y = layer(xg, lay_h)
     finally:
         linear._lib.call = real
-    if grad:  # the fp32 residual goes through the output product's own kernel
-        assert "p3d_out_residual" in calls, calls
+    # The fp32 residual goes through the output product's own kernel, and
+    # the projections through the linear-mode projection kernel, with and
+    # without autograd.
+    assert "p3d_out_residual" in calls and "p3d_project_linear" in calls, calls
+    assert "p3d_layer_norm_train" in calls, calls
     with torch.no_grad():
         exp = oracle(x, lay_r)
     assert y.dtype == torch.float32

@@ -5,8 +5,9 @@ the gradients of the input and of every parameter against the oracle layer,
 relative L2 below the harness's bar for bf16 (3.5e-2).
 
 The HIP layer runs in bf16 (weights and input, as ``model.to(dtype)`` holds
-them there); the oracle runs in fp32 on the CPU with the same bf16-rounded
-weights and input.
+them there), or in fp32 under bf16 autocast (benchmarks/vision.py:40,79,95: the
+"BF16 autocast" row); the oracle runs in fp32 on the CPU with the same
+weights and input (rounded to bf16 for the bf16 layer).
 """
 import math
 
@@ -26,32 +27,39 @@ PRESETS = {
 }
 
 
+@pytest.mark.parametrize("precision", ["bf16", "autocast"])
 @pytest.mark.parametrize("preset", sorted(PRESETS))
-def test_reference_benchmark_preset_probe(gpu, preset):
+def test_reference_benchmark_preset_probe(gpu, preset, precision):
     dim, heads, kv_heads, head_dim, block, pool, order, grid = PRESETS[preset]
-    print(f"preset {preset} probe {grid}", flush=True)
+    print(f"preset {preset} {precision} probe {grid}", flush=True)
+    autocast = precision == "autocast"
+    dt = torch.float32 if autocast else torch.bfloat16
     torch.manual_seed(31)
     oracle = ref.PACK3DAttention(dim, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
                                  block_volume=math.prod(block))
     with torch.no_grad():
         for prm in oracle.parameters():
-            prm.copy_(prm.to(torch.bfloat16).float())
+            prm.copy_(prm.to(dt).float())
     layer = p3d.PACK3DAttention(dim, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
                                 block_volume=math.prod(block))
     layer.load_state_dict(oracle.state_dict())
-    layer = layer.to(gpu, torch.bfloat16)
+    layer = layer.to(gpu, dt)
     lay_h = p3d.build_layout(grid, block, radius=1, pool_size=pool, layout=order, device=gpu)
     lay_r = ref.build_layout(grid, block, radius=1, pool_size=pool, layout=order)
     n = math.prod(grid)
-    x = torch.randn(1, n, dim, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    x = torch.randn(1, n, dim, generator=torch.Generator().manual_seed(1)).to(dt)
     dy = torch.randn(1, n, dim, generator=torch.Generator().manual_seed(2))
     xh = x.to(gpu).requires_grad_()
     xr = x.float().requires_grad_()
-    yh = layer(xh, lay_h)
+    with torch.autocast("cuda", torch.bfloat16, enabled=autocast):
+        with torch.inference_mode():
+            yi = layer(xh.detach(), lay_h)
+        yh = layer(xh, lay_h)
     yr = oracle(xr, lay_r)
-    yh.backward(dy.to(gpu, torch.bfloat16))
+    yh.backward(dy.to(gpu, yh.dtype))
     yr.backward(dy)
-    checks = [("output", yh, yr), ("input", xh.grad, xr.grad)]
+    assert yi.dtype == yh.dtype == dt
+    checks = [("inference output", yi, yr), ("output", yh, yr), ("input", xh.grad, xr.grad)]
     expected = dict(oracle.named_parameters())
     checks += [(name, prm.grad, expected[name].grad) for name, prm in layer.named_parameters()]
     for name, got, exp in checks:

@@ -683,7 +683,8 @@ __device__ __forceinline__ uint32_t stencil_mask(const AttnDev& a, int c, int g,
     return m;
 }
 
-// Local-pathway plane staging by the LDS DMA (16-bit types, head_dim <= 48).  Each
+// Local-pathway plane staging by the LDS DMA (16-bit types; head_dim <= 48
+// on 12-wide planes, head_dim 64 on 10-wide planes, see below).  Each
 // halo plane is copied into one of two plane buffers while the previous plane
 // is scored, so no wave waits on global memory between planes.  A buffer holds
 // K and V in the same key-major layout (key row stride KSTR: D / 8 data slots
@@ -693,29 +694,39 @@ __device__ __forceinline__ uint32_t stencil_mask(const AttnDev& a, int c, int g,
 // of every halo key of the brick is looked up once into a table in LDS; keys
 // outside the grid take the row of the nearest grid key (finite, and masked
 // by the stencil).
-template <typename C>
-constexpr bool kPlaneDma = sizeof(typename C::T_) == 2 && C::D <= 48;
+//
+// A plane holds PW keys per row (x) and 12 rows (y), key (ky, kx) at
+// ky * PW + kx.  PW = 12 covers radius 2.  At head_dim 64 two buffers of
+// 12-wide planes do not leave room for a second workgroup per CU, so that
+// head_dim takes radius <= 1 on 10-wide planes: a wave's 8-key-wide footprint
+// then reaches columns 10 and 11 of its rows, which fall on the first keys of
+// the next row (or, past the last row, on 12 - PW spare keys that hold grid
+// keys too): finite values that the stencil masks, as for the clamped keys.
+template <typename C, int PW>
+constexpr bool kPlaneDma = sizeof(typename C::T_) == 2 && (PW == 12 ? C::D <= 48 : PW == 10 && C::D == 64);
 
-template <typename C>
+template <typename C, int PW>
 struct PlaneDma {
     typedef typename C::T_ T;
     static constexpr int EP = Piece<T>::N;
+    static constexpr int PH = 12;                        // plane rows
+    static constexpr int KEYS = PH * PW + (12 - PW);     // keys of one plane, spares included
     static constexpr int KROW = C::KSTR / EP;           // 16-byte slots per key row
-    static constexpr int SLOTS = kPlaneKeys * KROW;      // slots of K (or V) of one plane
+    static constexpr int SLOTS = KEYS * KROW;            // slots of K (or V) of one plane
     static constexpr int CH = (SLOTS + 63) / 64;         // copies per region
     static constexpr int PER = (2 * CH + kWaves - 1) / kWaves;
     static constexpr size_t REGION = (size_t)SLOTS * 16;
     static constexpr size_t BUF = 2 * REGION;            // one plane: K region, then V region
-    static constexpr int kMaxPlanes = 8;                 // 4 + 2 rz with rz <= 2
-    static constexpr size_t ROWS = (size_t)kMaxPlanes * kPlaneKeys * sizeof(int);
+    static constexpr int kMaxPlanes = PW == 12 ? 8 : 6;  // 4 + 2 rz with rz <= 2 (or <= 1)
+    static constexpr size_t ROWS = (size_t)kMaxPlanes * KEYS * sizeof(int);
     static constexpr size_t BYTES = 2 * BUF + ROWS;      // two plane buffers and the row table
     static_assert(C::KSTR % EP == 0 && C::KSTR > C::D, "key rows need a spare slot");
 
     // Packed rows of the halo keys of planes [0, planes) (z from Z0 - rz).
     __device__ __forceinline__ static void fill_rows(const AttnDev& a, int Z0, int Y0, int X0, int planes,
                                                      int* rows) {
-        for (int i = threadIdx.x; i < planes * kPlaneKeys; i += blockDim.x) {
-            const int hz = i / kPlaneKeys, k = i - hz * kPlaneKeys, ky = k / kPlane, kx = k - ky * kPlane;
+        for (int i = threadIdx.x; i < planes * KEYS; i += blockDim.x) {
+            const int hz = i / KEYS, k = i - hz * KEYS, ky = k / PW, kx = k - ky * PW;
             const int gz = min(max(Z0 - a.rz + hz, 0), a.Z - 1);
             const int gy = min(max(Y0 - a.ry + ky, 0), a.Y - 1);
             const int gx = min(max(X0 - a.rx + kx, 0), a.X - 1);
@@ -743,11 +754,12 @@ struct PlaneDma {
     }
 
     // Rotate the K rows of plane hz in place (rows: that plane's row table).
+    // The spare keys past the last row stay as loaded (masked, never used).
     __device__ __forceinline__ static void rotate(const AttnDev& a, T* K, const int* rows, int hz,
                                                   const RopeWindow& win) {
         constexpr int PPR = C::D / EP;
-        for (int i = threadIdx.x; i < kPlaneKeys * PPR; i += blockDim.x) {
-            const int key = i / PPR, piece = i - key * PPR, ky = key / kPlane, kx = key - ky * kPlane;
+        for (int i = threadIdx.x; i < PH * PW * PPR; i += blockDim.x) {
+            const int key = i / PPR, piece = i - key * PPR, ky = key / PW, kx = key - ky * PW;
             uint4* p = reinterpret_cast<uint4*>(K + key * C::KSTR + piece * EP);
             const uint4 raw = *p;
             const T* kv = reinterpret_cast<const T*>(&raw);
@@ -801,35 +813,36 @@ template <typename C>
 constexpr size_t grid_park_bytes() {
     return (size_t)kWaves * 2 * (C::D / 8) * 64 * 4 * sizeof(typename C::T_);
 }
-template <typename C>
-constexpr bool kPark = kPlaneDma<C> || grid_main_bytes<C>() + grid_park_bytes<C>() <= 80 * 1024;
+template <typename C, int PW>
+constexpr bool kPark = kPlaneDma<C, PW> || grid_main_bytes<C>() + grid_park_bytes<C>() <= 80 * 1024;
 // With the plane DMA the regions after the rotation window are used twice:
 // in the local phase by the two plane buffers and the row table, in the
 // summary phase by the park buffer (over plane buffer 0, which the last
 // plane -- always of odd index -- does not use) and the summary stages.
-template <typename C>
+template <typename C, int PW>
 constexpr size_t grid_dma_bytes() {
     constexpr size_t ep = Piece<typename C::T_>::N;
     constexpr size_t stages =
         (kPiped<C> ? 3 : 2) * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(typename C::T_);
     constexpr size_t summary = grid_park_bytes<C>() + stages;
-    return kRopeWindowBytes + (PlaneDma<C>::BYTES > summary ? PlaneDma<C>::BYTES : summary);
+    return kRopeWindowBytes + (PlaneDma<C, PW>::BYTES > summary ? PlaneDma<C, PW>::BYTES : summary);
 }
-template <typename C>
+template <typename C, int PW>
 constexpr size_t grid_lds_bytes() {
-    if constexpr (kPlaneDma<C>) {
-        static_assert(grid_dma_bytes<C>() <= 80 * 1024, "two workgroups per CU");
-        static_assert(grid_park_bytes<C>() <= PlaneDma<C>::BUF, "park buffer within plane buffer 0");
-        return grid_dma_bytes<C>();
+    if constexpr (kPlaneDma<C, PW>) {
+        static_assert(grid_dma_bytes<C, PW>() <= 80 * 1024, "two workgroups per CU");
+        static_assert(grid_park_bytes<C>() <= PlaneDma<C, PW>::BUF, "park buffer within plane buffer 0");
+        return grid_dma_bytes<C, PW>();
     } else {
-        return grid_main_bytes<C>() + (kPark<C> ? grid_park_bytes<C>() : 0);
+        return grid_main_bytes<C>() + (kPark<C, PW> ? grid_park_bytes<C>() : 0);
     }
 }
 
 // Scores and products of one staged plane on this wave's two column blocks
 // (the chunks of its 8 x 8 key footprint).  Kb holds the plane's rotated K
-// rows; vfrag(c, mb, ks) returns the value fragment of chunk c.
-template <typename C, typename VFrag>
+// rows, PW keys per plane row; vfrag(c, mb, ks) returns the value fragment
+// of chunk c.
+template <typename C, int PW, typename VFrag>
 __device__ __forceinline__ void plane_chunks(const AttnDev& a, const typename C::T_* Kb, VFrag vfrag, int hz,
                                              int wy, int wx, int qi, int g, const uint32_t* kmask,
                                              const typename C::Frag (*qf)[C::NT], Soft<C::MB>* st) {
@@ -838,7 +851,7 @@ __device__ __forceinline__ void plane_chunks(const AttnDev& a, const typename C:
         if (4 * c >= 4 + 2 * a.ry) continue;
         const int kap = kperm<C::E, C::KS>(qi);
         typename C::Frag kf[C::NT], vf[C::MB * C::KSTEPS];
-        load_kfrags<C>(Kb + ((4 * wy + 4 * c + kap / 8) * kPlane + 4 * wx + kap % 8) * C::KSTR + C::E * g, kf);
+        load_kfrags<C>(Kb + ((4 * wy + 4 * c + kap / 8) * PW + 4 * wx + kap % 8) * C::KSTR + C::E * g, kf);
 #pragma unroll
         for (int mb = 0; mb < C::MB; ++mb)
 #pragma unroll
@@ -865,7 +878,7 @@ __device__ __forceinline__ void plane_chunks(const AttnDev& a, const typename C:
     }
 }
 
-template <typename T, int D>
+template <typename T, int D, int PW>
 __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     typedef Cfg<T, D> C;
     constexpr int EP = Piece<T>::N;
@@ -889,17 +902,18 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     const int wy = wave >> 1, wx = wave & 1;
     const int qy = (qi >> 2) & 3, qx = qi & 3;  // within the wave footprint
 
-    typedef PlaneDma<C> PD;
+    typedef PlaneDma<C, PW> PD;
+    constexpr bool DMA = kPlaneDma<C, PW>;
     unsigned char* const planes_lds = smem + kRopeWindowBytes;  // plane DMA: two buffers, then the row table
     int* const rowtab = reinterpret_cast<int*>(planes_lds + 2 * PD::BUF);
     const int planes = 4 + 2 * a.rz;
     const T* KL = tp<T>(a.kl) + b * a.ksb + kvh * a.ksh;
     const T* VL = tp<T>(a.vl) + b * a.vsb + kvh * a.vsh;
     if (!a.rope.packed) build_rope_window(a, D, Z0 - a.rz, Y0 - a.ry, X0 - a.rx, win);
-    if constexpr (kPlaneDma<C>) PD::fill_rows(a, Z0, Y0, X0, planes, rowtab);
+    if constexpr (DMA) PD::fill_rows(a, Z0, Y0, X0, planes, rowtab);
     __syncthreads();
     const int uwave = __builtin_amdgcn_readfirstlane(wave);
-    if constexpr (kPlaneDma<C>) {
+    if constexpr (DMA) {
         if ((unsigned)(Z0 - a.rz) < (unsigned)a.Z) PD::copy(a, KL, VL, rowtab, planes_lds, uwave, lane);
     }
 
@@ -931,7 +945,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     // ---- local pathway: halo planes z = Z0 - rz .. Z0 + 3 + rz
     const uint32_t kmask[2] = {stencil_mask<C>(a, 0, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx),
                                stencil_mask<C>(a, 1, g, qy, qx, Y0 + 4 * wy, X0 + 4 * wx)};
-    if constexpr (kPlaneDma<C>) {
+    if constexpr (DMA) {
         for (int hz = 0; hz < planes; ++hz) {
             const int gz = Z0 - a.rz + hz;
             unsigned char* const buf = planes_lds + (hz & 1) * PD::BUF;
@@ -940,18 +954,18 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
             dma_wait();
             __syncthreads();
             if (hz + 1 < planes && (unsigned)(gz + 1) < (unsigned)a.Z)
-                PD::copy(a, KL, VL, rowtab + (hz + 1) * kPlaneKeys, planes_lds + ((hz + 1) & 1) * PD::BUF, uwave,
+                PD::copy(a, KL, VL, rowtab + (hz + 1) * PD::KEYS, planes_lds + ((hz + 1) & 1) * PD::BUF, uwave,
                          lane);
             if ((unsigned)gz >= (unsigned)a.Z) continue;  // plane outside the grid: nothing to attend
             T* const Kb = reinterpret_cast<T*>(buf);
             const T* const Vb = reinterpret_cast<const T*>(buf + PD::REGION);
             if (!a.kl_rotated) {
-                PD::rotate(a, Kb, rowtab + hz * kPlaneKeys, hz, win);
+                PD::rotate(a, Kb, rowtab + hz * PD::KEYS, hz, win);
                 __syncthreads();
             }
-            plane_chunks<C>(a, Kb,
+            plane_chunks<C, PW>(a, Kb,
                             [&](int c, int mb, int ks) {
-                                return PD::vfrag(Vb, (4 * wy + 4 * c + (ks * C::KS + C::E * g) / 8) * kPlane + 4 * wx,
+                                return PD::vfrag(Vb, (4 * wy + 4 * c + (ks * C::KS + C::E * g) / 8) * PW + 4 * wx,
                                                  mb, lane);
                             },
                             hz, wy, wx, qi, g, kmask, qf, st);
@@ -965,7 +979,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
             stager.stage(a, KL, VL, hz, gz, Y0, X0, win, Kp, Vp, VPS);
             __syncthreads();
             if ((unsigned)gz >= (unsigned)a.Z) continue;  // plane outside the grid: nothing to attend
-            plane_chunks<C>(a, Kp,
+            plane_chunks<C, kPlane>(a, Kp,
                             [&](int c, int mb, int ks) {
                                 const int k0 = ks * C::KS + C::E * g;  // chunk key (4c + k0/8, k0 % 8) of the footprint
                                 return frag_load8<T>(Vp + (32 * mb + qi) * VPS + (4 * wy + 4 * c + k0 / 8) * kPlane +
@@ -974,8 +988,8 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
                             hz, wy, wx, qi, g, kmask, qf, st);
         }
     }
-    T* park = kPlaneDma<C> ? reinterpret_cast<T*>(planes_lds)
-                           : (kPark<C> ? reinterpret_cast<T*>(smem + grid_main_bytes<C>()) : nullptr);
+    T* park = DMA ? reinterpret_cast<T*>(planes_lds)
+                  : (kPark<C, PW> ? reinterpret_cast<T*>(smem + grid_main_bytes<C>()) : nullptr);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
         finish_local<C>(a, b, h, qrow[nb], qok[nb], g, st[nb],
@@ -985,11 +999,11 @@ __global__ __launch_bounds__(64 * kWaves, 2) void k_attn_grid(AttnDev a) {
     __syncthreads();  // the summary stages reuse the plane buffer
 
     // ---- global pathway (the rotation window is no longer needed)
-    global_pass<C, 64 * kWaves>(a, bg, kPlaneDma<C> ? reinterpret_cast<T*>(planes_lds + grid_park_bytes<C>()) : Kp,
+    global_pass<C, 64 * kWaves>(a, bg, DMA ? reinterpret_cast<T*>(planes_lds + grid_park_bytes<C>()) : Kp,
                                 qf, st, lane);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        if constexpr (kPark<C>)
+        if constexpr (kPark<C, PW>)
             epilogue<C, LOCAL_PARK>(a, b, h, qrow[nb], qok[nb], g, st[nb],
                                     park + (wave * 2 + nb) * (C::D / 8) * 64 * 4, lane);
         else
@@ -1066,10 +1080,10 @@ int fill_dev(const p3d_attn_args& x, AttnDev& d) {
     return P3D_OK;
 }
 
-template <typename T, int D>
+template <typename T, int D, int PW>
 size_t lds_grid() {
     typedef Cfg<T, D> C;
-    return grid_lds_bytes<C>();
+    return grid_lds_bytes<C, PW>();
 }
 
 template <typename T, int D>
@@ -1079,12 +1093,31 @@ size_t lds_rows() {
     return (kPiped<C> ? 3 : 2) * ((size_t)64 * C::KSTR + (size_t)32 * C::MB * (64 + ep)) * sizeof(T);
 }
 
+template <typename T, int D, int PW>
+void launch_grid_t(const AttnDev& d, dim3 grid, hipStream_t s) {
+    k_attn_grid<T, D, PW><<<grid, 64 * kWaves, lds_grid<T, D, PW>(), s>>>(d);
+}
+
+// Head_dim 64 in a 16-bit type with radius <= 1 stages its halo planes by the
+// LDS DMA on 10-wide planes; everything else takes 12-wide planes.
 template <int D>
 int launch_grid(const AttnDev& d, int dtype, dim3 grid, hipStream_t s) {
+    constexpr int NARROW = D == 64 ? 10 : 12;
+    const bool narrow = NARROW != 12 && d.rz <= 1 && d.ry <= 1 && d.rx <= 1;
     switch (dtype) {
-        case P3D_F32: k_attn_grid<float, D><<<grid, 64 * kWaves, lds_grid<float, D>(), s>>>(d); break;
-        case P3D_F16: k_attn_grid<_Float16, D><<<grid, 64 * kWaves, lds_grid<_Float16, D>(), s>>>(d); break;
-        default: k_attn_grid<__bf16, D><<<grid, 64 * kWaves, lds_grid<__bf16, D>(), s>>>(d); break;
+        case P3D_F32: launch_grid_t<float, D, 12>(d, grid, s); break;
+        case P3D_F16:
+            if (narrow)
+                launch_grid_t<_Float16, D, NARROW>(d, grid, s);
+            else
+                launch_grid_t<_Float16, D, 12>(d, grid, s);
+            break;
+        default:
+            if (narrow)
+                launch_grid_t<__bf16, D, NARROW>(d, grid, s);
+            else
+                launch_grid_t<__bf16, D, 12>(d, grid, s);
+            break;
     }
     return check_launch("p3d_attn_fwd_grid");
 }

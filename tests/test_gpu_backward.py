@@ -21,14 +21,24 @@ NAMES = ["q", "kl", "vl", "kg", "vg", "pool_weight", "slot_bias", "gate", "local
 
 
 def _compare(got, exp, dtype, what):
+    # The largest expected gradient entry: the scale of the rounding in the
+    # kernels' gradients.
+    scale = max(float(e.float().abs().max()) for e in exp)
     for name, a, e in zip(NAMES, got, exp):
         assert torch.isfinite(a).all(), (what, name)
-        err = rel_l2(a.float().cpu(), e.float())
         mx = (a.float().cpu() - e.float()).abs().max().item()
-        print(f"  {what} d{name}: rel_l2={err:.3g} max_abs={mx:.3g}", flush=True)
-        assert err < TOL[dtype], (what, name, err)
         if dtype == torch.float32:
             torch.testing.assert_close(a.cpu(), e, atol=3e-5, rtol=3e-5)
+        if float(e.float().norm()) == 0.0:
+            # An exactly zero gradient (radius 0: each local softmax has one
+            # key, so its scores get no gradient): the kernels' rounding,
+            # against the scale of the other gradients.
+            print(f"  {what} d{name}: expected zero, max_abs={mx:.3g} (scale {scale:.3g})", flush=True)
+            assert mx <= TOL[dtype] * scale, (what, name, mx, scale)
+            continue
+        err = rel_l2(a.float().cpu(), e.float())
+        print(f"  {what} d{name}: rel_l2={err:.3g} max_abs={mx:.3g}", flush=True)
+        assert err < TOL[dtype], (what, name, err)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])

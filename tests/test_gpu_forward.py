@@ -52,6 +52,12 @@ GRIDS = [
     ((5, 7, 9), (5, 7, 1), (0, 1, 2), "raster_block", 2, 2, 64),
     ((4, 16, 12), (2, 2, 2), 1, "raster_block", 4, 1, 16),
     ((12, 12, 12), (4, 4, 4), 2, "native_block_morton", 2, 2, 128),
+    # head_dim 64 with radius <= 1 (10-wide halo planes in 16-bit types):
+    # partial bricks on every axis, 4 query heads per kv head; an
+    # anisotropic radius; radius 0.
+    ((9, 12, 20), (1, 4, 4), 1, "raster_block", 8, 2, 64),
+    ((6, 10, 20), (2, 2, 2), (1, 0, 1), "native_block_morton", 4, 2, 64),
+    ((3, 8, 8), (1, 4, 4), 0, "raster_block", 2, 1, 64),
 ]
 
 

@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* 
     const int64_t step = (int64_t)gridDim.x * GROUPS;
     for (int64_t row = (int64_t)blockIdx.x * GROUPS + grp; row < rows; row += step) {
         const float mean = mean_in[row], rstd = rstd_in[row];
-        float xh[PPL][EP], g[PPL][EP];
+        float xh[PPL][EP], g[PPL][EP], rr[PPL][EP];
         float sg = 0.f, sgx = 0.f;
 #pragma unroll
         for (int i = 0; i < PPL; ++i) {
@@ -227,6 +227,9 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* 
                 float xv[EP], dv[EP];
                 load_n<TI, EP>(x + row * dim + p * EP, xv);
                 load_n<TD, EP>(dy + row * dim + p * EP, dv);
+                // The residual gradient is loaded with x and dy, so a row costs
+                // one round trip to memory rather than two.
+                if (dres) load_n<TO, EP>(dres + row * dim + p * EP, rr[i]);
 #pragma unroll
                 for (int e = 0; e < EP; ++e) {
                     xh[i][e] = (xv[e] - mean) * rstd;
@@ -247,10 +250,8 @@ __global__ __launch_bounds__(256) void k_layer_norm_bwd(const TD* dy, const TO* 
 #pragma unroll
                 for (int e = 0; e < EP; ++e) o[e] = rstd * (g[i][e] - mg - xh[i][e] * mgx);
                 if (dres) {
-                    float r[EP];
-                    load_n<TO, EP>(dres + row * dim + p * EP, r);
 #pragma unroll
-                    for (int e = 0; e < EP; ++e) o[e] += r[e];
+                    for (int e = 0; e < EP; ++e) o[e] += rr[i][e];
                 }
                 store_n<TO, EP>(dx + row * dim + p * EP, o);
             }

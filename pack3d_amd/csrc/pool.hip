@@ -25,6 +25,7 @@ constexpr int kNormSlots = 64;
 
 struct PoolDev {
     int B, G, N, F, V, P, M, Mp;
+    int bps, gsz;  // forward: fine blocks per 64-lane step, lanes per block's slot group
     float inv_tau, key_scale;
     const char *kg, *vg;
     int64_t ksb, ksh, ksn, vsb, vsh, vsn;
@@ -178,8 +179,13 @@ __device__ __forceinline__ uint4 round_piece<_Float16, 8>(float (&x)[8]) {
 
 // ------------------------------------------------------------------ forward
 //
-// One wave pools one (batch, kv head, summary) item at a time, one fine block
-// (a "step") after the other.  Each lane holds one slot (lane = slot).
+// One wave pools one (batch, kv head, summary) item at a time, one step
+// after the other.  A step holds bps fine blocks: with V slots per block a
+// power of two up to 32, bps = 64 / V and lane l holds slot l % V of block
+// l / V of the step (pool_size 16 with 16-slot blocks takes 4 steps instead
+// of 16); otherwise bps = 1 and lane l holds slot l.  The slot softmax runs
+// over each block's lanes, and the weighted sums over all 64 lanes add the
+// step's blocks together, as the coarse mean needs.
 //
 // The K and V rows of a step are loaded with 16 bytes per lane and
 // consecutive lanes on consecutive pieces of a row, so one load instruction
@@ -273,6 +279,38 @@ __device__ __forceinline__ void unpack_piece(const u32x4& raw, float (&x)[EP]) {
     const T* t = reinterpret_cast<const T*>(&raw);
 #pragma unroll
     for (int e = 0; e < EP; ++e) x[e] = to_f32(t[e]);
+}
+
+// Max / sum over aligned groups of gsz lanes (gsz a power of two): the first
+// log2(gsz) steps of wave_max / wave_sum, which reduce within 2, 4, 8, 16
+// and 32 lanes in turn.
+__device__ __forceinline__ float group_max(float x, int gsz) {
+    if (gsz >= 64) return wave_max(x);
+    if (gsz >= 2) x = fmaxf(x, dpp_move<0xB1>(x));
+    if (gsz >= 4) x = fmaxf(x, dpp_move<0x4E>(x));
+    if (gsz >= 8) x = fmaxf(x, dpp_move<0x141>(x));
+    if (gsz >= 16) x = fmaxf(x, dpp_move<0x140>(x));
+    if (gsz >= 32) x = fmaxf(x, lane_xor16(x));
+    return x;
+}
+__device__ __forceinline__ float group_sum(float x, int gsz) {
+    if (gsz >= 64) return wave_sum(x);
+    if (gsz >= 2) x += dpp_move<0xB1>(x);
+    if (gsz >= 4) x += dpp_move<0x4E>(x);
+    if (gsz >= 8) x += dpp_move<0x141>(x);
+    if (gsz >= 16) x += dpp_move<0x140>(x);
+    if (gsz >= 32) x += lane_xor16(x);
+    return x;
+}
+
+// Fine blocks of a step with at least one slot token: groups of V lanes of
+// the ballot `filled` (bps groups).
+__device__ __forceinline__ int blocks_filled(uint64_t filled, int bps, int V) {
+    if (bps == 1) return 1;
+    const uint64_t group = V == 64 ? ~0ull : ((1ull << V) - 1);
+    int n = 0;
+    for (int b = 0; b < bps; ++b) n += ((filled >> (b * V)) & group) != 0;
+    return n;
 }
 
 // Store the summary of (batch * kv head bg, summary m) from the lane's sums
@@ -424,12 +462,15 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
     auto item_of = [&](unsigned i) __attribute__((always_inline)) -> unsigned { return total - 1u - i; };
     auto steps_of = [&](unsigned i) __attribute__((always_inline)) -> int {
         const int m = (int)((item_of(i) / a.G) % a.Mp);
-        return m < a.M ? min(a.F, (m + 1) * a.P) - m * a.P : 1;
+        return m < a.M ? (min(a.F, (m + 1) * a.P) - m * a.P + a.bps - 1) / a.bps : 1;
     };
     // The lane's slot token of step (i, fl), or -1 (empty slot, padding summary).
+    const int lane_block = lane / (a.bps == 1 ? 64 : a.V), lane_slot = lane - lane_block * a.V;
     auto row_of = [&](unsigned i, int fl) __attribute__((always_inline)) -> int {
         const int m = (int)((item_of(i) / a.G) % a.Mp);
-        return (m < a.M && lane < a.V) ? a.blocks[(int64_t)(m * a.P + fl) * a.V + lane] : -1;
+        const int f = m * a.P + fl * a.bps + lane_block;
+        return (m < a.M && lane < a.bps * a.V && f < min(a.F, (m + 1) * a.P)) ? a.blocks[(int64_t)f * a.V + lane_slot]
+                                                                              : -1;
     };
     // Pair metadata of each piece's first pair and the table-run flags, as
     // wave-uniform values (scalar registers) for the whole loop.
@@ -509,8 +550,9 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
                 pool_fetch<T, D>(a, item_of(it1), idx1, lane, pk, pv);
             }
 
-            if (__ballot(idx >= 0) != 0) {  // empty fine block: no mass, no count
-                ++count;
+            const uint64_t filled = __ballot(idx >= 0);
+            if (filled != 0) {  // empty fine blocks: no mass, no count
+                count += blocks_filled(filled, a.bps, a.V);
                 // Rotate the slot's key, round it to the storage type, and form
                 // its logit (compression.py:31-35): (k . w) / tau + bias_s.
                 // 2-byte types read every (cos, sin) entry of the step first (one
@@ -545,10 +587,11 @@ __global__ __launch_bounds__((64 * PoolRowCfg<T, D>::MAX_WAVES)) void k_pool_fwd
 #pragma unroll
                     for (int e = 0; e < EP; ++e) dot += kx[e] * lweight[p * EP + e];
                 }
-                const float logit = idx >= 0 ? dot * a.inv_tau + lbias[lane] : -INFINITY;
-                const float mx = wave_max(logit);
+                const float logit = idx >= 0 ? dot * a.inv_tau + lbias[lane & (a.gsz - 1)] : -INFINITY;
+                const float mx = group_max(logit, a.gsz);
                 const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
-                const float wgt = ex / wave_sum(ex);
+                const float den = group_sum(ex, a.gsz);
+                const float wgt = den > 0.f ? ex / den : 0.f;  // a block of the step with no slot: 0
                 if constexpr (C::MF) {
                     typedef typename Mma<T>::Frag Frag;
                     // The rotated, rounded key over the lane's own staged row (only
@@ -987,6 +1030,8 @@ int fill_pool(const p3d_pool_args* args, PoolDev& d) {
     d.F = a.fine_blocks;
     d.V = a.slots;
     d.P = a.pool_size;
+    d.bps = (a.slots <= 32 && (a.slots & (a.slots - 1)) == 0) ? 64 / a.slots : 1;
+    d.gsz = d.bps == 1 ? 64 : a.slots;
     d.M = a.summaries;
     d.Mp = (int)cdiv(a.summaries, 32) * 32;
     P3D_REQUIRE((int64_t)a.batch * a.kv_heads * d.Mp < ((int64_t)1 << 31), "batch * kv_heads * summaries too large");

@@ -288,3 +288,58 @@ def test_fusion_declines_shapes_it_does_not_take(gpu, monkeypatch):
     layer = _layer(192, 4, 4, 48, dtype, gpu)
     x = torch.randn(1, math.prod(shape), 192, device=gpu, dtype=dtype)
     assert attention.pooled_core(layer, x, layout) is None  # parameters require grad, autograd on
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape,block,pool,kind", [
+    ((4, 6, 10), (1, 1, 2), 5, "raster_block"),             # 2 slots: 32 fine blocks per 64-lane step
+    ((6, 8, 10), (2, 2, 2), 3, "native_block_morton"),      # 8 slots, pools of 3 blocks
+    ((5, 16, 16), (1, 4, 4), 16, "raster_block"),           # 16 slots, pool 16 (the allen15 preset's)
+    ((4, 8, 12), (2, 4, 4), 5, "raster_block"),             # 32 slots, 2 blocks per step, a partial last summary
+    ((8, 8, 8), (4, 4, 4), 32, "raster_block"),             # 64 slots: one block per step
+    ((6, 9, 9), (3, 3, 3), 4, "raster_block"),              # 27 slots (not a power of two): one block per step
+    ((4, 4, 8), (1, 1, 1), 32, "native_block_morton"),      # 1 slot: 32 blocks in one step
+])
+def test_pool_fwd_packed_steps_match_fp64_oracle(gpu, dtype, shape, block, pool, kind):
+    """p3d_pool_fwd packs 64 / V fine blocks into each 64-lane step when the
+    slot count V is a power of two up to 32 (a per-block slot softmax, the
+    weighted sums over all 64 lanes).  Its summaries against the oracle's
+    pooling in fp64 on the same rotated, rounded keys: within one unit in the
+    last place of the storage type, as in the tests above; the key-norm slots
+    against the norms of the stored keys."""
+    import oracle.pack3d_oracle as ref
+    vol = math.prod(block)
+    print(f"pool packed {shape} block {block} (V={vol}) pool {pool} {kind} {dtype}", flush=True)
+    torch.manual_seed(vol + pool)
+    layer = p3d.PACK3DAttention(64, heads=2, kv_heads=2, head_dim=32, block_volume=vol, temperature=0.7)
+    with torch.no_grad():
+        layer.norm.weight.uniform_(0.5, 1.5)
+        layer.pool_weight.normal_(0.0, 0.5)
+        layer.slot_bias.normal_(0.0, 0.5)
+    layer = layer.to(gpu, dtype)
+    layout = p3d.build_layout(shape, block, radius=1, pool_size=pool, layout=kind, device=gpu)
+    x = (torch.randn(2, math.prod(shape), 64, generator=torch.Generator().manual_seed(5)) * 1.5).to(gpu, dtype)
+    rope = layer._rope(x, layout)
+    with torch.no_grad():
+        sep = attention._project_buffers(layer, x)
+        _lib.call("p3d_project", sep[0], _lib.stream_of(gpu))
+        plan = _plan(layer, sep, layout, rope)
+        plan.pool()
+    torch.cuda.synchronize()
+    m = layout.geometry.num_summaries
+    ks, vs = _summaries(plan, m)
+    plan.geometry_cpu = layout.geometry.to("cpu")
+    k64, v64 = _oracle_summaries(layer, sep, plan, rope, m)
+    for what, got, r in (("keys", ks, k64), ("values", vs, v64)):
+        u = _ulps(got.cpu(), r, dtype)
+        print(f"  {what}: max ulps vs fp64 oracle {float(u.max()):.3g}", flush=True)
+        assert torch.isfinite(got).all() and float(u.max()) <= 1.0, what
+    # Key-norm slots: slot s of (batch, kv head) holds the largest norm of
+    # the stored keys of summaries m = s mod 64 (times 1 + 1e-6).
+    norms = ks.cpu().double().norm(dim=-1)
+    b, g = norms.shape[:2]
+    exp = torch.zeros(b, g, 64, dtype=torch.float64)
+    for mm in range(m):
+        exp[:, :, mm % 64] = torch.maximum(exp[:, :, mm % 64], norms[:, :, mm])
+    got = plan.sk_norm_max.cpu().double().view(b, g, 64)
+    assert torch.allclose(got, exp * (1 + 1e-6), rtol=1e-5, atol=0), float((got - exp).abs().max())

@@ -726,6 +726,13 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
     const unsigned total = (unsigned)a.B * a.G * a.Mp;
     const unsigned stride = gridDim.x * waves;
     const int64_t slice = (int64_t)total * D;  // one split of the partials
+    // Fine blocks packed into a 64-lane step as in the forward: lane l holds
+    // slot l % V of block l / V of the step (bps = 64 / V blocks), or slot l.
+    const int lane_block = lane / (a.bps == 1 ? 64 : a.V), lane_slot = lane - lane_block * a.V;
+    auto slot_token = [&](int fs, int f_end) __attribute__((always_inline)) -> int {
+        const int f = fs + lane_block;
+        return (lane < a.bps * a.V && f < f_end) ? a.blocks[(int64_t)f * a.V + lane_slot] : -1;
+    };
     for (unsigned item = blockIdx.x * waves + wave; item < total; item += stride) {
         const int g = (int)(item % a.G);
         const unsigned bm = item / a.G;
@@ -733,9 +740,9 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
         const int64_t bg = (int64_t)b * a.G + g;
         const int f0 = m * a.P, f_end = m < a.M ? min(a.F, (m + 1) * a.P) : 0;
         int count = 0;
-        for (int f = f0; f < f_end; ++f) {
-            const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
-            count += __ballot(idx >= 0) != 0;
+        for (int fs = f0; fs < f_end; fs += a.bps) {
+            const uint64_t filled = __ballot(slot_token(fs, f_end) >= 0);
+            if (filled) count += blocks_filled(filled, a.bps, a.V);
         }
         float dwacc[C::SJ][CPD];
 #pragma unroll
@@ -778,8 +785,8 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
         const T* Vv = reinterpret_cast<const T*>(a.vg) + b * a.vsb + g * a.vsh;
         T* DK = reinterpret_cast<T*>(bd.dkg.data) + b * bd.dkg.sb + g * bd.dkg.sh;
         T* DV = reinterpret_cast<T*>(bd.dvg.data) + b * bd.dvg.sb + g * bd.dvg.sh;
-        for (int f = f0; f < f_end; ++f) {
-            const int idx = lane < a.V ? a.blocks[(int64_t)f * a.V + lane] : -1;
+        for (int fs = f0; fs < f_end; fs += a.bps) {
+            const int idx = slot_token(fs, f_end);
             if (__ballot(idx >= 0) == 0) continue;
             int pos[3];
             rope_position32(a.rope, max(idx, 0), pos);
@@ -823,12 +830,14 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
                     }
                     *reinterpret_cast<uint4*>(krows + lane * C::RD + p * 4) = raw;
                 }
-                logit = dot * a.inv_tau + lbias[lane];
+                logit = dot * a.inv_tau + lbias[lane & (a.gsz - 1)];
             }
-            const float mx = wave_max(logit);
+            // Softmax and sum_s a_s da_s over each block's lanes.
+            const float mx = group_max(logit, a.gsz);
             const float ex = idx >= 0 ? expf(logit - mx) : 0.f;
-            const float w = ex / wave_sum(ex);
-            const float sa = wave_sum(w * da);
+            const float den = group_sum(ex, a.gsz);
+            const float w = den > 0.f ? ex / den : 0.f;
+            const float sa = group_sum(w * da, a.gsz);
             const float dl = w * (da - sa);
             dbacc += dl;
             lw[lane] = dl * a.inv_tau;
@@ -869,6 +878,8 @@ __global__ __launch_bounds__(256) void k_pool_bwd(PoolDev a, PoolBwdDev bd) {
 #pragma unroll
                 for (int c = 0; c < CPD; ++c) dwp[u * CPD + c] = dwacc[j][c];
         }
+        // Slot s's bias gradient sums the lanes holding slot s of any block.
+        for (int o = a.gsz; o < 64; o <<= 1) dbacc += __shfl_xor(dbacc, o);
         if (lane < a.V) bd.db_part[(int64_t)item * a.V + lane] = dbacc;
     }
 }

@@ -319,3 +319,30 @@ def test_full_size_c4_layer_gradients(gpu):
     chunk by chunk over query rows."""
     print("full size c4 layer backward", flush=True)
     _autocast_layer_vs_oracle(gpu, (32, 128, 64), "c4 layer", chunk=2048)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape,block,pool,kind", [
+    ((4, 6, 10), (1, 1, 2), 5, "raster_block"),          # 2 slots: 32 fine blocks per pooling step
+    ((6, 8, 10), (2, 2, 2), 3, "native_block_morton"),   # 8 slots
+    ((5, 16, 16), (1, 4, 4), 16, "raster_block"),        # 16 slots, pool 16 (the allen15 preset's)
+    ((4, 8, 12), (2, 4, 4), 5, "raster_block"),          # 32 slots, a partial last summary
+    ((6, 9, 9), (3, 3, 3), 4, "raster_block"),           # 27 slots: one block per step
+])
+def test_every_gradient_pooled_grids(gpu, dtype, shape, block, pool, kind):
+    """Summaries of several fine blocks (pool_size > 1), with the pooling
+    forward and backward packing 64 / V blocks into a 64-lane step when V is
+    a power of two: every gradient against the oracle's autograd."""
+    print(f"backward pooled {shape} {block} pool {pool} {kind} {dtype}", flush=True)
+    lay_h = p3d.build_layout(shape, block, radius=1, pool_size=pool, layout=kind)
+    lay_r = ref.build_layout(shape, block, radius=1, pool_size=pool, layout=kind)
+    n, vol = math.prod(shape), math.prod(block)
+    inputs = random_core_inputs(2, 4, 2, n, 32, vol, dtype, seed=n + vol + pool)
+    xs = [t.to(gpu).requires_grad_() for t in inputs]
+    rs = [t.detach().clone().requires_grad_() for t in inputs]
+    y = p3d.pack3d_hip(*xs, lay_h.geometry, temperature=0.8)
+    e = ref.pack3d_reference(*rs, lay_r.geometry, temperature=0.8)
+    up = torch.randn(e.shape, generator=torch.Generator().manual_seed(19)).to(dtype)
+    got = torch.autograd.grad(y, xs, up.to(gpu))
+    exp = torch.autograd.grad(e, rs, up)
+    _compare(got, exp, dtype, f"pooled {shape}")

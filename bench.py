@@ -427,7 +427,7 @@ VISION_ROWS = (
 )
 
 
-def bench_vision_table(warmups=7, repeats=31):
+def bench_vision_table(warmups=7, repeats=31, only=None):
     """The rows of VISION_ROWS under the protocol of benchmarks/vision.py:
     seed 205 (repack seed 17); dim 512, 8 / 2 heads, head_dim 64, (1, 4, 4)
     blocks, pool 16 (the small row: dim 64, 4 / 2 heads, head_dim 16, (2, 2, 2)
@@ -436,7 +436,8 @@ def bench_vision_table(warmups=7, repeats=31):
     row); inference under inference_mode; forward + backward as
     forward(x).backward(dy) with a preallocated dy, the gradients cleared
     outside the timed region; synchronised wall time per step, the median of
-    `repeats` steps after `warmups`."""
+    `repeats` steps after `warmups`.  `only`: indices into VISION_ROWS to
+    time (all when None)."""
     import statistics
     from contextlib import nullcontext
 
@@ -444,7 +445,9 @@ def bench_vision_table(warmups=7, repeats=31):
 
     dev = torch.device("cuda:0")
     rows = []
-    for name, grid, order, repack, prec, batch, small, ref_inf, ref_fb in VISION_ROWS:
+    for index, (name, grid, order, repack, prec, batch, small, ref_inf, ref_fb) in enumerate(VISION_ROWS):
+        if only is not None and index not in only:
+            continue
         torch.manual_seed(205)
         if small:
             dim, heads, groups, head_dim, block, pool = 64, 4, 2, 16, (2, 2, 2), 4
@@ -653,6 +656,9 @@ def main():
                    help="time the c4 layer forward + backward instead (one JSON line of its own)")
     p.add_argument("--probe-rates", action="store_true",
                    help="measure the exp / fma / MFMA issue rates instead (one JSON line of its own)")
+    p.add_argument("--vision", metavar="ROWS",
+                   help="time only these rows of the reference's published latency table (comma-separated "
+                        "indices, 0-7, or 'all'; one JSON line of its own)")
     a = p.parse_args()
     if a.gpus != 1:
         print("bench.py: this build runs on one GPU only; --gpus must be 1", file=sys.stderr)
@@ -671,6 +677,10 @@ def main():
         return
     if a.probe_rates:
         print(json.dumps(probe_rates()), flush=True)
+        return
+    if a.vision:
+        only = None if a.vision == "all" else {int(v) for v in a.vision.split(",")}
+        print(json.dumps({"reference_vision_table": bench_vision_table(only=only)}), flush=True)
         return
 
     import pack3d_amd as p3d

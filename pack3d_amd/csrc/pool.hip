@@ -25,7 +25,7 @@ constexpr int kNormSlots = 64;
 
 struct PoolDev {
     int B, G, N, F, V, P, M, Mp;
-    int bps, gsz;  // forward: fine blocks per 64-lane step, lanes per block's slot group
+    int bps, gsz;  // fine blocks per 64-lane pooling step; lanes of a block's slot group (64 if bps is 1)
     float inv_tau, key_scale;
     const char *kg, *vg;
     int64_t ksb, ksh, ksn, vsb, vsh, vsn;

@@ -338,15 +338,16 @@ def test_copy_rows_into_projection_layout(gpu, dtype):
     assert torch.equal(others, torch.full_like(others, 7.0))
 
 
+@pytest.mark.parametrize("amp_dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("grad", [True, False])
-def test_layer_autocast_keeps_the_wide_residual(gpu, grad):
+def test_layer_autocast_keeps_the_wide_residual(gpu, grad, amp_dtype):
     """Under autocast with an fp32 input the reference returns
     ``residual + to_out(...)`` in fp32 with the residual unrounded
     (attention.py:89).  Inputs of scale 4 make a bf16-rounded residual miss
     the bound by a factor of ~3 while the bf16 attention branch stays inside."""
     import oracle.pack3d_oracle as ref
     from tests._cases import max_abs
-    print(f"layer autocast residual grad={grad}", flush=True)
+    print(f"layer autocast residual grad={grad} {amp_dtype}", flush=True)
     torch.manual_seed(0)
     shape = (8, 16, 12)
     n = math.prod(shape)
@@ -367,7 +368,7 @@ def test_layer_autocast_keeps_the_wide_residual(gpu, grad):
 
     linear._lib.call = counting
     try:
-        with torch.set_grad_enabled(grad), torch.autocast("cuda", dtype=torch.bfloat16):
+        with torch.set_grad_enabled(grad), torch.autocast("cuda", dtype=amp_dtype):
             y = layer(xg, lay_h)
     finally:
         linear._lib.call = real

@@ -346,3 +346,38 @@ def test_every_gradient_pooled_grids(gpu, dtype, shape, block, pool, kind):
     got = torch.autograd.grad(y, xs, up.to(gpu))
     exp = torch.autograd.grad(e, rs, up)
     _compare(got, exp, dtype, f"pooled {shape}")
+
+
+def test_full_size_allen15_layer_gradients_match_oracle(gpu):
+    """Forward + backward of the reference benchmark's allen15 preset at the
+    size of its published table's first row (dim 512, 8 / 2 heads, head_dim
+    64, (1, 4, 4) blocks, pool 16, radius 1, 32 x 128 x 64 = 262,144 tokens,
+    bf16 storage): the output, the input gradient and every parameter
+    gradient against the oracle layer's autograd on the same (rounded)
+    weights and input, relative L2 within the reference's bf16 bar."""
+    import oracle.pack3d_oracle as ref_mod
+    print("full size allen15 layer gradients vs oracle", flush=True)
+    shape, block = (32, 128, 64), (1, 4, 4)
+    n = math.prod(shape)
+    torch.manual_seed(205)
+    layer = p3d.PACK3DAttention(512, heads=8, kv_heads=2, head_dim=64, block_volume=16).to(gpu, torch.bfloat16)
+    oracle = ref_mod.PACK3DAttention(512, heads=8, kv_heads=2, head_dim=64, block_volume=16)
+    oracle.load_state_dict({k: v.detach().float().cpu() for k, v in layer.state_dict().items()})
+    lay = p3d.build_layout(shape, block, radius=1, pool_size=16, layout="raster_block", device=gpu)
+    lay_r = ref_mod.build_layout(shape, block, radius=1, pool_size=16, layout="raster_block")
+    x = torch.randn(1, n, 512, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    dy = torch.randn(1, n, 512, generator=torch.Generator().manual_seed(13))
+    xh = x.to(gpu).requires_grad_()
+    xr = x.float().requires_grad_()
+    yh = layer(xh, lay)
+    yh.backward(dy.to(gpu, torch.bfloat16))
+    yr = oracle(xr, lay_r, chunk=512)
+    yr.backward(dy)
+    checks = [("output", yh, yr), ("input", xh.grad, xr.grad)]
+    expected = dict(oracle.named_parameters())
+    checks += [(name, prm.grad, expected[name].grad) for name, prm in layer.named_parameters()]
+    for name, got, exp in checks:
+        assert got is not None and torch.isfinite(got.float()).all(), name
+        err = rel_l2(got.float().cpu(), exp)
+        print(f"  {name}: rel_l2={err:.3g}", flush=True)
+        assert err < TOL[torch.bfloat16], (name, err)

@@ -256,7 +256,7 @@ def test_core_loose_bound_takes_exact_path(gpu, grid):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("dim", [192, 64, 384, 512])
+@pytest.mark.parametrize("dim", [192, 64, 272, 384, 512])
 def test_layer_norm_kernel_matches_torch(gpu, dtype, dim):
     """The layer's LayerNorm kernel against torch's (attention.py:64), parameters
     in the storage type and in fp32."""

@@ -250,7 +250,8 @@ def test_project_linear_declines_unsupported_shapes():
 
 @pytest.mark.parametrize("x_dtype,y_dtype", [(torch.float32, torch.bfloat16), (torch.float32, torch.float16),
                                               (torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32)])
-@pytest.mark.parametrize("rows,dim", [(1, 192), (1003, 192), (517, 64), (300, 512), (777, 384), (4099, 512)])
+@pytest.mark.parametrize("rows,dim", [(1, 192), (1003, 192), (517, 64), (300, 512), (777, 384), (4099, 512),
+                                      (97, 272)])
 @pytest.mark.parametrize("residual", [False, True, "pass"])
 def test_layer_norm_train_forward_backward_match_torch(gpu, x_dtype, y_dtype, rows, dim, residual):
     """LayerNormTrain against torch.layer_norm in fp64 on the same inputs: the
